@@ -1,0 +1,170 @@
+"""Benchmark of the MI355X grouped GEMM on BASELINE.json's headline config.
+
+One "step" = one grouped GEMM launch (Backend::run) over the whole synthetic batch of the
+MoE gate+up projection config: B=8 groups x M=4096 tokens, N=4096, K=7168, bf16, balanced
+groups, x and w ~ N(0,1) from the seeded generator (x seed 1, w seed 2), inputs resident in
+HBM before timing (the reference's protocol, bench/bench_main.cpp:436-501).
+
+Prints ONE JSON line on stdout. Besides the driver's fields it carries:
+  roofline     the kernel against the dense bf16 MFMA peak (2.5 PFLOP/s): achieved = FLOPs
+               per launch / mean launch duration from HIP events on the launch stream;
+               traffic = HBM bytes per launch from the committed rocprofv3 PMC summary
+               (profiles/hbm_traffic_<workload>.json) when present, else null.
+  cpu_baseline the CPU oracle (OpenMP fp32, test infrastructure) timed on a bounded sample
+               of the same workload on this host; a reported baseline only.
+Human-readable progress goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import __graft_entry__ as entry  # noqa: E402
+
+WORKLOADS = {
+    # name: (dtype, B, M per group, N, K)
+    "moe_gate_up_b8_m4096_n4096_k7168_bf16": (0, 8, 4096, 4096, 7168),
+    "moe_down_b8_m4096_n7168_k2048_bf16": (0, 8, 4096, 7168, 2048),
+    "dense_expert_b8_m4096_n14336_k4096_fp16": (1, 8, 4096, 14336, 4096),
+    "dense_expert_b8_m4096_n14336_k4096_bf16": (0, 8, 4096, 14336, 4096),
+    "tails_b32_m520_n2880_k2880_bf16": (0, 32, 520, 2880, 2880),
+    "low_occupancy_b1_m2048_n7168_k2048_bf16": (0, 1, 2048, 7168, 2048),
+    "plumbing_b4_m256_n512_k1024_bf16": (0, 4, 256, 512, 1024),
+}
+HEADLINE = "moe_gate_up_b8_m4096_n4096_k7168_bf16"
+MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16/fp16
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(oracle, x, w, dtype, n, k, target_s):
+    """Time the CPU oracle on rows 0..R-1 of group 0 (all N columns, full K), R sized so the
+    timed pass takes about target_s seconds."""
+    import numpy as np
+    import torch
+
+    def bits(t):
+        return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+    w0 = bits(w[0])
+    probe_rows = 16
+    t0 = time.perf_counter()
+    oracle.group_rows(dtype, bits(x[:probe_rows]), w0)
+    probe = time.perf_counter() - t0
+    rows = int(max(probe_rows, min(x.shape[0], probe_rows * target_s / max(probe, 1e-6))))
+    rows = max(4, rows // 4 * 4)
+    xs = bits(x[:rows])
+    t0 = time.perf_counter()
+    oracle.group_rows(dtype, xs, w0)
+    dt = time.perf_counter() - t0
+    flops = 2.0 * rows * n * k
+    return {
+        "value": round(flops / dt / 1e12, 6),
+        "unit": "TFLOPS",
+        "cores": oracle.threads(),
+        "kind": "port",
+        "sample": f"rows 0..{rows - 1} of group 0 x all {n} columns x K={k} "
+                  f"({flops / 1e9:.1f} GFLOP, {dt:.1f} s), fp32 OpenMP oracle",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default=HEADLINE, choices=sorted(WORKLOADS))
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one MI355X only (asked for --gpus {args.gpus}); "
+              "groups shard across GPUs without any exchange, see DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    pkg = entry.load_package()
+    dtype, b, m, n, k = WORKLOADS[args.workload]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    td = torch.bfloat16 if dtype == 0 else torch.float16
+    group_m = [m] * b
+    x = torch.empty((b * m, k), dtype=td, device=dev)
+    w = torch.empty((b, n, k), dtype=td, device=dev)
+    out = torch.zeros((b * m, n), dtype=td, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    sh = stream.cuda_stream
+    pkg.fill_randn(pkg.DType(dtype), x.data_ptr(), x.numel(), 1, sh)
+    pkg.fill_randn(pkg.DType(dtype), w.data_ptr(), w.numel(), 2, sh)
+    prob = pkg.GroupedGemmProblem(pkg.DType(dtype), b, n, k, group_m, x.data_ptr(), w.data_ptr(),
+                                  out.data_ptr())
+    be = pkg.make_mi355x_backend()
+    why = be.prepare(prob, sh)
+    if why:
+        raise SystemExit(f"mi355x backend cannot run {args.workload}: {why}")
+    log(f"[bench] {args.workload}: {be.detail()}")
+
+    for _ in range(args.warmup):
+        be.run(sh)
+    torch.cuda.synchronize(dev)
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(args.steps):
+        be.run(sh)
+    stop.record(stream)
+    torch.cuda.synchronize(dev)
+    ms = start.elapsed_time(stop) / args.steps
+    flops = prob.flops()
+    tflops = flops / (ms * 1e-3) / 1e12
+    log(f"[bench] {args.steps} steps, {ms:.4f} ms/step, {tflops:.1f} TFLOPS")
+
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", f"hbm_traffic_{args.workload}.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log(f"[bench] cpu baseline (~{args.cpu_seconds:.0f} s of CPU work)...")
+        cpu = cpu_baseline(entry.load_oracle(), x, w, dtype, n, k, args.cpu_seconds)
+        log(f"[bench] cpu baseline: {cpu['value']} TFLOPS on {cpu['cores']} threads")
+    be.release()
+
+    line = {
+        "metric": "grouped-GEMM TFLOPS (bf16) + % of MFMA peak, 1 MI355X, per config",
+        "value": round(tflops, 2),
+        "unit": "TFLOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if dtype == 0 else "fp16",
+        "data": "synthetic (seeded N(0,1), balanced groups)",
+        "config": {"workload": args.workload, "groups": b, "m_per_group": m, "n": n, "k": k,
+                   "layout": "RCR", "parallelism": "single GPU"},
+        "pct_of_mfma_peak": round(100.0 * tflops / MFMA_PEAK_TFLOPS, 2),
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
+                     "traffic": traffic},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,229 @@
+// extern "C" boundary of the grouped GEMM (declared in include/gg_grouped_gemm.h).
+//
+// Host side of the reference's ck_tile backend, redone for the hand-written gfx950 kernel:
+// CkTileBackend::prepare_typed / finish / run / release (ck_kernel/ck_grouped_gemm.cpp:126-226).
+// prepare validates the problem, builds the device group table (row offset, rows, first
+// tile per group) and the launch shape; run enqueues one launch and never synchronizes.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstdio>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "gg_grouped_gemm.h"
+#include "gg_kernel.h"
+
+struct gg_plan {
+    int                 dtype       = GG_DTYPE_BF16;
+    int                 group_num   = 0;
+    int64_t             n           = 0;
+    int64_t             k           = 0;
+    int64_t             total_m     = 0;
+    int                 total_tiles = 0;
+    int                 grid        = 0;
+    const void         *x           = nullptr;
+    const void         *w           = nullptr;
+    void               *out         = nullptr;
+    gg::GroupEntry     *d_groups    = nullptr;
+    gg::KernelArgs      args{};
+    std::string         detail;
+};
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int status, const std::string &msg) {
+    g_last_error = msg;
+    return status;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+    return fail(GG_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// XCDs of the device: MI355X (gfx950) has 8, each with its own L2. Workgroups are
+// dispatched round-robin over them.
+int xcd_count(const hipDeviceProp_t &prop) {
+    const std::string arch = prop.gcnArchName;
+    if (arch.rfind("gfx950", 0) == 0 || arch.rfind("gfx942", 0) == 0)
+        return 8;
+    return 1;
+}
+
+} // namespace
+
+extern "C" {
+
+int gg_prepare(int dtype, int group_num, int64_t n, int64_t k, const int64_t *group_m,
+               const void *x, const void *w, void *out, void *stream, gg_plan **plan_out) {
+    g_last_error.clear();
+    if (plan_out == nullptr)
+        return fail(GG_ERR_INVALID, "plan_out is null");
+    *plan_out = nullptr;
+    if (dtype != GG_DTYPE_BF16 && dtype != GG_DTYPE_FP16)
+        return fail(GG_ERR_INVALID, "dtype must be GG_DTYPE_BF16 or GG_DTYPE_FP16");
+    if (group_num < 0 || n < 0 || k < 0)
+        return fail(GG_ERR_INVALID, "group_num, n and k must be >= 0");
+    if (group_num > 0 && group_m == nullptr)
+        return fail(GG_ERR_INVALID, "group_m is null");
+
+    int64_t total_m = 0;
+    for (int g = 0; g < group_num; ++g) {
+        if (group_m[g] < 0)
+            return fail(GG_ERR_INVALID, "group_m[" + std::to_string(g) + "] < 0");
+        total_m += group_m[g];
+    }
+    const bool has_output = total_m > 0 && n > 0;
+    if (has_output && (out == nullptr || (k > 0 && (x == nullptr || w == nullptr))))
+        return fail(GG_ERR_INVALID, "x, w and out must be device pointers");
+
+    // Shapes the kernel cannot take: reported like a non-empty Backend::prepare result.
+    if (n % 8 != 0)
+        return fail(GG_ERR_UNSUPPORTED, "N must be a multiple of 8 (16-byte output rows)");
+    if (k % 8 != 0)
+        return fail(GG_ERR_UNSUPPORTED, "K must be a multiple of 8 (16-byte input rows)");
+    if (has_output && (!aligned16(out) || (k > 0 && (!aligned16(x) || !aligned16(w)))))
+        return fail(GG_ERR_UNSUPPORTED, "x, w and out must be 16-byte aligned");
+    // 32-bit per-tile byte offsets: a 256-row slice of x, w or out must stay below 2 GiB.
+    if (k > (int64_t(1) << 21) || n > (int64_t(1) << 21))
+        return fail(GG_ERR_UNSUPPORTED, "N and K must be at most 2097152");
+
+    auto *plan = new (std::nothrow) gg_plan;
+    if (plan == nullptr)
+        return fail(GG_ERR_INVALID, "out of host memory");
+    plan->dtype     = dtype;
+    plan->group_num = group_num;
+    plan->n         = n;
+    plan->k         = k;
+    plan->total_m   = total_m;
+    plan->x         = x;
+    plan->w         = w;
+    plan->out       = out;
+
+    // Group table: row offset, rows and first tile of every group (empty groups own no
+    // tiles; the kernel skips them while scanning forward).
+    const int64_t n_tiles = gg::cdiv(n, gg::kTileN);
+    std::vector<gg::GroupEntry> table(static_cast<size_t>(group_num));
+    int64_t row = 0, tiles = 0;
+    for (int g = 0; g < group_num; ++g) {
+        table[g].row0  = row;
+        table[g].m     = static_cast<int32_t>(group_m[g]);
+        table[g].tile0 = static_cast<int32_t>(tiles);
+        tiles += gg::cdiv(group_m[g], gg::kTileM) * n_tiles;
+        row += group_m[g];
+        if (group_m[g] > INT32_MAX || tiles > INT32_MAX) {
+            delete plan;
+            return fail(GG_ERR_UNSUPPORTED, "too many rows or tiles for 32-bit tile indices");
+        }
+    }
+    plan->total_tiles = has_output && k > 0 ? static_cast<int>(tiles) : 0;
+
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (plan->total_tiles > 0) {
+        int dev = 0;
+        hipError_t e = hipGetDevice(&dev);
+        hipDeviceProp_t prop;
+        if (e == hipSuccess)
+            e = hipGetDeviceProperties(&prop, dev);
+        if (e != hipSuccess) {
+            delete plan;
+            return hip_fail(e, "hipGetDeviceProperties");
+        }
+        const size_t bytes = table.size() * sizeof(gg::GroupEntry);
+        e = hipMalloc(&plan->d_groups, bytes);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(plan->d_groups, table.data(), bytes, hipMemcpyHostToDevice, s);
+        if (e == hipSuccess)
+            e = hipStreamSynchronize(s);
+        if (e != hipSuccess) {
+            if (plan->d_groups != nullptr)
+                (void)hipFree(plan->d_groups);
+            delete plan;
+            return hip_fail(e, "group table upload");
+        }
+        // Persistent grid: one workgroup per CU (160 KB of LDS each), never more than tiles.
+        plan->grid = std::min(prop.multiProcessorCount, plan->total_tiles);
+        const int n_xcd = xcd_count(prop);
+
+        gg::KernelArgs &a = plan->args;
+        a.x           = x;
+        a.w           = w;
+        a.out         = out;
+        a.groups      = plan->d_groups;
+        a.group_num   = group_num;
+        a.total_tiles = plan->total_tiles;
+        a.n           = static_cast<int>(n);
+        a.k           = static_cast<int>(k);
+        a.n_tiles     = static_cast<int>(n_tiles);
+        a.k_tiles     = static_cast<int>(gg::cdiv(k, gg::kTileK));
+        a.n_xcd       = plan->grid % n_xcd == 0 ? n_xcd : 1;
+        a.band        = gg::kBand;
+        plan->detail  = "mi355x persistent 256x256x64 " +
+                       std::string(dtype == GG_DTYPE_BF16 ? "bf16" : "fp16") +
+                       " grid=" + std::to_string(plan->grid) +
+                       " tiles=" + std::to_string(plan->total_tiles) +
+                       " xcd=" + std::to_string(a.n_xcd);
+    } else {
+        plan->detail = "mi355x: no launch (" +
+                       std::string(has_output ? "K = 0, zero fill" : "empty output") + ")";
+    }
+    *plan_out = plan;
+    return GG_OK;
+}
+
+int gg_run(const gg_plan *plan, void *stream) {
+    if (plan == nullptr)
+        return fail(GG_ERR_INVALID, "plan is null");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (plan->total_tiles == 0) {
+        // K == 0 with a non-empty output: out = 0.
+        if (plan->total_m > 0 && plan->n > 0 && plan->k == 0) {
+            const hipError_t e = hipMemsetAsync(plan->out, 0, size_t(plan->total_m) * plan->n * 2, s);
+            if (e != hipSuccess)
+                return hip_fail(e, "hipMemsetAsync");
+        }
+        return GG_OK;
+    }
+    const hipError_t e =
+        gg::launch_grouped_gemm(plan->args, plan->dtype == GG_DTYPE_FP16, plan->grid, s);
+    if (e != hipSuccess)
+        return hip_fail(e, "grouped GEMM launch");
+    return GG_OK;
+}
+
+void gg_release(gg_plan *plan) {
+    if (plan == nullptr)
+        return;
+    if (plan->d_groups != nullptr)
+        (void)hipFree(plan->d_groups);
+    delete plan;
+}
+
+const char *gg_plan_detail(const gg_plan *plan) { return plan ? plan->detail.c_str() : ""; }
+
+int gg_plan_grid(const gg_plan *plan) { return plan ? plan->grid : 0; }
+
+int gg_plan_tiles(const gg_plan *plan) { return plan ? plan->total_tiles : 0; }
+
+const char *gg_last_error(void) { return g_last_error.c_str(); }
+
+int gg_fill_randn(int dtype, void *p, size_t count, uint64_t seed, void *stream) {
+    g_last_error.clear();
+    if (dtype != GG_DTYPE_BF16 && dtype != GG_DTYPE_FP16)
+        return fail(GG_ERR_INVALID, "dtype must be GG_DTYPE_BF16 or GG_DTYPE_FP16");
+    if (count > 0 && p == nullptr)
+        return fail(GG_ERR_INVALID, "p is null");
+    const hipError_t e = gg::launch_fill_randn(p, count, seed, dtype == GG_DTYPE_FP16,
+                                               static_cast<hipStream_t>(stream));
+    if (e != hipSuccess)
+        return hip_fail(e, "fill launch");
+    return GG_OK;
+}
+
+} // extern "C"

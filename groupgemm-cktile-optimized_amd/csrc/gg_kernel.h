@@ -1,0 +1,36 @@
+// Launch interface between the C ABI layer (gg_capi.hip) and the gfx950 kernel
+// (gg_kernel.hip). Host-only declarations; no device code here.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "gg_schedule.h"
+
+namespace gg {
+
+// Kernel arguments, passed by value in the kernarg segment. Everything a workgroup needs
+// to find its tiles: the device group table plus the problem-wide sizes.
+struct KernelArgs {
+    const void       *x;      // [sum(M), K] row-major
+    const void       *w;      // [B, N, K] row-major
+    void             *out;    // [sum(M), N] row-major
+    const GroupEntry *groups; // [group_num], device memory
+    int               group_num;
+    int               total_tiles; // output tiles over all groups
+    int               n;           // N
+    int               k;           // K (multiple of 8)
+    int               n_tiles;     // ceil(N / kTileN)
+    int               k_tiles;     // ceil(K / kTileK)
+    int               n_xcd;       // XCDs the grid is spread over (1 = no remap)
+    int               band;        // M-tiles per band of the in-group tile order
+};
+
+// Enqueue the persistent grouped GEMM: `grid` workgroups of 256 threads on `stream`.
+// fp16 selects the f16 MFMA, otherwise bf16. Returns the launch status.
+hipError_t launch_grouped_gemm(const KernelArgs &args, bool fp16, int grid, hipStream_t stream);
+
+// Seeded N(0,1) fill (benchmark input generator).
+hipError_t launch_fill_randn(void *p, size_t count, uint64_t seed, bool fp16, hipStream_t stream);
+
+} // namespace gg

@@ -1,0 +1,466 @@
+// Persistent grouped GEMM for MI355X (gfx950, CDNA4): out[g] = x[g] @ w[g]^T, bf16/fp16 in,
+// fp32 accumulate, bf16/fp16 out (RNE).
+//
+// Replaces the reference's hot path: CK's persistent GroupedGemmKernel tile loop, the
+// hand-scheduled HandPipelineAsmS main loop and FastEpilogue
+// (ck_kernel/ck_grouped_gemm.cpp:97, hand_pipeline_asm_s.hpp:155-357, fast_epilogue.hpp:29-118).
+// Written directly against gfx950: no CK headers, no portability layers.
+//
+// Work decomposition
+//   * Output tile 256 x 256, K step 64. One workgroup = 4 waves, one per SIMD; wave (wm, wn)
+//     owns the 128 x 128 sub-tile rows wm*128.., cols wn*128.. as 8 x 8 MFMA tiles of 16 x 16.
+//   * v_mfma_f32_16x16x32_{bf16,f16}. The w fragment is the first source and the x fragment
+//     the second, so each 16 x 16 accumulator holds C^T: lane l has row l%16 of the block and
+//     the four consecutive columns 4*(l/16)..+3, i.e. 8 contiguous output bytes.
+//   * All 256 accumulators per lane live in AGPRs (inline-asm MFMAs with "a" operands);
+//     fragments, offsets and addresses use the 256 arch VGPRs.
+//   * grid = min(#CUs, #tiles) persistent workgroups walking the tile list of all groups
+//     (gg_schedule.h: banded in-group order + XCD remap).
+//
+// LDS (160 KB, all of it): A (x rows) 2 stages + B (w rows) 3 stages of 256 rows x 128 B.
+// Row r keeps its 16-byte chunk c at chunk position c ^ (r % 8): the eight lanes that a
+// ds_read_b128 serves together (8 consecutive rows, same chunk) hit eight different 16-byte
+// slots of a 128-byte window, which is conflict-free on gfx950.
+// Global -> LDS copies use buffer_load_dwordx4 ... lds (no VGPR staging): one instruction
+// moves 64 lanes x 16 B = 8 rows; lane l fetches logical chunk (l%8) ^ (l/8) of row l/8 so
+// that the fixed lane -> LDS mapping (M0 + 16 l) realises the swizzle.
+//
+// K-step schedule (one "iteration" kt, 8 rows of 16 MFMAs per wave, see the plan_* table):
+//   * x fragments are read one row ahead (2-row register ring); w fragments of step kt+1
+//     are pre-read during step kt into the second half of a double-buffered register set.
+//   * DMA: A(kt+1) in rows 0-2 (its first two loads were issued at the end of step kt-1),
+//     B(kt+3) in rows 3-6, the first two loads of A(kt+2) at the end of row 7.
+//   * One barrier per step, in row 7: after it A(kt+1) is complete in LDS, every wave is done
+//     with A(kt) and with B(kt+1)'s LDS copy, so their stages can be refilled.
+//   * Buffer resources are bounded by the tile's valid rows: rows past M or N read zeros and
+//     are never stored. Prefetches past the last K step use a zero-length resource (no
+//     traffic, the DMA writes zeros) so the DMA count, and every vmcnt, stays static.
+//     K % 64 != 0: the last K step's out-of-range 16-byte chunks get an out-of-range offset.
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+#include <type_traits>
+
+#include "gg_kernel.h"
+
+#pragma clang diagnostic ignored "-Winline-asm"
+
+namespace gg {
+namespace {
+
+typedef int      i32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+typedef float    f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16   bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kThreads  = 256;
+constexpr int kWaves    = kThreads / 64;
+constexpr int kRowBytes = kTileK * 2;           // 128: one K step of one operand row
+constexpr int kOpBytes  = kTileM * kRowBytes;   // 32 KB: one K step of one operand tile
+static_assert(kTileM == kTileN, "x and w tiles share one load layout");
+constexpr int kAStages  = 2;
+constexpr int kBStages  = 3;
+constexpr int kLdsBytes = (kAStages + kBStages) * kOpBytes; // 163840 = all of gfx950's LDS
+constexpr int kLoads    = kOpBytes / 1024 / kWaves;         // 1 KB DMAs per wave per operand step
+constexpr int kEarlyA   = 2;                                // A(kt+2) DMAs issued in step kt
+constexpr int kCStride  = kTileN * 2 + 16;                  // staged C row stride (528 B)
+static_assert(kLoads == 8 && kEarlyA == 2, "the slot plan below is written for 8 + 2 DMAs");
+static_assert(kTileM * kCStride <= kLdsBytes, "the staged C tile must fit in LDS");
+
+constexpr int a_stage(int s) { return s * kOpBytes; }
+constexpr int b_stage(int s) { return (kAStages + s) * kOpBytes; }
+
+// ---------------------------------------------------------------------------------------
+// Slot plan of one K step. Row mi (0..7) issues 16 MFMAs, idx = kh * 8 + ni; each function
+// says which memory operation follows MFMA idx of row mi (-1: none). LDS reads sit after odd
+// MFMAs, DMAs after even ones, so no MFMA gap holds more than one memory operation.
+// ---------------------------------------------------------------------------------------
+constexpr int kBarRow = 7, kBarIdx = 7; // the step's barrier follows this MFMA
+
+// x fragments of row mi+1 (k-half kh) into the register ring.
+constexpr int plan_read_a_next(int mi, int idx) {
+    return (mi < 7 && (idx == 1 || idx == 3)) ? idx / 2 : -1;
+}
+// w fragments of step kt+1, column block ni = mi, k-half kh (rows 0-6 after MFMAs 5 and 7,
+// row 7 after 1 and 3 so they are complete before the barrier).
+constexpr int plan_read_b_next(int mi, int idx) {
+    if (mi < 7)
+        return idx == 5 ? 0 : idx == 7 ? 1 : -1;
+    return idx == 1 ? 0 : idx == 3 ? 1 : -1;
+}
+// x fragments of row 0 of step kt+1, after the barrier.
+constexpr int plan_read_a_row0(int mi, int idx) {
+    return (mi == 7 && (idx == 9 || idx == 11)) ? (idx - 9) / 2 : -1;
+}
+// DMA j of A(kt+1), j = kEarlyA..7: rows 0-2 after MFMAs 0 and 8.
+constexpr int plan_load_a(int mi, int idx) {
+    return (mi <= 2 && (idx == 0 || idx == 8)) ? kEarlyA + mi * 2 + idx / 8 : -1;
+}
+// DMA j of B(kt+3): rows 3-6 after MFMAs 0 and 8.
+constexpr int plan_load_b(int mi, int idx) {
+    return (mi >= 3 && mi <= 6 && (idx == 0 || idx == 8)) ? (mi - 3) * 2 + idx / 8 : -1;
+}
+// DMA j < kEarlyA of A(kt+2): row 7 after MFMAs 12 and 14 (its stage is free after the barrier).
+constexpr int plan_load_a_early(int mi, int idx) {
+    return (mi == 7 && (idx == 12 || idx == 14)) ? (idx - 12) / 2 : -1;
+}
+// DMAs that may still be in flight at the barrier: those issued after the last A(kt+1) DMA.
+// Loads complete in order, so vmcnt(this) means all of A(kt+1) (and everything older) landed.
+constexpr int vm_at_barrier() {
+    int last_a = -1;
+    for (int p = 0; p < 8 * 16; ++p)
+        if (plan_load_a(p / 16, p % 16) >= 0)
+            last_a = p;
+    int n = 0;
+    for (int p = last_a + 1; p < kBarRow * 16 + kBarIdx; ++p)
+        n += (plan_load_b(p / 16, p % 16) >= 0) + (plan_load_a_early(p / 16, p % 16) >= 0);
+    return n;
+}
+constexpr int count_plan(int (*f)(int, int)) {
+    int n = 0;
+    for (int p = 0; p < 8 * 16; ++p)
+        n += f(p / 16, p % 16) >= 0;
+    return n;
+}
+static_assert(count_plan(plan_load_a) == kLoads - kEarlyA, "A DMAs");
+static_assert(count_plan(plan_load_b) == kLoads, "B DMAs");
+static_assert(count_plan(plan_load_a_early) == kEarlyA, "early A DMAs");
+static_assert(count_plan(plan_read_b_next) == 16, "w fragments of the next step");
+
+// ---------------------------------------------------------------------------------------
+// Device primitives
+// ---------------------------------------------------------------------------------------
+template <int N> using ic = std::integral_constant<int, N>;
+template <int B, int E, typename F> __device__ __forceinline__ void sfor(F &&f) {
+    if constexpr (B < E) {
+        f(ic<B>{});
+        sfor<B + 1, E>(static_cast<F &&>(f));
+    }
+}
+
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// Make a value look freshly produced at this point. Values derived from it are then
+// recomputed next to their uses inside the loop instead of being hoisted out of it as loop
+// invariants (which would keep dozens of precomputed addresses live across the K loop).
+__device__ __forceinline__ void fresh_v(int &v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void fresh_s(uint32_t &v) { asm volatile("" : "+s"(v)); }
+
+// Buffer resource for the LDS DMA (SGPR quad): base, stride 0, byte bound, gfx9 raw format.
+__device__ __forceinline__ i32x4 dma_rsrc(const void *p, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(p);
+    i32x4 r;
+    r[0] = static_cast<int>(static_cast<uint32_t>(a));
+    r[1] = static_cast<int>(static_cast<uint32_t>(a >> 32) & 0xffffu);
+    r[2] = static_cast<int>(bytes);
+    r[3] = 0x00020000;
+    return r;
+}
+
+// 64 lanes x 16 B from global (resource + lane offset + K-step offset) into LDS at
+// lds_dst + 16 * lane. The compiler cannot see this LDS write: waits are placed by hand.
+__device__ __forceinline__ void dma16(uint32_t lds_dst, int voff, const i32x4 &rsrc, int soff) {
+    asm volatile("s_mov_b32 m0, %0\n\t"
+                 "s_nop 0\n\t"
+                 "buffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :
+                 : "s"(lds_dst), "v"(voff), "s"(rsrc), "s"(soff)
+                 : "memory", "m0");
+}
+
+template <int VM> __device__ __forceinline__ void wait_vm_lds_barrier() {
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(VM) : "memory");
+}
+
+template <bool F16>
+__device__ __forceinline__ void mfma(f32x4 &c, const i32x4 &a, const i32x4 &b) {
+    if constexpr (F16)
+        asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+    else
+        asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+}
+// First K half of a tile: C = 0, so the accumulators need no clearing.
+template <bool F16>
+__device__ __forceinline__ void mfma_first(f32x4 &c, const i32x4 &a, const i32x4 &b) {
+    if constexpr (F16)
+        asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, 0" : "=a"(c) : "v"(a), "v"(b));
+    else
+        asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=a"(c) : "v"(a), "v"(b));
+}
+
+// Four fp32 accumulators -> four 16-bit outputs (RNE), as two packed dwords.
+template <bool F16> __device__ __forceinline__ u32x2 pack4(const f32x4 &v) {
+    u32x2 r;
+    if constexpr (F16) {
+        r[0] = __builtin_bit_cast(unsigned, f16x2{(_Float16)v[0], (_Float16)v[1]});
+        r[1] = __builtin_bit_cast(unsigned, f16x2{(_Float16)v[2], (_Float16)v[3]});
+    } else {
+        r[0] = __builtin_bit_cast(unsigned, bf16x2{(__bf16)v[0], (__bf16)v[1]});
+        r[1] = __builtin_bit_cast(unsigned, bf16x2{(__bf16)v[2], (__bf16)v[3]});
+    }
+    return r;
+}
+
+// ---------------------------------------------------------------------------------------
+// The kernel
+// ---------------------------------------------------------------------------------------
+template <bool F16>
+__global__ void __launch_bounds__(kThreads, 1) __attribute__((amdgpu_waves_per_eu(1, 1)))
+grouped_gemm_kernel(const KernelArgs args) {
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[kLdsBytes];
+    typedef __attribute__((address_space(3))) uint8_t lds_u8;
+    const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8 *)smem));
+
+    const int lane = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6) & 3;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int K = args.k, N = args.n, T = args.k_tiles;
+
+    // DMA j of an operand step covers tile rows j*32 + wave*8 .. +8; lane -> row lane/8,
+    // logical chunk (lane%8) ^ (lane/8). x and w rows have the same length K, so one set of
+    // offsets serves both operands and every tile.
+    const int ld_row   = lane >> 3;
+    const int ld_chunk = (lane & 7) ^ ld_row;
+    int voff[kLoads];
+    sfor<0, kLoads>([&](auto j) {
+        voff[j] = ((j * 32 + wave * 8 + ld_row) * K + ld_chunk * 8) * 2;
+    });
+    // Last K step when K % 64 != 0: chunks at k >= K get an offset past every bound.
+    const int k_last    = K - (T - 1) * kTileK; // valid K of the last step, 8..64
+    int       ktail_bad = (ld_chunk * 8 >= k_last) ? static_cast<int>(0x80000000u) : 0;
+
+    // Fragment reads: lane -> row lane%16 of a 16-row block, logical chunk kh*4 + lane/16.
+    const int fr_row = lane & 15, fr_q = lane >> 4;
+    int frag_a[2], frag_b[2];
+    sfor<0, 2>([&](auto kh) {
+        const int off = fr_row * kRowBytes + (((kh * 4 + fr_q) ^ (fr_row & 7)) * 16);
+        frag_a[kh]    = wm * 128 * kRowBytes + off;
+        frag_b[kh]    = wn * 128 * kRowBytes + off;
+    });
+    auto lds_read = [&](int off) -> i32x4 { return *reinterpret_cast<const i32x4 *>(smem + off); };
+
+    f32x4 acc[8][8];
+    i32x4 fa[2][2];    // x fragments: row ring x k-half
+    i32x4 fb[2][8][2]; // w fragments: step parity x column block x k-half
+
+    int g = 0;
+    for (int t = blockIdx.x; t < args.total_tiles; t += gridDim.x) {
+        // ---- which tile ---------------------------------------------------------------
+        const int L = xcd_remap(t, args.total_tiles, gridDim.x, args.n_xcd);
+        while (g + 1 < args.group_num && args.groups[g + 1].tile0 <= L)
+            ++g;
+        const GroupEntry ge      = args.groups[g];
+        const int        m_tiles = (ge.m + kTileM - 1) / kTileM;
+        int              tm, tn;
+        band_coords(L - ge.tile0, m_tiles, args.n_tiles, args.band, &tm, &tn);
+        const int     m_valid = min(kTileM, ge.m - tm * kTileM);
+        const int     n_valid = min(kTileN, N - tn * kTileN);
+        const int64_t row0    = ge.row0 + static_cast<int64_t>(tm) * kTileM;
+        const int64_t col0    = static_cast<int64_t>(tn) * kTileN;
+        const uint16_t *a_ptr = static_cast<const uint16_t *>(args.x) + row0 * K;
+        const uint16_t *b_ptr = static_cast<const uint16_t *>(args.w) +
+                                (static_cast<int64_t>(g) * N + col0) * K;
+        uint16_t *c_ptr = static_cast<uint16_t *>(args.out) + row0 * N + col0;
+
+        const i32x4 rsrc_a = dma_rsrc(a_ptr, static_cast<uint32_t>(m_valid) * K * 2);
+        const i32x4 rsrc_b = dma_rsrc(b_ptr, static_cast<uint32_t>(n_valid) * K * 2);
+        const i32x4 rsrc_0 = dma_rsrc(a_ptr, 0);
+
+        // DMA j of K step kidx into the stage at byte offset `stage`. CHECKED: kidx may be past
+        // the last step (zero-length resource) or be the last, partial step (masked chunks).
+        // Per-wave LDS destination base and per-lane offsets, re-materialised at the top of
+        // every loop body (see fresh_v).
+        uint32_t dma_base = lds0 + wave * 1024;
+        auto refresh = [&]() {
+            fresh_s(dma_base);
+            sfor<0, kLoads>([&](auto j) { fresh_v(voff[j]); });
+            fresh_v(ktail_bad);
+            sfor<0, 2>([&](auto h) { fresh_v(frag_a[h]); fresh_v(frag_b[h]); });
+        };
+        auto dma = [&](const i32x4 &rsrc, int stage, auto j, int kidx, auto checked) {
+            sched_fence();
+            const uint32_t dst = dma_base + stage + j * 4096;
+            if constexpr (decltype(checked)::value) {
+                const i32x4 rs   = kidx < T ? rsrc : rsrc_0;
+                const int   last = kidx == T - 1 ? -1 : 0; // uniform
+                dma16(dst, voff[j] | (ktail_bad & last), rs, kidx * kRowBytes);
+            } else {
+                dma16(dst, voff[j], rsrc, kidx * kRowBytes);
+            }
+            sched_fence();
+        };
+
+        // ---- prologue: A(0), B(0..2), first DMAs of A(1); then B(0) and A(0) row 0 -> regs
+        wait_vm_lds_barrier<63>(); // previous tile's epilogue is done with LDS everywhere
+        refresh();
+        sfor<0, kLoads>([&](auto j) { dma(rsrc_a, a_stage(0), j, 0, std::true_type{}); });
+        sfor<0, kLoads>([&](auto j) { dma(rsrc_b, b_stage(0), j, 0, std::true_type{}); });
+        sfor<0, kLoads>([&](auto j) { dma(rsrc_b, b_stage(1), j, 1, std::true_type{}); });
+        sfor<0, kLoads>([&](auto j) { dma(rsrc_b, b_stage(2), j, 2, std::true_type{}); });
+        sfor<0, kEarlyA>([&](auto j) { dma(rsrc_a, a_stage(1), j, 1, std::true_type{}); });
+        wait_vm_lds_barrier<kLoads + kEarlyA>(); // A(0), B(0), B(1) landed everywhere
+        sfor<0, 8>([&](auto ni) {
+            sfor<0, 2>([&](auto kh) {
+                fb[0][ni][kh] = lds_read(frag_b[kh] + b_stage(0) + ni * 16 * kRowBytes);
+            });
+        });
+        sfor<0, 2>([&](auto kh) { fa[0][kh] = lds_read(frag_a[kh] + a_stage(0)); });
+        wait_vm_lds_barrier<63>(); // every wave holds B(0): its stage may be refilled
+
+        // ---- one K step -----------------------------------------------------------------
+        // SA = kt % 2 (A stage, w register set), SB = kt % 3 (B stage).
+        auto step = [&]<int SA, int SB, bool FIRST, bool CHECKED>(int kt) {
+            constexpr int NX = SA ^ 1;
+            constexpr int SB_NEXT = (SB + 1) % 3;
+            using chk = std::integral_constant<bool, CHECKED>;
+            sfor<0, 8>([&](auto mi_) {
+                constexpr int mi = decltype(mi_)::value;
+                sfor<0, 16>([&](auto idx_) {
+                    constexpr int idx = decltype(idx_)::value;
+                    constexpr int kh = idx / 8, ni = idx % 8;
+                    if constexpr (FIRST && kh == 0)
+                        mfma_first<F16>(acc[mi][ni], fb[SA][ni][0], fa[mi & 1][0]);
+                    else
+                        mfma<F16>(acc[mi][ni], fb[SA][ni][kh], fa[mi & 1][kh]);
+                    sched_fence();
+                    if constexpr (mi == kBarRow && idx == kBarIdx) {
+                        wait_vm_lds_barrier<vm_at_barrier()>();
+                        sched_fence();
+                    }
+                    if constexpr (plan_read_a_next(mi, idx) >= 0) {
+                        constexpr int h = plan_read_a_next(mi, idx);
+                        fa[(mi + 1) & 1][h] =
+                            lds_read(frag_a[h] + a_stage(SA) + (mi + 1) * 16 * kRowBytes);
+                        sched_fence();
+                    }
+                    if constexpr (plan_read_b_next(mi, idx) >= 0) {
+                        constexpr int h = plan_read_b_next(mi, idx);
+                        fb[NX][mi][h] = lds_read(frag_b[h] + b_stage(SB_NEXT) + mi * 16 * kRowBytes);
+                        sched_fence();
+                    }
+                    if constexpr (plan_read_a_row0(mi, idx) >= 0) {
+                        constexpr int h = plan_read_a_row0(mi, idx);
+                        fa[0][h] = lds_read(frag_a[h] + a_stage(NX));
+                        sched_fence();
+                    }
+                    if constexpr (plan_load_a(mi, idx) >= 0)
+                        dma(rsrc_a, a_stage(NX), ic<plan_load_a(mi, idx)>{}, kt + 1, chk{});
+                    if constexpr (plan_load_b(mi, idx) >= 0)
+                        dma(rsrc_b, b_stage(SB), ic<plan_load_b(mi, idx)>{}, kt + 3, chk{});
+                    if constexpr (plan_load_a_early(mi, idx) >= 0)
+                        dma(rsrc_a, a_stage(SA), ic<plan_load_a_early(mi, idx)>{}, kt + 2, chk{});
+                });
+            });
+        };
+
+        step.template operator()<0, 0, true, true>(0);
+        int kt = 1; // kt % 6 == 1 at the top of each block of six steps
+        // Unchecked: every prefetch of the block (up to kt + 8) is a full step before T-1.
+        for (; kt + 9 < T; kt += 6) {
+            refresh();
+            step.template operator()<1, 1, false, false>(kt);
+            step.template operator()<0, 2, false, false>(kt + 1);
+            step.template operator()<1, 0, false, false>(kt + 2);
+            step.template operator()<0, 1, false, false>(kt + 3);
+            step.template operator()<1, 2, false, false>(kt + 4);
+            step.template operator()<0, 0, false, false>(kt + 5);
+        }
+        for (; kt < T; kt += 6) { // at most 9 steps left
+            refresh();
+            step.template operator()<1, 1, false, true>(kt);
+            if (kt + 1 < T) step.template operator()<0, 2, false, true>(kt + 1);
+            if (kt + 2 < T) step.template operator()<1, 0, false, true>(kt + 2);
+            if (kt + 3 < T) step.template operator()<0, 1, false, true>(kt + 3);
+            if (kt + 4 < T) step.template operator()<1, 2, false, true>(kt + 4);
+            if (kt + 5 < T) step.template operator()<0, 0, false, true>(kt + 5);
+        }
+
+        // ---- epilogue: accumulators -> 16-bit -> LDS (row major) -> 16-byte NT stores ----
+        wait_vm_lds_barrier<0>(); // trailing DMAs landed, every wave is done reading LDS
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" ::: "memory"); // MFMA -> VALU read distance
+        {
+            const int row = wm * 128 + (lane & 15);
+            const int col = wn * 128 + (lane >> 4) * 4;
+            const int off = row * kCStride + col * 2;
+            sfor<0, 8>([&](auto mi) {
+                sfor<0, 8>([&](auto ni) {
+                    *reinterpret_cast<u32x2 *>(smem + off + mi * 16 * kCStride + ni * 16 * 2) =
+                        pack4<F16>(acc[mi][ni]);
+                });
+            });
+        }
+        wait_vm_lds_barrier<63>();
+        {
+            // wave w streams rows w*64 .. +64, two 512-byte rows per instruction
+            const int row   = wave * 64 + (lane >> 5);
+            const int chunk = lane & 31;
+            const int loff  = row * kCStride + chunk * 16;
+            // rows past m_valid fall outside the resource; chunks past n_valid get an
+            // out-of-range offset. N % 8 == 0, so a chunk never straddles N.
+            const int goff = chunk * 8 < n_valid ? (row * N + chunk * 8) * 2
+                                                 : static_cast<int>(0x80000000u);
+            const __amdgpu_buffer_rsrc_t crs = __builtin_amdgcn_make_buffer_rsrc(
+                c_ptr, static_cast<short>(0), static_cast<int>(m_valid * N * 2), 0x00020000);
+            sfor<0, 2>([&](auto half) {
+                i32x4 d[16];
+                sfor<0, 16>([&](auto i) {
+                    d[i] = lds_read(loff + (half * 16 + i) * 2 * kCStride);
+                });
+                sfor<0, 16>([&](auto i) {
+                    __builtin_amdgcn_raw_buffer_store_b128(
+                        __builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, d[i]), crs,
+                        goff + (half * 16 + i) * 2 * N * 2, 0, /*nt*/ 2);
+                });
+            });
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// Benchmark input generator: splitmix64 of (seed, index) -> Box-Muller N(0, 1).
+// ---------------------------------------------------------------------------------------
+__device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+template <bool F16> __global__ void fill_randn_kernel(uint16_t *p, size_t n, uint64_t seed) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n; i += stride) {
+        const uint64_t r  = splitmix64(seed ^ (i * 0x2545F4914F6CDD1Dull));
+        const float    u1 = (static_cast<float>(r >> 40) + 1.0f) * (1.0f / 16777217.0f); // (0, 1]
+        const float    u2 = static_cast<float>((r >> 16) & 0xFFFFFF) * (1.0f / 16777216.0f);
+        const float    v  = sqrtf(-2.0f * logf(u1)) * cospif(2.0f * u2);
+        if constexpr (F16)
+            p[i] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+        else
+            p[i] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
+    }
+}
+
+} // namespace
+
+hipError_t launch_grouped_gemm(const KernelArgs &args, bool fp16, int grid, hipStream_t stream) {
+    if (fp16)
+        hipLaunchKernelGGL(grouped_gemm_kernel<true>, dim3(grid), dim3(kThreads), 0, stream, args);
+    else
+        hipLaunchKernelGGL(grouped_gemm_kernel<false>, dim3(grid), dim3(kThreads), 0, stream, args);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_randn(void *p, size_t count, uint64_t seed, bool fp16, hipStream_t stream) {
+    if (count == 0)
+        return hipSuccess;
+    if (fp16)
+        hipLaunchKernelGGL(fill_randn_kernel<true>, dim3(4096), dim3(256), 0, stream,
+                           static_cast<uint16_t *>(p), count, seed);
+    else
+        hipLaunchKernelGGL(fill_randn_kernel<false>, dim3(4096), dim3(256), 0, stream,
+                           static_cast<uint16_t *>(p), count, seed);
+    return hipGetLastError();
+}
+
+} // namespace gg
