@@ -107,20 +107,13 @@ int gg_prepare(int dtype, int group_num, int64_t n, int64_t k, const int64_t *gr
     plan->out       = out;
 
     // Group table: row offset, rows and first tile of every group (empty groups own no
-    // tiles; the kernel skips them while scanning forward).
+    // tiles; the kernel steps over them while scanning forward).
     const int64_t n_tiles = gg::cdiv(n, gg::kTileN);
     std::vector<gg::GroupEntry> table(static_cast<size_t>(group_num));
-    int64_t row = 0, tiles = 0;
-    for (int g = 0; g < group_num; ++g) {
-        table[g].row0  = row;
-        table[g].m     = static_cast<int32_t>(group_m[g]);
-        table[g].tile0 = static_cast<int32_t>(tiles);
-        tiles += gg::cdiv(group_m[g], gg::kTileM) * n_tiles;
-        row += group_m[g];
-        if (group_m[g] > INT32_MAX || tiles > INT32_MAX) {
-            delete plan;
-            return fail(GG_ERR_UNSUPPORTED, "too many rows or tiles for 32-bit tile indices");
-        }
+    const int64_t tiles = gg::build_group_table(group_m, group_num, n_tiles, table.data());
+    if (tiles < 0) {
+        delete plan;
+        return fail(GG_ERR_UNSUPPORTED, "too many rows or tiles for 32-bit tile indices");
     }
     plan->total_tiles = has_output && k > 0 ? static_cast<int>(tiles) : 0;
 

@@ -248,12 +248,9 @@ grouped_gemm_kernel(const KernelArgs args) {
     for (int t = blockIdx.x; t < args.total_tiles; t += gridDim.x) {
         // ---- which tile ---------------------------------------------------------------
         const int L = xcd_remap(t, args.total_tiles, gridDim.x, args.n_xcd);
-        while (g + 1 < args.group_num && args.groups[g + 1].tile0 <= L)
-            ++g;
-        const GroupEntry ge      = args.groups[g];
-        const int        m_tiles = (ge.m + kTileM - 1) / kTileM;
-        int              tm, tn;
-        band_coords(L - ge.tile0, m_tiles, args.n_tiles, args.band, &tm, &tn);
+        int       tm, tn;
+        locate_tile(L, args.groups, args.group_num, args.n_tiles, args.band, &g, &tm, &tn);
+        const GroupEntry ge = args.groups[g];
         const int     m_valid = min(kTileM, ge.m - tm * kTileM);
         const int     n_valid = min(kTileN, N - tn * kTileN);
         const int64_t row0    = ge.row0 + static_cast<int64_t>(tm) * kTileM;

@@ -20,6 +20,7 @@
 #pragma once
 
 #include <stdint.h>
+#include <limits.h>
 
 #if defined(__HIPCC__)
 #define GG_HD __host__ __device__ inline
@@ -75,5 +76,37 @@ struct GroupEntry {
     int32_t m;     // rows (tokens) in the group; 0 for an empty group
     int32_t tile0; // first logical tile of the group
 };
+
+// Fill `table` (group_num entries) from the group sizes; returns the total tile count, or
+// -1 if a size is negative or a count overflows 32 bits.
+inline int64_t build_group_table(const int64_t *group_m, int group_num, int64_t n_tiles,
+                                 GroupEntry *table) {
+    int64_t row = 0, tiles = 0;
+    for (int g = 0; g < group_num; ++g) {
+        if (group_m[g] < 0 || group_m[g] > INT32_MAX)
+            return -1;
+        table[g].row0  = row;
+        table[g].m     = static_cast<int32_t>(group_m[g]);
+        table[g].tile0 = static_cast<int32_t>(tiles);
+        tiles += cdiv(group_m[g], kTileM) * n_tiles;
+        row += group_m[g];
+        if (tiles > INT32_MAX)
+            return -1;
+    }
+    return tiles;
+}
+
+// Group and (M-tile, N-tile) of logical tile L. *g is a hint: the group of a smaller L seen
+// before (0 at the start); logical tiles only grow for one workgroup, so the scan only moves
+// forward. Empty groups own no tiles and are stepped over.
+GG_HD void locate_tile(int L, const GroupEntry *groups, int group_num, int n_tiles, int band,
+                       int *g, int *tm, int *tn) {
+    int gi = *g;
+    while (gi + 1 < group_num && groups[gi + 1].tile0 <= L)
+        ++gi;
+    *g                = gi;
+    const int m_tiles = (groups[gi].m + kTileM - 1) / kTileM;
+    band_coords(L - groups[gi].tile0, m_tiles, n_tiles, band, tm, tn);
+}
 
 } // namespace gg

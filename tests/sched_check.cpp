@@ -1,0 +1,144 @@
+// Host check of the kernel's tile scheduler (gg_schedule.h is compiled here with g++, the same
+// code the gfx950 kernel runs). Exit status 0 = every property holds. Checked:
+//   * xcd_remap is a bijection of [0, total) that keeps every round (grid slots) inside
+//     itself, and gives the workgroups of one XCD one contiguous run of logical tiles;
+//   * band_coords visits every (M-tile, N-tile) of a group exactly once, and 32 consecutive
+//     tiles of a full band touch at most `band` M-tiles and ceil(32 / band) + 1 N-tiles;
+//   * the whole kernel walk (workgroup w handles slots w, w + grid, ...; remap; locate_tile
+//     with its forward-only group hint) covers every (group, M-tile, N-tile) exactly once,
+//     with empty groups owning nothing, and each workgroup's logical tiles only increase.
+#include <cstdio>
+#include <cstdlib>
+#include <set>
+#include <tuple>
+#include <vector>
+
+#include "gg_schedule.h"
+
+static int failures = 0;
+#define CHECK(cond, ...)                                                                      \
+    do {                                                                                      \
+        if (!(cond)) {                                                                        \
+            if (failures < 20) {                                                              \
+                std::printf("FAIL %s:%d: ", __FILE__, __LINE__);                              \
+                std::printf(__VA_ARGS__);                                                     \
+                std::printf("\n");                                                            \
+            }                                                                                 \
+            ++failures;                                                                       \
+        }                                                                                     \
+    } while (0)
+
+static void check_remap(int total, int grid, int n_xcd) {
+    std::vector<int> seen(total, 0);
+    for (int t = 0; t < total; ++t) {
+        const int L = gg::xcd_remap(t, total, grid, n_xcd);
+        CHECK(L >= 0 && L < total, "remap out of range t=%d total=%d grid=%d", t, total, grid);
+        if (L < 0 || L >= total)
+            continue;
+        CHECK(L / grid == t / grid, "remap leaves its round t=%d L=%d grid=%d", t, L, grid);
+        ++seen[L];
+    }
+    for (int L = 0; L < total; ++L)
+        CHECK(seen[L] == 1, "logical tile %d hit %d times (total=%d grid=%d xcd=%d)", L, seen[L],
+              total, grid, n_xcd);
+    if (n_xcd > 1 && grid % n_xcd == 0) {
+        // contiguity: per round and XCD, the logical tiles form one interval
+        for (int base = 0; base < total; base += grid) {
+            for (int x = 0; x < n_xcd; ++x) {
+                int lo = total, hi = -1, cnt = 0;
+                for (int i = x; i < grid && base + i < total; i += n_xcd) {
+                    const int L = gg::xcd_remap(base + i, total, grid, n_xcd);
+                    lo = L < lo ? L : lo;
+                    hi = L > hi ? L : hi;
+                    ++cnt;
+                }
+                CHECK(cnt == 0 || hi - lo + 1 == cnt, "XCD %d of round %d not contiguous", x,
+                      base / grid);
+            }
+        }
+    }
+}
+
+static void check_band(int m_tiles, int n_tiles, int band) {
+    std::set<std::pair<int, int>> seen;
+    const int total = m_tiles * n_tiles;
+    for (int i = 0; i < total; ++i) {
+        int tm, tn;
+        gg::band_coords(i, m_tiles, n_tiles, band, &tm, &tn);
+        CHECK(tm >= 0 && tm < m_tiles && tn >= 0 && tn < n_tiles, "band coords out of range");
+        CHECK(seen.insert({tm, tn}).second, "tile (%d,%d) visited twice", tm, tn);
+    }
+    CHECK((int)seen.size() == total, "band order misses tiles");
+    // locality inside full bands
+    const int full_bands = m_tiles / band;
+    for (int b = 0; b < full_bands; ++b)
+        for (int s = b * band * n_tiles; s + 32 <= (b + 1) * band * n_tiles; s += 32) {
+            std::set<int> ms, ns;
+            for (int i = s; i < s + 32; ++i) {
+                int tm, tn;
+                gg::band_coords(i, m_tiles, n_tiles, band, &tm, &tn);
+                ms.insert(tm);
+                ns.insert(tn);
+            }
+            CHECK((int)ms.size() <= band && (int)ns.size() <= (32 + band - 1) / band + 1,
+                  "32 consecutive tiles touch %zu M-tiles and %zu N-tiles", ms.size(), ns.size());
+        }
+}
+
+static void check_walk(const std::vector<int64_t> &group_m, int64_t n, int grid, int n_xcd) {
+    const int64_t n_tiles = gg::cdiv(n, gg::kTileN);
+    std::vector<gg::GroupEntry> table(group_m.size());
+    const int64_t total = gg::build_group_table(group_m.data(), (int)group_m.size(), n_tiles,
+                                                table.data());
+    CHECK(total >= 0, "table build failed");
+    std::set<std::tuple<int, int, int>> seen;
+    for (int wg = 0; wg < grid; ++wg) {
+        int g = 0, prevL = -1;
+        for (int t = wg; t < total; t += grid) {
+            const int L = gg::xcd_remap(t, (int)total, grid, n_xcd);
+            CHECK(L > prevL, "logical tiles of workgroup %d not increasing", wg);
+            prevL = L;
+            int tm, tn;
+            gg::locate_tile(L, table.data(), (int)group_m.size(), (int)n_tiles, gg::kBand, &g, &tm,
+                            &tn);
+            CHECK(group_m[g] > 0, "tile assigned to empty group %d", g);
+            CHECK(tm * gg::kTileM < group_m[g] && tn * gg::kTileN < n, "tile outside group");
+            CHECK(seen.insert({g, tm, tn}).second, "tile (%d,%d,%d) twice", g, tm, tn);
+        }
+    }
+    int64_t want = 0;
+    for (int64_t m : group_m)
+        want += gg::cdiv(m, gg::kTileM) * n_tiles;
+    CHECK((int64_t)seen.size() == want && want == total, "walk covers %zu of %lld tiles",
+          seen.size(), (long long)want);
+}
+
+int main() {
+    for (int n_xcd : {1, 8})
+        for (int grid : {1, 8, 24, 100, 224, 256})
+            for (int total = 1; total <= 1100; total += (total < 300 ? 1 : 37))
+                check_remap(total, grid, n_xcd);
+    check_remap(2048, 256, 8);
+    check_remap(7168, 256, 8);
+    for (int band = 1; band <= 5; ++band)
+        for (int m = 1; m <= 18; ++m)
+            for (int nt = 1; nt <= 30; nt += 3)
+                check_band(m, nt, band);
+    check_band(16, 16, 4);
+    check_band(16, 28, 4);
+    // the BASELINE configs and ragged / empty groups
+    check_walk(std::vector<int64_t>(4, 256), 512, 8, 8);
+    check_walk(std::vector<int64_t>(8, 4096), 4096, 256, 8);
+    check_walk(std::vector<int64_t>(8, 4096), 7168, 256, 8);
+    check_walk(std::vector<int64_t>(32, 520), 2880, 256, 8);
+    check_walk(std::vector<int64_t>(1, 2048), 7168, 224, 8);
+    check_walk({0, 300, 0, 0, 1, 2000, 0}, 1000, 17, 1);
+    check_walk({0, 300, 0, 0, 1, 2000, 0}, 1000, 24, 8);
+    check_walk({257, 0, 255, 4096, 3}, 264, 256, 8);
+    if (failures) {
+        std::printf("%d failures\n", failures);
+        return 1;
+    }
+    std::printf("schedule OK\n");
+    return 0;
+}

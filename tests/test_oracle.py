@@ -1,0 +1,208 @@
+"""Pins the CPU oracle (oracle/gg_oracle.c) before anything is checked against it.
+
+Each check is independent of the oracle's own formulas: the C++ standard's known answer and
+libstdc++'s engine for mt19937_64, numpy/torch conversions for the 16-bit formats, numpy
+float64 / int64 matmul for the GEMM, and the reference driver's specification
+(bench/bench_main.cpp:208-271) for the sampler and the tolerance rule.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+# --------------------------------------------------------------------------------------
+# mt19937_64 (the sampler's engine)
+# --------------------------------------------------------------------------------------
+def test_mt19937_64_standard_known_answer(oracle):
+    # C++ standard [rand.predef]: the 10000th output of a default-constructed mt19937_64
+    assert oracle.mt19937_64_nth(5489, 10000) == 9981545732273789042
+
+
+def test_mt19937_64_matches_libstdcxx(oracle):
+    with open(os.path.join(HERE, "golden", "mt19937_64.json")) as f:
+        gold = json.load(f)
+    for seed in (1234, 5489):
+        want = np.array([int(v) for v in gold[f"seed_{seed}"]], dtype=np.uint64)
+        assert np.array_equal(oracle.mt19937_64(seed, len(want)), want)
+    assert oracle.mt19937_64_nth(5489, 10000) == int(gold["default_10000th"])
+
+
+# --------------------------------------------------------------------------------------
+# 16-bit formats
+# --------------------------------------------------------------------------------------
+def test_bf16_decode_all_patterns(oracle):
+    bits = np.arange(1 << 16, dtype=np.uint16)
+    got = oracle.decode(0, bits)
+    want = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).float().numpy()
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_fp16_decode_all_patterns(oracle):
+    bits = np.arange(1 << 16, dtype=np.uint16)
+    got = oracle.decode(1, bits)
+    want = bits.view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def _encode_cases():
+    rng = np.random.default_rng(3)
+    v = np.concatenate([
+        rng.standard_normal(200000).astype(np.float32) * 50,
+        rng.standard_normal(20000).astype(np.float32) * 1e-5,           # fp16 subnormals
+        (rng.integers(0, 1 << 16, 40000) << 16 | 0x8000).astype(np.uint32).view(np.float32),  # bf16 ties
+        (rng.integers(0, 1 << 16, 40000) << 16 | 0x7fff).astype(np.uint32).view(np.float32),
+        np.array([0.0, -0.0, np.inf, -np.inf, 65504, 65519.99, 65520, 65536, 3e38, -3e38,
+                  6.1035156e-05, 6.0e-08, 2.98e-08, 2.99e-08, 1.0009765625, 1.00048828125],
+                 dtype=np.float32),
+    ])
+    return v[np.isfinite(v) | np.isinf(v)]
+
+
+def test_bf16_encode_rne(oracle):
+    v = _encode_cases()
+    got = oracle.encode(0, v)
+    want = torch.from_numpy(v).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, want)
+
+
+def test_fp16_encode_rne(oracle):
+    v = _encode_cases()
+    with np.errstate(over="ignore"):
+        want = v.astype(np.float16).view(np.uint16)
+    got = oracle.encode(1, v)
+    assert np.array_equal(got, want)
+
+
+def test_encode_nan_stays_nan(oracle):
+    v = np.array([np.nan, -np.nan], dtype=np.float32)
+    for dt in (0, 1):
+        assert np.isnan(oracle.decode(dt, oracle.encode(dt, v))).all()
+
+
+# --------------------------------------------------------------------------------------
+# the grouped GEMM
+# --------------------------------------------------------------------------------------
+def _rand_problem(dt, group_m, n, k, seed):
+    rng = np.random.default_rng(seed)
+    tot = sum(group_m)
+    x = oracle_encode_np(dt, rng.standard_normal((tot, k)).astype(np.float32))
+    w = oracle_encode_np(dt, rng.standard_normal((len(group_m), n, k)).astype(np.float32))
+    return x, w
+
+
+def oracle_encode_np(dt, v):
+    if dt == 0:
+        return torch.from_numpy(v).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    return v.astype(np.float16).view(np.uint16)
+
+
+def _decode_np(dt, b):
+    if dt == 0:
+        return torch.from_numpy(b.view(np.int16)).view(torch.bfloat16).float().numpy()
+    return b.view(np.float16).astype(np.float32)
+
+
+@pytest.mark.parametrize("dt,group_m,n,k", [
+    (0, [5, 0, 17, 1], 24, 40),
+    (1, [33, 2], 8, 7),
+    (0, [0, 0], 16, 16),
+    (0, [64, 64, 64], 72, 129),
+    (1, [300], 40, 1000),
+])
+def test_grouped_gemm_vs_numpy_float64(oracle, dt, group_m, n, k):
+    """Per group out_g = x_g @ w_g^T (numpy float64 on the same decoded inputs)."""
+    x, w = _rand_problem(dt, group_m, n, k, seed=k + n)
+    got = oracle.grouped_gemm(dt, x, w, group_m)
+    xf, wf = _decode_np(dt, x).astype(np.float64), _decode_np(dt, w).astype(np.float64)
+    row = 0
+    for g, m in enumerate(group_m):
+        want = xf[row:row + m] @ wf[g].T
+        np.testing.assert_allclose(got[row:row + m], want, rtol=1e-4, atol=1e-4 * np.sqrt(k))
+        row += m
+    assert got.shape == (sum(group_m), n)
+
+
+def test_grouped_gemm_exact_integers(oracle):
+    """Small integers: every fp32 partial sum is exact, so the result equals int64 matmul."""
+    rng = np.random.default_rng(11)
+    group_m, n, k = [7, 0, 12, 30], 20, 77
+    xi = rng.integers(-8, 9, (sum(group_m), k))
+    wi = rng.integers(-8, 9, (len(group_m), n, k))
+    x = oracle_encode_np(0, xi.astype(np.float32))
+    w = oracle_encode_np(0, wi.astype(np.float32))
+    got = oracle.grouped_gemm(0, x, w, group_m)
+    row = 0
+    for g, m in enumerate(group_m):
+        assert np.array_equal(got[row:row + m].astype(np.int64), xi[row:row + m] @ wi[g].T)
+        row += m
+
+
+def test_group_rows_and_sampled_agree_with_full(oracle):
+    dt, group_m, n, k = 0, [40, 9, 33], 56, 200
+    x, w = _rand_problem(dt, group_m, n, k, seed=5)
+    full = oracle.grouped_gemm(dt, x, w, group_m)
+    part = oracle.group_rows(dt, x[40:49], w[1])
+    np.testing.assert_allclose(part, full[40:49], rtol=1e-6, atol=1e-5)
+    s = oracle.make_samples(len(group_m), n, group_m, 256)
+    ref = oracle.sampled(dt, x, w, s)
+    np.testing.assert_allclose(ref, full[s[:, 0], s[:, 1]], rtol=1e-5, atol=1e-4)
+
+
+# --------------------------------------------------------------------------------------
+# sampler (bench/bench_main.cpp:208-227)
+# --------------------------------------------------------------------------------------
+def test_samples_follow_reference_rule(oracle):
+    group_m, n = [5, 0, 300, 1], 1000
+    s = oracle.make_samples(len(group_m), n, group_m, 256)
+    assert s.shape == (3 * 260, 3)  # empty groups get none
+    seq = oracle.mt19937_64(1234, 2 * 256 * 3)  # one engine for all groups, row draw first
+    pos, draw, row0 = 0, 0, 0
+    for g, m in enumerate(group_m):
+        if m == 0:
+            continue
+        corners = [(row0, 0), (row0, n - 1), (row0 + m - 1, 0), (row0 + m - 1, n - 1)]
+        assert [tuple(r[:2]) for r in s[pos:pos + 4]] == corners
+        for i in range(256):
+            r, c, gg = s[pos + 4 + i]
+            assert gg == g and row0 <= r < row0 + m and 0 <= c < n
+            assert r == row0 + int(seq[draw]) % m and c == int(seq[draw + 1]) % n
+            draw += 2
+        pos += 260
+        row0 += m
+
+
+# --------------------------------------------------------------------------------------
+# tolerance rule (bench/bench_main.cpp:235-271)
+# --------------------------------------------------------------------------------------
+def test_check_rule(oracle):
+    ref = np.array([0.0, 100.0, -100.0, 5.0, 1.0, 1.0], dtype=np.float32)
+    got = np.array([0.01, 101.0, -101.5, 5.0, np.nan, np.inf], dtype=np.float32)
+    bad, mx = oracle.check(got, ref)
+    # 0.01 <= 0.01 pass; 1.0 <= 1.01 pass; 1.5 > 1.01 fail; exact pass; NaN fail; inf fail
+    assert bad == 3
+    assert mx == np.inf
+    bad, mx = oracle.check(got[:4], ref[:4])
+    assert bad == 1 and abs(mx - 1.5) < 1e-6
+
+
+# --------------------------------------------------------------------------------------
+# input generator (bench/bench_main.cpp:160-176); exact bits unpinned (device math library)
+# --------------------------------------------------------------------------------------
+@pytest.mark.parametrize("dt", [0, 1])
+def test_fill_randn_is_standard_normal(oracle, dt):
+    from scipy import stats
+
+    v = _decode_np(dt, oracle.fill_randn(dt, 400000, 1)).astype(np.float64)
+    assert abs(v.mean()) < 0.01 and abs(v.std() - 1.0) < 0.01
+    assert stats.kstest(v, "norm").statistic < 0.01
+    assert np.array_equal(oracle.fill_randn(dt, 1000, 1), oracle.fill_randn(dt, 4000, 1)[:1000])
+    assert not np.array_equal(oracle.fill_randn(dt, 1000, 1), oracle.fill_randn(dt, 1000, 2))
