@@ -84,6 +84,9 @@ def main():
     ap.add_argument("--workload", default=HEADLINE, choices=sorted(WORKLOADS))
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
+                    help="only run 3 device copies of BYTES bytes (reference kernel for the "
+                         "FETCH_SIZE / WRITE_SIZE scale factors) and exit")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -92,6 +95,15 @@ def main():
         sys.exit(2)
 
     import torch
+
+    if args.calibrate_copy:
+        src = torch.ones(args.calibrate_copy, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": args.calibrate_copy, "copies": 3}), flush=True)
+        return
 
     pkg = entry.load_package()
     dtype, b, m, n, k = WORKLOADS[args.workload]
