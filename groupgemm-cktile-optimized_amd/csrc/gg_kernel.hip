@@ -63,9 +63,34 @@ constexpr int kAStages  = 2;
 constexpr int kBStages  = 3;
 constexpr int kLdsBytes = (kAStages + kBStages) * kOpBytes; // 163840 = all of gfx950's LDS
 constexpr int kLoads    = kOpBytes / 1024 / kWaves;         // 1 KB DMAs per wave per operand step
-constexpr int kEarlyA   = 2;                                // A(kt+2) DMAs issued in step kt
+// Slot-plan knobs (compile-time; the defaults are the tuned plan).
+#ifndef GG_EARLY_A
+#define GG_EARLY_A 2 // DMAs of A(kt+2) issued at the end of step kt
+#endif
+#ifndef GG_A_PER_ROW
+#define GG_A_PER_ROW 2 // A(kt+1) DMAs per row: 2 (after MFMAs 0, 8) or 4 (0, 4, 8, 12)
+#endif
+#ifndef GG_B_ROW0
+#define GG_B_ROW0 3 // B(kt+3) DMAs: two per row in rows GG_B_ROW0 .. +3
+#endif
+#ifndef GG_B_SLOT0
+#define GG_B_SLOT0 0 // ... after MFMAs GG_B_SLOT0 and GG_B_SLOT0 + 8
+#endif
+#ifndef GG_BAR_IDX
+#define GG_BAR_IDX 7 // the step's barrier follows this MFMA of row 7
+#endif
+#ifndef GG_M0_AHEAD
+#define GG_M0_AHEAD 1 // write M0 for a DMA before the MFMA of its slot (1) or next to it (0)
+#endif
+#ifndef GG_ROW0_AT_BAR
+#define GG_ROW0_AT_BAR 1 // next step's row-0 x fragments right after the barrier (1) or 2 slots later (0)
+#endif
+#ifndef GG_STAGE_BASES
+#define GG_STAGE_BASES 1 // per-stage LDS base registers so every read uses the 16-bit offset field
+#endif
+constexpr int kEarlyA   = GG_EARLY_A;
 constexpr int kCStride  = kTileN * 2 + 16;                  // staged C row stride (528 B)
-static_assert(kLoads == 8 && kEarlyA == 2, "the slot plan below is written for 8 + 2 DMAs");
+static_assert(kLoads == 8 && kEarlyA >= 0 && kEarlyA <= 4, "slot plan written for 8 DMAs per operand");
 static_assert(kTileM * kCStride <= kLdsBytes, "the staged C tile must fit in LDS");
 
 constexpr int a_stage(int s) { return s * kOpBytes; }
@@ -76,7 +101,8 @@ constexpr int b_stage(int s) { return (kAStages + s) * kOpBytes; }
 // says which memory operation follows MFMA idx of row mi (-1: none). LDS reads sit after odd
 // MFMAs, DMAs after even ones, so no MFMA gap holds more than one memory operation.
 // ---------------------------------------------------------------------------------------
-constexpr int kBarRow = 7, kBarIdx = 7; // the step's barrier follows this MFMA
+constexpr int kBarRow = 7, kBarIdx = GG_BAR_IDX; // the step's barrier follows this MFMA
+static_assert(kBarIdx >= 4 && kBarIdx <= 11 && kBarIdx % 2 == 1, "barrier slot");
 
 // x fragments of row mi+1 (k-half kh) into the register ring.
 constexpr int plan_read_a_next(int mi, int idx) {
@@ -89,22 +115,47 @@ constexpr int plan_read_b_next(int mi, int idx) {
         return idx == 5 ? 0 : idx == 7 ? 1 : -1;
     return idx == 1 ? 0 : idx == 3 ? 1 : -1;
 }
-// x fragments of row 0 of step kt+1, after the barrier.
+// x fragments of row 0 of step kt+1, right after the barrier.
 constexpr int plan_read_a_row0(int mi, int idx) {
-    return (mi == 7 && (idx == 9 || idx == 11)) ? (idx - 9) / 2 : -1;
+    constexpr int first = GG_ROW0_AT_BAR ? kBarIdx : kBarIdx + 2;
+    return (mi == 7 && (idx == first || idx == first + 2)) ? (idx - first) / 2 : -1;
 }
-// DMA j of A(kt+1), j = kEarlyA..7: rows 0-2 after MFMAs 0 and 8.
+// DMA j of A(kt+1), j = kEarlyA..7: GG_A_PER_ROW per row from row 0.
 constexpr int plan_load_a(int mi, int idx) {
-    return (mi <= 2 && (idx == 0 || idx == 8)) ? kEarlyA + mi * 2 + idx / 8 : -1;
+    constexpr int per = GG_A_PER_ROW, step = 16 / per;
+    if (idx % step != 0)
+        return -1;
+    const int j = kEarlyA + mi * per + idx / step;
+    return j < kLoads ? j : -1;
 }
-// DMA j of B(kt+3): rows 3-6 after MFMAs 0 and 8.
+// DMA j of B(kt+3): two per row in rows GG_B_ROW0 .. +3.
 constexpr int plan_load_b(int mi, int idx) {
-    return (mi >= 3 && mi <= 6 && (idx == 0 || idx == 8)) ? (mi - 3) * 2 + idx / 8 : -1;
+    return (mi >= GG_B_ROW0 && mi < GG_B_ROW0 + 4 && (idx == GG_B_SLOT0 || idx == GG_B_SLOT0 + 8))
+               ? (mi - GG_B_ROW0) * 2 + (idx - GG_B_SLOT0) / 8
+               : -1;
 }
-// DMA j < kEarlyA of A(kt+2): row 7 after MFMAs 12 and 14 (its stage is free after the barrier).
+// DMA j < kEarlyA of A(kt+2): the first even slots of row 7 after the barrier (A(kt)'s
+// stage is free once every wave passed it).
 constexpr int plan_load_a_early(int mi, int idx) {
-    return (mi == 7 && (idx == 12 || idx == 14)) ? (idx - 12) / 2 : -1;
+    const int j = (idx - (kBarIdx + 1)) / 2;
+    return (mi == 7 && idx > kBarIdx && idx % 2 == 0 && j < kEarlyA) ? j : -1;
 }
+// The DMA that follows MFMA idx of row mi: 0 none, 1 A(kt+1), 2 B(kt+3), 3 A(kt+2).
+constexpr int plan_dma_kind(int mi, int idx) {
+    return plan_load_a(mi, idx) >= 0 ? 1 : plan_load_b(mi, idx) >= 0 ? 2 : plan_load_a_early(mi, idx) >= 0 ? 3 : 0;
+}
+constexpr int plan_dma_j(int mi, int idx) {
+    return plan_load_a(mi, idx) >= 0 ? plan_load_a(mi, idx)
+           : plan_load_b(mi, idx) >= 0 ? plan_load_b(mi, idx) : plan_load_a_early(mi, idx);
+}
+constexpr bool one_dma_per_slot() {
+    for (int p = 0; p < 8 * 16; ++p)
+        if ((plan_load_a(p / 16, p % 16) >= 0) + (plan_load_b(p / 16, p % 16) >= 0) +
+                (plan_load_a_early(p / 16, p % 16) >= 0) > 1)
+            return false;
+    return true;
+}
+static_assert(one_dma_per_slot(), "at most one DMA per MFMA gap");
 // DMAs that may still be in flight at the barrier: those issued after the last A(kt+1) DMA.
 // Loads complete in order, so vmcnt(this) means all of A(kt+1) (and everything older) landed.
 constexpr int vm_at_barrier() {
@@ -159,7 +210,17 @@ __device__ __forceinline__ i32x4 dma_rsrc(const void *p, uint32_t bytes) {
 }
 
 // 64 lanes x 16 B from global (resource + lane offset + K-step offset) into LDS at
-// lds_dst + 16 * lane. The compiler cannot see this LDS write: waits are placed by hand.
+// M0 + 16 * lane. The compiler cannot see this LDS write: waits are placed by hand.
+// set_m0 must precede the load by at least one instruction (SALU M0 write -> LDS DMA).
+template <int OFF> __device__ __forceinline__ void set_m0(uint32_t lds_base) {
+    asm volatile("s_add_u32 m0, %0, %1" : : "s"(lds_base), "n"(OFF) : "memory");
+}
+__device__ __forceinline__ void dma16_m0(int voff, const i32x4 &rsrc, int soff) {
+    asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds"
+                 :
+                 : "v"(voff), "s"(rsrc), "s"(soff)
+                 : "memory");
+}
 __device__ __forceinline__ void dma16(uint32_t lds_dst, int voff, const i32x4 &rsrc, int soff) {
     asm volatile("s_mov_b32 m0, %0\n\t"
                  "s_nop 0\n\t"
@@ -238,6 +299,11 @@ grouped_gemm_kernel(const KernelArgs args) {
         frag_a[kh]    = wm * 128 * kRowBytes + off;
         frag_b[kh]    = wn * 128 * kRowBytes + off;
     });
+    int base_b0[2], base_b1[2];
+    sfor<0, 2>([&](auto kh) {
+        base_b0[kh] = frag_b[kh] + b_stage(0);
+        base_b1[kh] = frag_b[kh] + b_stage(1);
+    });
     auto lds_read = [&](int off) -> i32x4 { return *reinterpret_cast<const i32x4 *>(smem + off); };
 
     f32x4 acc[8][8];
@@ -273,7 +339,34 @@ grouped_gemm_kernel(const KernelArgs args) {
             fresh_s(dma_base);
             sfor<0, kLoads>([&](auto j) { fresh_v(voff[j]); });
             fresh_v(ktail_bad);
-            sfor<0, 2>([&](auto h) { fresh_v(frag_a[h]); fresh_v(frag_b[h]); });
+            sfor<0, 2>([&](auto h) {
+                fresh_v(frag_a[h]);
+                fresh_v(frag_b[h]);
+                fresh_v(base_b0[h]);
+                fresh_v(base_b1[h]);
+            });
+        };
+        // w fragment (stage S, column block ni, k-half h) as base + 16-bit immediate: B0 from
+        // its own base, B1 and B2 from a base at B1 (B2 = +32 KB).
+        auto read_b = [&]<int S>(int h, int ni) -> i32x4 {
+            if constexpr (!GG_STAGE_BASES)
+                return lds_read(frag_b[h] + b_stage(S) + ni * 16 * kRowBytes);
+            else if constexpr (S == 0)
+                return lds_read(base_b0[h] + ni * 16 * kRowBytes);
+            else
+                return lds_read(base_b1[h] + (S - 1) * kOpBytes + ni * 16 * kRowBytes);
+        };
+        // The DMA of a slot whose M0 was written before the slot's MFMA.
+        auto dma_m0 = [&](const i32x4 &rsrc, auto j, int kidx, auto checked) {
+            sched_fence();
+            if constexpr (decltype(checked)::value) {
+                const i32x4 rs   = kidx < T ? rsrc : rsrc_0;
+                const int   last = kidx == T - 1 ? -1 : 0; // uniform
+                dma16_m0(voff[j] | (ktail_bad & last), rs, kidx * kRowBytes);
+            } else {
+                dma16_m0(voff[j], rsrc, kidx * kRowBytes);
+            }
+            sched_fence();
         };
         auto dma = [&](const i32x4 &rsrc, int stage, auto j, int kidx, auto checked) {
             sched_fence();
@@ -299,7 +392,7 @@ grouped_gemm_kernel(const KernelArgs args) {
         wait_vm_lds_barrier<kLoads + kEarlyA>(); // A(0), B(0), B(1) landed everywhere
         sfor<0, 8>([&](auto ni) {
             sfor<0, 2>([&](auto kh) {
-                fb[0][ni][kh] = lds_read(frag_b[kh] + b_stage(0) + ni * 16 * kRowBytes);
+                fb[0][ni][kh] = read_b.template operator()<0>(kh, ni);
             });
         });
         sfor<0, 2>([&](auto kh) { fa[0][kh] = lds_read(frag_a[kh] + a_stage(0)); });
@@ -316,6 +409,12 @@ grouped_gemm_kernel(const KernelArgs args) {
                 sfor<0, 16>([&](auto idx_) {
                     constexpr int idx = decltype(idx_)::value;
                     constexpr int kh = idx / 8, ni = idx % 8;
+                    constexpr int dk = plan_dma_kind(mi, idx), dj = plan_dma_j(mi, idx);
+                    constexpr int d_stage = dk == 1 ? a_stage(NX) : dk == 2 ? b_stage(SB) : a_stage(SA);
+                    if constexpr (dk != 0 && GG_M0_AHEAD) {
+                        set_m0<d_stage + dj * 4096>(dma_base); // the MFMA below is the wait state
+                        sched_fence();
+                    }
                     if constexpr (FIRST && kh == 0)
                         mfma_first<F16>(acc[mi][ni], fb[SA][ni][0], fa[mi & 1][0]);
                     else
@@ -333,7 +432,7 @@ grouped_gemm_kernel(const KernelArgs args) {
                     }
                     if constexpr (plan_read_b_next(mi, idx) >= 0) {
                         constexpr int h = plan_read_b_next(mi, idx);
-                        fb[NX][mi][h] = lds_read(frag_b[h] + b_stage(SB_NEXT) + mi * 16 * kRowBytes);
+                        fb[NX][mi][h] = read_b.template operator()<SB_NEXT>(h, mi);
                         sched_fence();
                     }
                     if constexpr (plan_read_a_row0(mi, idx) >= 0) {
@@ -341,12 +440,14 @@ grouped_gemm_kernel(const KernelArgs args) {
                         fa[0][h] = lds_read(frag_a[h] + a_stage(NX));
                         sched_fence();
                     }
-                    if constexpr (plan_load_a(mi, idx) >= 0)
-                        dma(rsrc_a, a_stage(NX), ic<plan_load_a(mi, idx)>{}, kt + 1, chk{});
-                    if constexpr (plan_load_b(mi, idx) >= 0)
-                        dma(rsrc_b, b_stage(SB), ic<plan_load_b(mi, idx)>{}, kt + 3, chk{});
-                    if constexpr (plan_load_a_early(mi, idx) >= 0)
-                        dma(rsrc_a, a_stage(SA), ic<plan_load_a_early(mi, idx)>{}, kt + 2, chk{});
+                    if constexpr (dk != 0) {
+                        const int   kidx = dk == 1 ? kt + 1 : dk == 2 ? kt + 3 : kt + 2;
+                        const i32x4 &rs  = dk == 2 ? rsrc_b : rsrc_a;
+                        if constexpr (GG_M0_AHEAD)
+                            dma_m0(rs, ic<dj>{}, kidx, chk{});
+                        else
+                            dma(rs, d_stage, ic<dj>{}, kidx, chk{});
+                    }
                 });
             });
         };
