@@ -88,6 +88,25 @@ constexpr int kLoads    = kOpBytes / 1024 / kWaves;         // 1 KB DMAs per wav
 #ifndef GG_STAGE_BASES
 #define GG_STAGE_BASES 1 // per-stage LDS base registers so every read uses the 16-bit offset field
 #endif
+#ifndef GG_DMA_CPOL_ID
+#define GG_DMA_CPOL_ID 0 // cache-policy modifiers of the operand DMAs: see GG_DMA_CPOL
+#endif
+#if GG_DMA_CPOL_ID == 0
+#define GG_DMA_CPOL ""
+#elif GG_DMA_CPOL_ID == 1
+#define GG_DMA_CPOL "nt"
+#elif GG_DMA_CPOL_ID == 2
+#define GG_DMA_CPOL "sc0"
+#elif GG_DMA_CPOL_ID == 3
+#define GG_DMA_CPOL "sc1"
+#elif GG_DMA_CPOL_ID == 4
+#define GG_DMA_CPOL "sc0 sc1"
+#elif GG_DMA_CPOL_ID == 5
+#define GG_DMA_CPOL "sc1 nt"
+#endif
+#ifndef GG_EPILOGUE_LDS
+#define GG_EPILOGUE_LDS 1 // C through LDS in whole rows (1) or straight from registers (0)
+#endif
 constexpr int kEarlyA   = GG_EARLY_A;
 constexpr int kCStride  = kTileN * 2 + 16;                  // staged C row stride (528 B)
 static_assert(kLoads == 8 && kEarlyA >= 0 && kEarlyA <= 4, "slot plan written for 8 DMAs per operand");
@@ -216,7 +235,7 @@ template <int OFF> __device__ __forceinline__ void set_m0(uint32_t lds_base) {
     asm volatile("s_add_u32 m0, %0, %1" : : "s"(lds_base), "n"(OFF) : "memory");
 }
 __device__ __forceinline__ void dma16_m0(int voff, const i32x4 &rsrc, int soff) {
-    asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds"
+    asm volatile("buffer_load_dwordx4 %0, %1, %2 offen " GG_DMA_CPOL " lds"
                  :
                  : "v"(voff), "s"(rsrc), "s"(soff)
                  : "memory");
@@ -224,7 +243,7 @@ __device__ __forceinline__ void dma16_m0(int voff, const i32x4 &rsrc, int soff) 
 __device__ __forceinline__ void dma16(uint32_t lds_dst, int voff, const i32x4 &rsrc, int soff) {
     asm volatile("s_mov_b32 m0, %0\n\t"
                  "s_nop 0\n\t"
-                 "buffer_load_dwordx4 %1, %2, %3 offen lds"
+                 "buffer_load_dwordx4 %1, %2, %3 offen " GG_DMA_CPOL " lds"
                  :
                  : "s"(lds_dst), "v"(voff), "s"(rsrc), "s"(soff)
                  : "memory", "m0");
@@ -310,148 +329,245 @@ grouped_gemm_kernel(const KernelArgs args) {
     i32x4 fa[2][2];    // x fragments: row ring x k-half
     i32x4 fb[2][8][2]; // w fragments: step parity x column block x k-half
 
-    int g = 0;
-    for (int t = blockIdx.x; t < args.total_tiles; t += gridDim.x) {
-        // ---- which tile ---------------------------------------------------------------
+    // One output tile: its DMA sources and where its C block goes.
+    struct Tile {
+        i32x4     rsrc_a, rsrc_b; // x rows / w rows of the tile, bounded to the valid rows
+        uint16_t *c_ptr;          // output block origin
+        int       m_valid, n_valid;
+    };
+    int  g         = 0; // group hint of locate_tile (logical tiles only grow)
+    auto make_tile = [&](int t) -> Tile {
         const int L = xcd_remap(t, args.total_tiles, gridDim.x, args.n_xcd);
         int       tm, tn;
         locate_tile(L, args.groups, args.group_num, args.n_tiles, args.band, &g, &tm, &tn);
         const GroupEntry ge = args.groups[g];
-        const int     m_valid = min(kTileM, ge.m - tm * kTileM);
-        const int     n_valid = min(kTileN, N - tn * kTileN);
-        const int64_t row0    = ge.row0 + static_cast<int64_t>(tm) * kTileM;
-        const int64_t col0    = static_cast<int64_t>(tn) * kTileN;
-        const uint16_t *a_ptr = static_cast<const uint16_t *>(args.x) + row0 * K;
-        const uint16_t *b_ptr = static_cast<const uint16_t *>(args.w) +
-                                (static_cast<int64_t>(g) * N + col0) * K;
-        uint16_t *c_ptr = static_cast<uint16_t *>(args.out) + row0 * N + col0;
+        Tile             tl;
+        tl.m_valid         = min(kTileM, ge.m - tm * kTileM);
+        tl.n_valid         = min(kTileN, N - tn * kTileN);
+        const int64_t row0 = ge.row0 + static_cast<int64_t>(tm) * kTileM;
+        const int64_t col0 = static_cast<int64_t>(tn) * kTileN;
+        tl.rsrc_a = dma_rsrc(static_cast<const uint16_t *>(args.x) + row0 * K,
+                             static_cast<uint32_t>(tl.m_valid) * K * 2);
+        tl.rsrc_b = dma_rsrc(static_cast<const uint16_t *>(args.w) + (static_cast<int64_t>(g) * N + col0) * K,
+                             static_cast<uint32_t>(tl.n_valid) * K * 2);
+        tl.c_ptr  = static_cast<uint16_t *>(args.out) + row0 * N + col0;
+        return tl;
+    };
+    const i32x4 rsrc_0 = dma_rsrc(args.x, 0); // zero length: no traffic, the DMA writes zeros
 
-        const i32x4 rsrc_a = dma_rsrc(a_ptr, static_cast<uint32_t>(m_valid) * K * 2);
-        const i32x4 rsrc_b = dma_rsrc(b_ptr, static_cast<uint32_t>(n_valid) * K * 2);
-        const i32x4 rsrc_0 = dma_rsrc(a_ptr, 0);
+    int t = blockIdx.x;
+    if (t >= args.total_tiles)
+        return;
+    Tile cur = make_tile(t);
+    const i32x4 &rsrc_a = cur.rsrc_a;
+    const i32x4 &rsrc_b = cur.rsrc_b;
 
-        // DMA j of K step kidx into the stage at byte offset `stage`. CHECKED: kidx may be past
-        // the last step (zero-length resource) or be the last, partial step (masked chunks).
-        // Per-wave LDS destination base and per-lane offsets, re-materialised at the top of
-        // every loop body (see fresh_v).
-        uint32_t dma_base = lds0 + wave * 1024;
-        auto refresh = [&]() {
-            fresh_s(dma_base);
-            sfor<0, kLoads>([&](auto j) { fresh_v(voff[j]); });
-            fresh_v(ktail_bad);
-            sfor<0, 2>([&](auto h) {
-                fresh_v(frag_a[h]);
-                fresh_v(frag_b[h]);
-                fresh_v(base_b0[h]);
-                fresh_v(base_b1[h]);
-            });
-        };
-        // w fragment (stage S, column block ni, k-half h) as base + 16-bit immediate: B0 from
-        // its own base, B1 and B2 from a base at B1 (B2 = +32 KB).
-        auto read_b = [&]<int S>(int h, int ni) -> i32x4 {
-            if constexpr (!GG_STAGE_BASES)
-                return lds_read(frag_b[h] + b_stage(S) + ni * 16 * kRowBytes);
-            else if constexpr (S == 0)
-                return lds_read(base_b0[h] + ni * 16 * kRowBytes);
-            else
-                return lds_read(base_b1[h] + (S - 1) * kOpBytes + ni * 16 * kRowBytes);
-        };
-        // The DMA of a slot whose M0 was written before the slot's MFMA.
-        auto dma_m0 = [&](const i32x4 &rsrc, auto j, int kidx, auto checked) {
-            sched_fence();
-            if constexpr (decltype(checked)::value) {
-                const i32x4 rs   = kidx < T ? rsrc : rsrc_0;
-                const int   last = kidx == T - 1 ? -1 : 0; // uniform
-                dma16_m0(voff[j] | (ktail_bad & last), rs, kidx * kRowBytes);
-            } else {
-                dma16_m0(voff[j], rsrc, kidx * kRowBytes);
-            }
-            sched_fence();
-        };
-        auto dma = [&](const i32x4 &rsrc, int stage, auto j, int kidx, auto checked) {
-            sched_fence();
-            const uint32_t dst = dma_base + stage + j * 4096;
-            if constexpr (decltype(checked)::value) {
-                const i32x4 rs   = kidx < T ? rsrc : rsrc_0;
-                const int   last = kidx == T - 1 ? -1 : 0; // uniform
-                dma16(dst, voff[j] | (ktail_bad & last), rs, kidx * kRowBytes);
-            } else {
-                dma16(dst, voff[j], rsrc, kidx * kRowBytes);
-            }
-            sched_fence();
-        };
+    // DMA j of K step kidx into the stage at byte offset `stage`. CHECKED: kidx may be past
+    // the last step (zero-length resource) or be the last, partial step (masked chunks).
+    // Per-wave LDS destination base and per-lane offsets, re-materialised at the top of
+    // every loop body (see fresh_v).
+    uint32_t dma_base = lds0 + wave * 1024;
+    auto refresh = [&]() {
+        fresh_s(dma_base);
+        sfor<0, kLoads>([&](auto j) { fresh_v(voff[j]); });
+        fresh_v(ktail_bad);
+        sfor<0, 2>([&](auto h) {
+            fresh_v(frag_a[h]);
+            fresh_v(frag_b[h]);
+            fresh_v(base_b0[h]);
+            fresh_v(base_b1[h]);
+        });
+    };
+    // w fragment (stage S, column block ni, k-half h) as base + 16-bit immediate: B0 from
+    // its own base, B1 and B2 from a base at B1 (B2 = +32 KB).
+    auto read_b = [&]<int S>(int h, int ni) -> i32x4 {
+        if constexpr (!GG_STAGE_BASES)
+            return lds_read(frag_b[h] + b_stage(S) + ni * 16 * kRowBytes);
+        else if constexpr (S == 0)
+            return lds_read(base_b0[h] + ni * 16 * kRowBytes);
+        else
+            return lds_read(base_b1[h] + (S - 1) * kOpBytes + ni * 16 * kRowBytes);
+    };
+    // The DMA of a slot whose M0 was written before the slot's MFMA.
+    auto dma_m0 = [&](const i32x4 &rsrc, auto j, int kidx, auto checked) {
+        sched_fence();
+        if constexpr (decltype(checked)::value) {
+            const i32x4 rs   = kidx < T ? rsrc : rsrc_0;
+            const int   last = kidx == T - 1 ? -1 : 0; // uniform
+            dma16_m0(voff[j] | (ktail_bad & last), rs, kidx * kRowBytes);
+        } else {
+            dma16_m0(voff[j], rsrc, kidx * kRowBytes);
+        }
+        sched_fence();
+    };
+    auto dma = [&](const i32x4 &rsrc, int stage, auto j, int kidx, auto checked) {
+        sched_fence();
+        const uint32_t dst = dma_base + stage + j * 4096;
+        if constexpr (decltype(checked)::value) {
+            const i32x4 rs   = kidx < T ? rsrc : rsrc_0;
+            const int   last = kidx == T - 1 ? -1 : 0; // uniform
+            dma16(dst, voff[j] | (ktail_bad & last), rs, kidx * kRowBytes);
+        } else {
+            dma16(dst, voff[j], rsrc, kidx * kRowBytes);
+        }
+        sched_fence();
+    };
 
-        // ---- prologue: A(0), B(0..2), first DMAs of A(1); then B(0) and A(0) row 0 -> regs
-        wait_vm_lds_barrier<63>(); // previous tile's epilogue is done with LDS everywhere
+    // ---- prologue: A(0), B(0..2) and the first DMAs of A(1) of tile `cur` -------------
+    auto issue_prologue = [&]() {
         refresh();
         sfor<0, kLoads>([&](auto j) { dma(rsrc_a, a_stage(0), j, 0, std::true_type{}); });
         sfor<0, kLoads>([&](auto j) { dma(rsrc_b, b_stage(0), j, 0, std::true_type{}); });
         sfor<0, kLoads>([&](auto j) { dma(rsrc_b, b_stage(1), j, 1, std::true_type{}); });
         sfor<0, kLoads>([&](auto j) { dma(rsrc_b, b_stage(2), j, 2, std::true_type{}); });
         sfor<0, kEarlyA>([&](auto j) { dma(rsrc_a, a_stage(1), j, 1, std::true_type{}); });
-        wait_vm_lds_barrier<kLoads + kEarlyA>(); // A(0), B(0), B(1) landed everywhere
+    };
+    // Then B(0) and A(0) row 0 into registers. VM: DMAs/stores issued after B(1)'s last.
+    auto finish_prologue = [&]<int VM>() {
+        wait_vm_lds_barrier<VM>(); // A(0), B(0), B(1) landed everywhere
         sfor<0, 8>([&](auto ni) {
-            sfor<0, 2>([&](auto kh) {
-                fb[0][ni][kh] = read_b.template operator()<0>(kh, ni);
-            });
+            sfor<0, 2>([&](auto kh) { fb[0][ni][kh] = read_b.template operator()<0>(kh, ni); });
         });
         sfor<0, 2>([&](auto kh) { fa[0][kh] = lds_read(frag_a[kh] + a_stage(0)); });
         wait_vm_lds_barrier<63>(); // every wave holds B(0): its stage may be refilled
+    };
 
-        // ---- one K step -----------------------------------------------------------------
-        // SA = kt % 2 (A stage, w register set), SB = kt % 3 (B stage).
-        auto step = [&]<int SA, int SB, bool FIRST, bool CHECKED>(int kt) {
-            constexpr int NX = SA ^ 1;
-            constexpr int SB_NEXT = (SB + 1) % 3;
-            using chk = std::integral_constant<bool, CHECKED>;
-            sfor<0, 8>([&](auto mi_) {
-                constexpr int mi = decltype(mi_)::value;
-                sfor<0, 16>([&](auto idx_) {
-                    constexpr int idx = decltype(idx_)::value;
-                    constexpr int kh = idx / 8, ni = idx % 8;
-                    constexpr int dk = plan_dma_kind(mi, idx), dj = plan_dma_j(mi, idx);
-                    constexpr int d_stage = dk == 1 ? a_stage(NX) : dk == 2 ? b_stage(SB) : a_stage(SA);
-                    if constexpr (dk != 0 && GG_M0_AHEAD) {
-                        set_m0<d_stage + dj * 4096>(dma_base); // the MFMA below is the wait state
-                        sched_fence();
-                    }
-                    if constexpr (FIRST && kh == 0)
-                        mfma_first<F16>(acc[mi][ni], fb[SA][ni][0], fa[mi & 1][0]);
-                    else
-                        mfma<F16>(acc[mi][ni], fb[SA][ni][kh], fa[mi & 1][kh]);
-                    sched_fence();
-                    if constexpr (mi == kBarRow && idx == kBarIdx) {
-                        wait_vm_lds_barrier<vm_at_barrier()>();
-                        sched_fence();
-                    }
-                    if constexpr (plan_read_a_next(mi, idx) >= 0) {
-                        constexpr int h = plan_read_a_next(mi, idx);
-                        fa[(mi + 1) & 1][h] =
-                            lds_read(frag_a[h] + a_stage(SA) + (mi + 1) * 16 * kRowBytes);
-                        sched_fence();
-                    }
-                    if constexpr (plan_read_b_next(mi, idx) >= 0) {
-                        constexpr int h = plan_read_b_next(mi, idx);
-                        fb[NX][mi][h] = read_b.template operator()<SB_NEXT>(h, mi);
-                        sched_fence();
-                    }
-                    if constexpr (plan_read_a_row0(mi, idx) >= 0) {
-                        constexpr int h = plan_read_a_row0(mi, idx);
-                        fa[0][h] = lds_read(frag_a[h] + a_stage(NX));
-                        sched_fence();
-                    }
-                    if constexpr (dk != 0) {
-                        const int   kidx = dk == 1 ? kt + 1 : dk == 2 ? kt + 3 : kt + 2;
-                        const i32x4 &rs  = dk == 2 ? rsrc_b : rsrc_a;
-                        if constexpr (GG_M0_AHEAD)
-                            dma_m0(rs, ic<dj>{}, kidx, chk{});
-                        else
-                            dma(rs, d_stage, ic<dj>{}, kidx, chk{});
-                    }
+    // ---- epilogue of a finished tile, straight from the accumulators ------------------
+    // Lane l holds C^T blocks: row l%16, columns 4q..4q+3 (q = l/16) of each 16 x 16 block.
+    // One v_permlane16_swap per dword between the blocks 2j and 2j+1 of a row block leaves
+    // every lane with 8 consecutive columns (16 B) of one row: rows q=0,2 get block 2j,
+    // q=1,3 block 2j+1, columns 0-7 (q<2) or 8-15. 4 stores of 1 KB per 16-row block.
+    // ---- epilogue through LDS: accumulators -> 16-bit -> LDS (row major, 528-byte row stride)
+    // -> every wave streams 64 whole rows with 16-byte NT stores, two 512-byte rows per store.
+    // Needs all of LDS, so the next tile's prologue goes out after it.
+    auto epilogue_lds = [&](uint16_t *c_ptr, int m_valid, int n_valid) {
+        wait_vm_lds_barrier<0>(); // trailing DMAs landed, every wave is done reading LDS
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" ::: "memory"); // MFMA -> VALU read distance
+        {
+            int row = wm * 128 + (lane & 15);
+            fresh_v(row);
+            const int col = wn * 128 + (lane >> 4) * 4;
+            const int off = row * kCStride + col * 2;
+            sfor<0, 8>([&](auto mi) {
+                sfor<0, 8>([&](auto ni) {
+                    asm volatile("" : "+a"(acc[mi][ni]));
+                    *reinterpret_cast<u32x2 *>(smem + off + mi * 16 * kCStride + ni * 16 * 2) =
+                        pack4<F16>(acc[mi][ni]);
                 });
             });
-        };
+        }
+        wait_vm_lds_barrier<63>();
+        int row = wave * 64 + (lane >> 5);
+        fresh_v(row);
+        const int chunk = lane & 31;
+        const int loff  = row * kCStride + chunk * 16;
+        // rows past m_valid fall outside the resource; chunks past n_valid get an
+        // out-of-range offset. N % 8 == 0, so a chunk never straddles N.
+        const int goff = chunk * 8 < n_valid ? (row * N + chunk * 8) * 2 : static_cast<int>(0x80000000u);
+        const __amdgpu_buffer_rsrc_t crs = __builtin_amdgcn_make_buffer_rsrc(
+            c_ptr, static_cast<short>(0), static_cast<int>(m_valid * N * 2), 0x00020000);
+        sfor<0, 2>([&](auto half) {
+            i32x4 d[16];
+            sfor<0, 16>([&](auto i) { d[i] = lds_read(loff + (half * 16 + i) * 2 * kCStride); });
+            sfor<0, 16>([&](auto i) {
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    __builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, d[i]), crs,
+                    goff + (half * 16 + i) * 2 * N * 2, 0, /*nt*/ 2);
+            });
+        });
+        wait_vm_lds_barrier<63>(); // every wave is done reading the staged C
+    };
 
+    constexpr int kStores = 32; // per wave and tile
+    auto epilogue = [&](uint16_t *c_ptr, int m_valid, int n_valid) {
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" ::: "memory"); // MFMA -> VALU read distance
+        const int q   = lane >> 4;
+        const int row = wm * 128 + (lane & 15);
+        int       col = wn * 128 + (q & 1) * 16 + (q >> 1) * 8;
+        fresh_v(col); // computed here, not hoisted out of the tile loop
+        const int voffc = (row * N + col) * 2;
+        // rows past m_valid fall outside the resource; chunks past n_valid get an
+        // out-of-range offset (N % 8 == 0: a chunk never straddles N)
+        const __amdgpu_buffer_rsrc_t crs = __builtin_amdgcn_make_buffer_rsrc(
+            c_ptr, static_cast<short>(0), static_cast<int>(m_valid * N * 2), 0x00020000);
+        sfor<0, 8>([&](auto mi) {
+            int vrow = voffc + mi * 16 * N * 2;
+            fresh_v(vrow);
+            sfor<0, 4>([&](auto j) {
+                sched_fence();
+                // Reads of these accumulators may not move above this point (and so not above
+                // the MFMA -> VALU wait states at the top of the epilogue).
+                asm volatile("" : "+a"(acc[mi][2 * j]), "+a"(acc[mi][2 * j + 1]));
+                const u32x2 p0 = pack4<F16>(acc[mi][2 * j]);
+                const u32x2 p1 = pack4<F16>(acc[mi][2 * j + 1]);
+                const auto  s0 = __builtin_amdgcn_permlane16_swap(p0[0], p1[0], false, false);
+                const auto  s1 = __builtin_amdgcn_permlane16_swap(p0[1], p1[1], false, false);
+                typedef unsigned u32x4v __attribute__((ext_vector_type(4)));
+                const u32x4v d  = {s0[0], s1[0], s0[1], s1[1]};
+                const int    vo = col + 32 * j < n_valid ? vrow + j * 64 : static_cast<int>(0x80000000u);
+                __builtin_amdgcn_raw_buffer_store_b128(d, crs, vo, 0, /*nt*/ 2);
+            });
+        });
+    };
+
+    // ---- one K step -----------------------------------------------------------------
+    // SA = kt % 2 (A stage, w register set), SB = kt % 3 (B stage).
+    auto step = [&]<int SA, int SB, bool FIRST, bool CHECKED>(int kt) {
+        constexpr int NX = SA ^ 1;
+        constexpr int SB_NEXT = (SB + 1) % 3;
+        using chk = std::integral_constant<bool, CHECKED>;
+        sfor<0, 8>([&](auto mi_) {
+            constexpr int mi = decltype(mi_)::value;
+            sfor<0, 16>([&](auto idx_) {
+                constexpr int idx = decltype(idx_)::value;
+                constexpr int kh = idx / 8, ni = idx % 8;
+                constexpr int dk = plan_dma_kind(mi, idx), dj = plan_dma_j(mi, idx);
+                constexpr int d_stage = dk == 1 ? a_stage(NX) : dk == 2 ? b_stage(SB) : a_stage(SA);
+                if constexpr (dk != 0 && GG_M0_AHEAD) {
+                    set_m0<d_stage + dj * 4096>(dma_base); // the MFMA below is the wait state
+                    sched_fence();
+                }
+                if constexpr (FIRST && kh == 0)
+                    mfma_first<F16>(acc[mi][ni], fb[SA][ni][0], fa[mi & 1][0]);
+                else
+                    mfma<F16>(acc[mi][ni], fb[SA][ni][kh], fa[mi & 1][kh]);
+                sched_fence();
+                if constexpr (mi == kBarRow && idx == kBarIdx) {
+                    wait_vm_lds_barrier<vm_at_barrier()>();
+                    sched_fence();
+                }
+                if constexpr (plan_read_a_next(mi, idx) >= 0) {
+                    constexpr int h = plan_read_a_next(mi, idx);
+                    fa[(mi + 1) & 1][h] =
+                        lds_read(frag_a[h] + a_stage(SA) + (mi + 1) * 16 * kRowBytes);
+                    sched_fence();
+                }
+                if constexpr (plan_read_b_next(mi, idx) >= 0) {
+                    constexpr int h = plan_read_b_next(mi, idx);
+                    fb[NX][mi][h] = read_b.template operator()<SB_NEXT>(h, mi);
+                    sched_fence();
+                }
+                if constexpr (plan_read_a_row0(mi, idx) >= 0) {
+                    constexpr int h = plan_read_a_row0(mi, idx);
+                    fa[0][h] = lds_read(frag_a[h] + a_stage(NX));
+                    sched_fence();
+                }
+                if constexpr (dk != 0) {
+                    const int   kidx = dk == 1 ? kt + 1 : dk == 2 ? kt + 3 : kt + 2;
+                    const i32x4 &rs  = dk == 2 ? rsrc_b : rsrc_a;
+                    if constexpr (GG_M0_AHEAD)
+                        dma_m0(rs, ic<dj>{}, kidx, chk{});
+                    else
+                        dma(rs, d_stage, ic<dj>{}, kidx, chk{});
+                }
+            });
+        });
+    };
+
+    // ---- the persistent loop --------------------------------------------------------------
+    issue_prologue();
+    finish_prologue.template operator()<kLoads + kEarlyA>();
+    while (true) {
         step.template operator()<0, 0, true, true>(0);
         int kt = 1; // kt % 6 == 1 at the top of each block of six steps
         // Unchecked: every prefetch of the block (up to kt + 8) is a full step before T-1.
@@ -474,43 +590,31 @@ grouped_gemm_kernel(const KernelArgs args) {
             if (kt + 5 < T) step.template operator()<0, 0, false, true>(kt + 5);
         }
 
-        // ---- epilogue: accumulators -> 16-bit -> LDS (row major) -> 16-byte NT stores ----
-        wait_vm_lds_barrier<0>(); // trailing DMAs landed, every wave is done reading LDS
-        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" ::: "memory"); // MFMA -> VALU read distance
-        {
-            const int row = wm * 128 + (lane & 15);
-            const int col = wn * 128 + (lane >> 4) * 4;
-            const int off = row * kCStride + col * 2;
-            sfor<0, 8>([&](auto mi) {
-                sfor<0, 8>([&](auto ni) {
-                    *reinterpret_cast<u32x2 *>(smem + off + mi * 16 * kCStride + ni * 16 * 2) =
-                        pack4<F16>(acc[mi][ni]);
-                });
-            });
-        }
-        wait_vm_lds_barrier<63>();
-        {
-            // wave w streams rows w*64 .. +64, two 512-byte rows per instruction
-            const int row   = wave * 64 + (lane >> 5);
-            const int chunk = lane & 31;
-            const int loff  = row * kCStride + chunk * 16;
-            // rows past m_valid fall outside the resource; chunks past n_valid get an
-            // out-of-range offset. N % 8 == 0, so a chunk never straddles N.
-            const int goff = chunk * 8 < n_valid ? (row * N + chunk * 8) * 2
-                                                 : static_cast<int>(0x80000000u);
-            const __amdgpu_buffer_rsrc_t crs = __builtin_amdgcn_make_buffer_rsrc(
-                c_ptr, static_cast<short>(0), static_cast<int>(m_valid * N * 2), 0x00020000);
-            sfor<0, 2>([&](auto half) {
-                i32x4 d[16];
-                sfor<0, 16>([&](auto i) {
-                    d[i] = lds_read(loff + (half * 16 + i) * 2 * kCStride);
-                });
-                sfor<0, 16>([&](auto i) {
-                    __builtin_amdgcn_raw_buffer_store_b128(
-                        __builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, d[i]), crs,
-                        goff + (half * 16 + i) * 2 * N * 2, 0, /*nt*/ 2);
-                });
-            });
+        // The tile's K loop is done. Register epilogue: once every wave is done reading LDS,
+        // the next tile's prologue DMAs go out first and this tile's stores overlap their
+        // latency. LDS epilogue: C is staged through LDS first, then the next prologue.
+        t += gridDim.x;
+        const bool more = t < args.total_tiles;
+        if constexpr (GG_EPILOGUE_LDS) {
+            epilogue_lds(cur.c_ptr, cur.m_valid, cur.n_valid);
+            if (!more)
+                break;
+            cur = make_tile(t);
+            issue_prologue();
+            finish_prologue.template operator()<kLoads + kEarlyA>();
+        } else {
+            wait_vm_lds_barrier<63>();
+            uint16_t *const done_c = cur.c_ptr;
+            const int       done_m = cur.m_valid, done_n = cur.n_valid;
+            if (more) {
+                cur = make_tile(t);
+                issue_prologue();
+            }
+            epilogue(done_c, done_m, done_n);
+            if (!more)
+                break;
+            // in flight after B(1): B(2), the early A(1) DMAs and the stores
+            finish_prologue.template operator()<kLoads + kEarlyA + kStores>();
         }
     }
 }
