@@ -231,8 +231,10 @@ __device__ __forceinline__ i32x4 dma_rsrc(const void *p, uint32_t bytes) {
 // 64 lanes x 16 B from global (resource + lane offset + K-step offset) into LDS at
 // M0 + 16 * lane. The compiler cannot see this LDS write: waits are placed by hand.
 // set_m0 must precede the load by at least one instruction (SALU M0 write -> LDS DMA).
+// s_add_u32 writes SCC: the clobber keeps the compiler from holding a branch condition in SCC
+// across it.
 template <int OFF> __device__ __forceinline__ void set_m0(uint32_t lds_base) {
-    asm volatile("s_add_u32 m0, %0, %1" : : "s"(lds_base), "n"(OFF) : "memory");
+    asm volatile("s_add_u32 m0, %0, %1" : : "s"(lds_base), "n"(OFF) : "memory", "scc");
 }
 __device__ __forceinline__ void dma16_m0(int voff, const i32x4 &rsrc, int soff) {
     asm volatile("buffer_load_dwordx4 %0, %1, %2 offen " GG_DMA_CPOL " lds"
@@ -285,6 +287,35 @@ template <bool F16> __device__ __forceinline__ u32x2 pack4(const f32x4 &v) {
 // ---------------------------------------------------------------------------------------
 // The kernel
 // ---------------------------------------------------------------------------------------
+// Cross-tile pipeline (GG_CROSS_TILE): the DMAs of a tile's last three K steps already fetch
+// the first K steps of the workgroup's next tile, and the finished tile's accumulators are
+// stored from registers inside the next tile's first step, row block by row block, just before
+// the first MFMAs of that step overwrite them. No prologue bubble and no drained pipeline at a
+// tile boundary. Needs >= 4 K steps per tile; shorter K falls back to a prologue per tile.
+#ifndef GG_CROSS_TILE
+#define GG_CROSS_TILE 1
+#endif
+constexpr bool kCross = GG_CROSS_TILE;
+
+// Fused epilogue slots of a tile's first step: chunk j (output blocks 2j, 2j+1) of the previous
+// tile's row block mi+1 follows MFMA 2 + 4j of row mi (row block 0 is stored before the step).
+constexpr int plan_epi(int mi, int idx) {
+    return (mi < 7 && idx % 4 == 2) ? (idx - 2) / 4 : -1;
+}
+// vmcnt at the barrier of a fused first step: DMAs and stores issued after the last A(kt+1) DMA.
+constexpr int vm_at_barrier_fused() {
+    int last_a = -1;
+    for (int p = 0; p < 8 * 16; ++p)
+        if (plan_load_a(p / 16, p % 16) >= 0)
+            last_a = p;
+    int n = 0;
+    for (int p = last_a + 1; p < kBarRow * 16 + kBarIdx; ++p)
+        n += (plan_load_b(p / 16, p % 16) >= 0) + (plan_load_a_early(p / 16, p % 16) >= 0) +
+             (plan_epi(p / 16, p % 16) >= 0);
+    return n;
+}
+static_assert(vm_at_barrier_fused() <= 63, "vmcnt field");
+
 template <bool F16>
 __global__ void __launch_bounds__(kThreads, 1) __attribute__((amdgpu_waves_per_eu(1, 1)))
 grouped_gemm_kernel(const KernelArgs args) {
@@ -318,11 +349,49 @@ grouped_gemm_kernel(const KernelArgs args) {
         frag_a[kh]    = wm * 128 * kRowBytes + off;
         frag_b[kh]    = wn * 128 * kRowBytes + off;
     });
-    int base_b0[2], base_b1[2];
-    sfor<0, 2>([&](auto kh) {
-        base_b0[kh] = frag_b[kh] + b_stage(0);
-        base_b1[kh] = frag_b[kh] + b_stage(1);
-    });
+
+    // Register epilogue: lane (row l%16, q = l/16) stores 16 bytes at column ecol + 32 j of
+    // its row in output chunk j of a 16-row block (see store_chunk).
+    const int q    = lane >> 4;
+    const int ecol = wn * 128 + (q & 1) * 16 + (q >> 1) * 8;
+    int       voffc = ((wm * 128 + (lane & 15)) * N + ecol) * 2;
+    const int blk_stride = 16 * N * 2; // bytes between 16-row blocks of C
+
+    // Logical stage L of an operand (the K step's index mod 2 for A, mod 3 for B within the
+    // tile) lives in physical stage (L + rot) mod n. A tile that follows with prefetched data
+    // rotates by its predecessor's K-step count.
+    int      rot_a = 0, rot_b = 0;
+    const int t_mod3 = T % 3;
+    int      a_rd[2][2], b_rd[3][2]; // LDS read base per logical stage and k-half
+    uint32_t a_dst[2], b_dst[3];     // this wave's DMA destination per logical stage
+    auto set_stages = [&]() {
+        sfor<0, 2>([&](auto L) {
+            const int p = ((L + rot_a) & 1) * kOpBytes;
+            a_dst[L]    = lds0 + wave * 1024 + a_stage(0) + p;
+            sfor<0, 2>([&](auto h) { a_rd[L][h] = frag_a[h] + a_stage(0) + p; });
+        });
+        sfor<0, 3>([&](auto L) {
+            int s = L + rot_b;
+            s     = s >= 3 ? s - 3 : s;
+            const int p = b_stage(0) + s * kOpBytes;
+            b_dst[L]    = lds0 + wave * 1024 + p;
+            sfor<0, 2>([&](auto h) { b_rd[L][h] = frag_b[h] + p; });
+        });
+    };
+    // Re-materialise loop-invariant offsets at the top of every loop body (see fresh_v).
+    auto refresh = [&]() {
+        sfor<0, kLoads>([&](auto j) { fresh_v(voff[j]); });
+        fresh_v(ktail_bad);
+        fresh_v(voffc);
+        sfor<0, 2>([&](auto L) {
+            fresh_s(a_dst[L]);
+            sfor<0, 2>([&](auto h) { fresh_v(a_rd[L][h]); });
+        });
+        sfor<0, 3>([&](auto L) {
+            fresh_s(b_dst[L]);
+            sfor<0, 2>([&](auto h) { fresh_v(b_rd[L][h]); });
+        });
+    };
     auto lds_read = [&](int off) -> i32x4 { return *reinterpret_cast<const i32x4 *>(smem + off); };
 
     f32x4 acc[8][8];
@@ -353,94 +422,110 @@ grouped_gemm_kernel(const KernelArgs args) {
         tl.c_ptr  = static_cast<uint16_t *>(args.out) + row0 * N + col0;
         return tl;
     };
+    auto c_rsrc = [&](const Tile &tl) {
+        // rows past m_valid fall outside the resource
+        return __builtin_amdgcn_make_buffer_rsrc(tl.c_ptr, static_cast<short>(0),
+                                                 static_cast<int>(tl.m_valid * N * 2), 0x00020000);
+    };
     const i32x4 rsrc_0 = dma_rsrc(args.x, 0); // zero length: no traffic, the DMA writes zeros
 
     int t = blockIdx.x;
     if (t >= args.total_tiles)
         return;
-    Tile cur = make_tile(t);
-    const i32x4 &rsrc_a = cur.rsrc_a;
-    const i32x4 &rsrc_b = cur.rsrc_b;
+    Tile cur = make_tile(t), nxt = cur;
+    bool cross_next = false; // the DMAs past this tile's last K step fetch `nxt`
 
-    // DMA j of K step kidx into the stage at byte offset `stage`. CHECKED: kidx may be past
-    // the last step (zero-length resource) or be the last, partial step (masked chunks).
-    // Per-wave LDS destination base and per-lane offsets, re-materialised at the top of
-    // every loop body (see fresh_v).
-    uint32_t dma_base = lds0 + wave * 1024;
-    auto refresh = [&]() {
-        fresh_s(dma_base);
-        sfor<0, kLoads>([&](auto j) { fresh_v(voff[j]); });
-        fresh_v(ktail_bad);
-        sfor<0, 2>([&](auto h) {
-            fresh_v(frag_a[h]);
-            fresh_v(frag_b[h]);
-            fresh_v(base_b0[h]);
-            fresh_v(base_b1[h]);
-        });
-    };
-    // w fragment (stage S, column block ni, k-half h) as base + 16-bit immediate: B0 from
-    // its own base, B1 and B2 from a base at B1 (B2 = +32 KB).
-    auto read_b = [&]<int S>(int h, int ni) -> i32x4 {
-        if constexpr (!GG_STAGE_BASES)
-            return lds_read(frag_b[h] + b_stage(S) + ni * 16 * kRowBytes);
-        else if constexpr (S == 0)
-            return lds_read(base_b0[h] + ni * 16 * kRowBytes);
-        else
-            return lds_read(base_b1[h] + (S - 1) * kOpBytes + ni * 16 * kRowBytes);
-    };
-    // The DMA of a slot whose M0 was written before the slot's MFMA.
-    auto dma_m0 = [&](const i32x4 &rsrc, auto j, int kidx, auto checked) {
-        sched_fence();
-        if constexpr (decltype(checked)::value) {
-            const i32x4 rs   = kidx < T ? rsrc : rsrc_0;
-            const int   last = kidx == T - 1 ? -1 : 0; // uniform
-            dma16_m0(voff[j] | (ktail_bad & last), rs, kidx * kRowBytes);
-        } else {
-            dma16_m0(voff[j], rsrc, kidx * kRowBytes);
+    // Source of DMA j of K step kidx of operand B_OP (false: x, true: w). CHECKED: kidx may be
+    // past the tile's last step (next tile, or nothing) or its last, partial step.
+    auto dma_src = [&](auto b_op, auto j, int kidx, auto checked, i32x4 &rs, int &vo, int &so) {
+        constexpr bool B  = decltype(b_op)::value;
+        i32x4          rc = cur.rsrc_a, rn = nxt.rsrc_a;
+        if constexpr (B) {
+            rc = cur.rsrc_b;
+            rn = nxt.rsrc_b;
         }
-        sched_fence();
-    };
-    auto dma = [&](const i32x4 &rsrc, int stage, auto j, int kidx, auto checked) {
-        sched_fence();
-        const uint32_t dst = dma_base + stage + j * 4096;
         if constexpr (decltype(checked)::value) {
-            const i32x4 rs   = kidx < T ? rsrc : rsrc_0;
-            const int   last = kidx == T - 1 ? -1 : 0; // uniform
-            dma16(dst, voff[j] | (ktail_bad & last), rs, kidx * kRowBytes);
+            const bool in_cur = kidx < T;
+            const int  koff   = in_cur ? kidx : kidx - T;
+            rs                = in_cur ? rc : (cross_next ? rn : rsrc_0);
+            const int last    = koff == T - 1 ? -1 : 0; // uniform
+            vo                = voff[j] | (ktail_bad & last);
+            so                = koff * kRowBytes;
         } else {
-            dma16(dst, voff[j], rsrc, kidx * kRowBytes);
+            rs = rc;
+            vo = voff[j];
+            so = kidx * kRowBytes;
         }
+    };
+    // DMA with its own M0 write (prologue).
+    auto dma_now = [&](uint32_t dst, auto b_op, auto j, int kidx) {
+        sched_fence();
+        i32x4 rs;
+        int   vo, so;
+        dma_src(b_op, j, kidx, std::true_type{}, rs, vo, so);
+        dma16(dst + j * 4096, vo, rs, so);
         sched_fence();
     };
+    // DMA whose M0 was written before the slot's MFMA.
+    auto dma_go = [&](auto b_op, auto j, int kidx, auto checked) {
+        sched_fence();
+        i32x4 rs;
+        int   vo, so;
+        dma_src(b_op, j, kidx, checked, rs, vo, so);
+        dma16_m0(vo, rs, so);
+        sched_fence();
+    };
+    using A_OP = std::false_type;
+    using B_OP = std::true_type;
 
-    // ---- prologue: A(0), B(0..2) and the first DMAs of A(1) of tile `cur` -------------
+    // ---- prologue of a tile that starts cold: A(0), B(0..2), the first DMAs of A(1) ----------
     auto issue_prologue = [&]() {
         refresh();
-        sfor<0, kLoads>([&](auto j) { dma(rsrc_a, a_stage(0), j, 0, std::true_type{}); });
-        sfor<0, kLoads>([&](auto j) { dma(rsrc_b, b_stage(0), j, 0, std::true_type{}); });
-        sfor<0, kLoads>([&](auto j) { dma(rsrc_b, b_stage(1), j, 1, std::true_type{}); });
-        sfor<0, kLoads>([&](auto j) { dma(rsrc_b, b_stage(2), j, 2, std::true_type{}); });
-        sfor<0, kEarlyA>([&](auto j) { dma(rsrc_a, a_stage(1), j, 1, std::true_type{}); });
+        sfor<0, kLoads>([&](auto j) { dma_now(a_dst[0], A_OP{}, j, 0); });
+        sfor<0, kLoads>([&](auto j) { dma_now(b_dst[0], B_OP{}, j, 0); });
+        sfor<0, kLoads>([&](auto j) { dma_now(b_dst[1], B_OP{}, j, 1); });
+        sfor<0, kLoads>([&](auto j) { dma_now(b_dst[2], B_OP{}, j, 2); });
+        sfor<0, kEarlyA>([&](auto j) { dma_now(a_dst[1], A_OP{}, j, 1); });
     };
     // Then B(0) and A(0) row 0 into registers. VM: DMAs/stores issued after B(1)'s last.
     auto finish_prologue = [&]<int VM>() {
         wait_vm_lds_barrier<VM>(); // A(0), B(0), B(1) landed everywhere
         sfor<0, 8>([&](auto ni) {
-            sfor<0, 2>([&](auto kh) { fb[0][ni][kh] = read_b.template operator()<0>(kh, ni); });
+            sfor<0, 2>([&](auto kh) { fb[0][ni][kh] = lds_read(b_rd[0][kh] + ni * 16 * kRowBytes); });
         });
-        sfor<0, 2>([&](auto kh) { fa[0][kh] = lds_read(frag_a[kh] + a_stage(0)); });
+        sfor<0, 2>([&](auto kh) { fa[0][kh] = lds_read(a_rd[0][kh]); });
         wait_vm_lds_barrier<63>(); // every wave holds B(0): its stage may be refilled
     };
 
-    // ---- epilogue of a finished tile, straight from the accumulators ------------------
-    // Lane l holds C^T blocks: row l%16, columns 4q..4q+3 (q = l/16) of each 16 x 16 block.
-    // One v_permlane16_swap per dword between the blocks 2j and 2j+1 of a row block leaves
-    // every lane with 8 consecutive columns (16 B) of one row: rows q=0,2 get block 2j,
-    // q=1,3 block 2j+1, columns 0-7 (q<2) or 8-15. 4 stores of 1 KB per 16-row block.
-    // ---- epilogue through LDS: accumulators -> 16-bit -> LDS (row major, 528-byte row stride)
-    // -> every wave streams 64 whole rows with 16-byte NT stores, two 512-byte rows per store.
-    // Needs all of LDS, so the next tile's prologue goes out after it.
-    auto epilogue_lds = [&](uint16_t *c_ptr, int m_valid, int n_valid) {
+    // ---- register epilogue: one 1 KB store of 16 rows x 64 B ---------------------------------
+    // Lane l holds C^T blocks: row l%16, columns 4q..4q+3 of each 16 x 16 block. One
+    // v_permlane16_swap per dword between blocks 2j and 2j+1 leaves every lane with 8
+    // consecutive columns of one row: q = 0, 2 get block 2j, q = 1, 3 block 2j+1, columns 0-7
+    // (q < 2) or 8-15. Chunks past n_valid get an out-of-range offset (N % 8 == 0).
+    auto store_chunk = [&](auto r, auto j, const __amdgpu_buffer_rsrc_t &crs, int n_valid) {
+        sched_fence();
+        // reads of these accumulators may not move above this point
+        asm volatile("" : "+a"(acc[r][2 * j]), "+a"(acc[r][2 * j + 1]));
+        const u32x2 p0 = pack4<F16>(acc[r][2 * j]);
+        const u32x2 p1 = pack4<F16>(acc[r][2 * j + 1]);
+        const auto  s0 = __builtin_amdgcn_permlane16_swap(p0[0], p1[0], false, false);
+        const auto  s1 = __builtin_amdgcn_permlane16_swap(p0[1], p1[1], false, false);
+        typedef unsigned u32x4v __attribute__((ext_vector_type(4)));
+        const u32x4v d  = {s0[0], s1[0], s0[1], s1[1]};
+        const int    vo = ecol + 32 * j < n_valid ? voffc + r * blk_stride + j * 64
+                                                  : static_cast<int>(0x80000000u);
+        __builtin_amdgcn_raw_buffer_store_b128(d, crs, vo, 0, /*nt*/ 2);
+        sched_fence();
+    };
+    constexpr int kStores = 32; // per wave and tile
+    auto epilogue_reg = [&](const Tile &tl) {
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" ::: "memory"); // MFMA -> VALU read distance
+        const __amdgpu_buffer_rsrc_t crs = c_rsrc(tl);
+        sfor<0, 8>([&](auto r) { sfor<0, 4>([&](auto j) { store_chunk(r, j, crs, tl.n_valid); }); });
+    };
+    // ---- epilogue through LDS: accumulators -> 16-bit -> LDS (528-byte row stride) -> every wave
+    // streams 64 whole rows, two 512-byte rows per 16-byte-per-lane store. Needs all of LDS.
+    auto epilogue_lds = [&](const Tile &tl) {
         wait_vm_lds_barrier<0>(); // trailing DMAs landed, every wave is done reading LDS
         asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" ::: "memory"); // MFMA -> VALU read distance
         {
@@ -461,11 +546,8 @@ grouped_gemm_kernel(const KernelArgs args) {
         fresh_v(row);
         const int chunk = lane & 31;
         const int loff  = row * kCStride + chunk * 16;
-        // rows past m_valid fall outside the resource; chunks past n_valid get an
-        // out-of-range offset. N % 8 == 0, so a chunk never straddles N.
-        const int goff = chunk * 8 < n_valid ? (row * N + chunk * 8) * 2 : static_cast<int>(0x80000000u);
-        const __amdgpu_buffer_rsrc_t crs = __builtin_amdgcn_make_buffer_rsrc(
-            c_ptr, static_cast<short>(0), static_cast<int>(m_valid * N * 2), 0x00020000);
+        const int goff  = chunk * 8 < tl.n_valid ? (row * N + chunk * 8) * 2 : static_cast<int>(0x80000000u);
+        const __amdgpu_buffer_rsrc_t crs = c_rsrc(tl);
         sfor<0, 2>([&](auto half) {
             i32x4 d[16];
             sfor<0, 16>([&](auto i) { d[i] = lds_read(loff + (half * 16 + i) * 2 * kCStride); });
@@ -478,41 +560,16 @@ grouped_gemm_kernel(const KernelArgs args) {
         wait_vm_lds_barrier<63>(); // every wave is done reading the staged C
     };
 
-    constexpr int kStores = 32; // per wave and tile
-    auto epilogue = [&](uint16_t *c_ptr, int m_valid, int n_valid) {
-        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" ::: "memory"); // MFMA -> VALU read distance
-        const int q   = lane >> 4;
-        const int row = wm * 128 + (lane & 15);
-        int       col = wn * 128 + (q & 1) * 16 + (q >> 1) * 8;
-        fresh_v(col); // computed here, not hoisted out of the tile loop
-        const int voffc = (row * N + col) * 2;
-        // rows past m_valid fall outside the resource; chunks past n_valid get an
-        // out-of-range offset (N % 8 == 0: a chunk never straddles N)
-        const __amdgpu_buffer_rsrc_t crs = __builtin_amdgcn_make_buffer_rsrc(
-            c_ptr, static_cast<short>(0), static_cast<int>(m_valid * N * 2), 0x00020000);
-        sfor<0, 8>([&](auto mi) {
-            int vrow = voffc + mi * 16 * N * 2;
-            fresh_v(vrow);
-            sfor<0, 4>([&](auto j) {
-                sched_fence();
-                // Reads of these accumulators may not move above this point (and so not above
-                // the MFMA -> VALU wait states at the top of the epilogue).
-                asm volatile("" : "+a"(acc[mi][2 * j]), "+a"(acc[mi][2 * j + 1]));
-                const u32x2 p0 = pack4<F16>(acc[mi][2 * j]);
-                const u32x2 p1 = pack4<F16>(acc[mi][2 * j + 1]);
-                const auto  s0 = __builtin_amdgcn_permlane16_swap(p0[0], p1[0], false, false);
-                const auto  s1 = __builtin_amdgcn_permlane16_swap(p0[1], p1[1], false, false);
-                typedef unsigned u32x4v __attribute__((ext_vector_type(4)));
-                const u32x4v d  = {s0[0], s1[0], s0[1], s1[1]};
-                const int    vo = col + 32 * j < n_valid ? vrow + j * 64 : static_cast<int>(0x80000000u);
-                __builtin_amdgcn_raw_buffer_store_b128(d, crs, vo, 0, /*nt*/ 2);
-            });
-        });
-    };
-
-    // ---- one K step -----------------------------------------------------------------
-    // SA = kt % 2 (A stage, w register set), SB = kt % 3 (B stage).
-    auto step = [&]<int SA, int SB, bool FIRST, bool CHECKED>(int kt) {
+    // ---- one K step ---------------------------------------------------------------------------
+    // SA = kt % 2 (A logical stage, w register set), SB = kt % 3 (B logical stage).
+    // FUSE: first step of a tile whose predecessor's accumulators are still to be stored
+    // (row blocks 1-7 here; block 0 before the step), to prev_crs / prev_n.
+    // Nothing to store before the first tile: zero-length resource, the stores are dropped.
+    const __amdgpu_buffer_rsrc_t null_crs =
+        __builtin_amdgcn_make_buffer_rsrc(cur.c_ptr, static_cast<short>(0), 0, 0x00020000);
+    __amdgpu_buffer_rsrc_t prev_crs = null_crs;
+    int                    prev_n   = 0;
+    auto step = [&]<int SA, int SB, bool FIRST, bool CHECKED, bool FUSE>(int kt) {
         constexpr int NX = SA ^ 1;
         constexpr int SB_NEXT = (SB + 1) % 3;
         using chk = std::integral_constant<bool, CHECKED>;
@@ -522,100 +579,118 @@ grouped_gemm_kernel(const KernelArgs args) {
                 constexpr int idx = decltype(idx_)::value;
                 constexpr int kh = idx / 8, ni = idx % 8;
                 constexpr int dk = plan_dma_kind(mi, idx), dj = plan_dma_j(mi, idx);
-                constexpr int d_stage = dk == 1 ? a_stage(NX) : dk == 2 ? b_stage(SB) : a_stage(SA);
-                if constexpr (dk != 0 && GG_M0_AHEAD) {
-                    set_m0<d_stage + dj * 4096>(dma_base); // the MFMA below is the wait state
-                    sched_fence();
-                }
+                if constexpr (dk == 1)
+                    set_m0<dj * 4096>(a_dst[NX]); // the MFMA below is the wait state
+                else if constexpr (dk == 2)
+                    set_m0<dj * 4096>(b_dst[SB]);
+                else if constexpr (dk == 3)
+                    set_m0<dj * 4096>(a_dst[SA]);
+                sched_fence();
                 if constexpr (FIRST && kh == 0)
                     mfma_first<F16>(acc[mi][ni], fb[SA][ni][0], fa[mi & 1][0]);
                 else
                     mfma<F16>(acc[mi][ni], fb[SA][ni][kh], fa[mi & 1][kh]);
                 sched_fence();
                 if constexpr (mi == kBarRow && idx == kBarIdx) {
-                    wait_vm_lds_barrier<vm_at_barrier()>();
+                    wait_vm_lds_barrier<FUSE ? vm_at_barrier_fused() : vm_at_barrier()>();
                     sched_fence();
                 }
                 if constexpr (plan_read_a_next(mi, idx) >= 0) {
                     constexpr int h = plan_read_a_next(mi, idx);
-                    fa[(mi + 1) & 1][h] =
-                        lds_read(frag_a[h] + a_stage(SA) + (mi + 1) * 16 * kRowBytes);
+                    fa[(mi + 1) & 1][h] = lds_read(a_rd[SA][h] + (mi + 1) * 16 * kRowBytes);
                     sched_fence();
                 }
                 if constexpr (plan_read_b_next(mi, idx) >= 0) {
                     constexpr int h = plan_read_b_next(mi, idx);
-                    fb[NX][mi][h] = read_b.template operator()<SB_NEXT>(h, mi);
+                    fb[NX][mi][h] = lds_read(b_rd[SB_NEXT][h] + mi * 16 * kRowBytes);
                     sched_fence();
                 }
                 if constexpr (plan_read_a_row0(mi, idx) >= 0) {
                     constexpr int h = plan_read_a_row0(mi, idx);
-                    fa[0][h] = lds_read(frag_a[h] + a_stage(NX));
+                    fa[0][h] = lds_read(a_rd[NX][h]);
                     sched_fence();
                 }
+                if constexpr (FUSE && plan_epi(mi, idx) >= 0)
+                    store_chunk(ic<mi + 1>{}, ic<plan_epi(mi, idx)>{}, prev_crs, prev_n);
                 if constexpr (dk != 0) {
-                    const int   kidx = dk == 1 ? kt + 1 : dk == 2 ? kt + 3 : kt + 2;
-                    const i32x4 &rs  = dk == 2 ? rsrc_b : rsrc_a;
-                    if constexpr (GG_M0_AHEAD)
-                        dma_m0(rs, ic<dj>{}, kidx, chk{});
+                    const int kidx = dk == 1 ? kt + 1 : dk == 2 ? kt + 3 : kt + 2;
+                    if constexpr (dk == 2)
+                        dma_go(B_OP{}, ic<dj>{}, kidx, chk{});
                     else
-                        dma(rs, d_stage, ic<dj>{}, kidx, chk{});
+                        dma_go(A_OP{}, ic<dj>{}, kidx, chk{});
                 }
             });
         });
     };
 
-    // ---- the persistent loop --------------------------------------------------------------
+    // ---- the persistent loop ------------------------------------------------------------------
+    set_stages();
     issue_prologue();
     finish_prologue.template operator()<kLoads + kEarlyA>();
     while (true) {
-        step.template operator()<0, 0, true, true>(0);
+        refresh();
+        cross_next = false;
+        // First step: stores the previous tile's accumulators (to nowhere if there is none)
+        // while it overwrites them. Always the same code, so the accumulators never merge
+        // across branches and stay in AGPRs.
+        sfor<0, 4>([&](auto j) { store_chunk(ic<0>{}, j, prev_crs, prev_n); });
+        step.template operator()<0, 0, true, true, true>(0);
         int kt = 1; // kt % 6 == 1 at the top of each block of six steps
         // Unchecked: every prefetch of the block (up to kt + 8) is a full step before T-1.
         for (; kt + 9 < T; kt += 6) {
             refresh();
-            step.template operator()<1, 1, false, false>(kt);
-            step.template operator()<0, 2, false, false>(kt + 1);
-            step.template operator()<1, 0, false, false>(kt + 2);
-            step.template operator()<0, 1, false, false>(kt + 3);
-            step.template operator()<1, 2, false, false>(kt + 4);
-            step.template operator()<0, 0, false, false>(kt + 5);
+            step.template operator()<1, 1, false, false, false>(kt);
+            step.template operator()<0, 2, false, false, false>(kt + 1);
+            step.template operator()<1, 0, false, false, false>(kt + 2);
+            step.template operator()<0, 1, false, false, false>(kt + 3);
+            step.template operator()<1, 2, false, false, false>(kt + 4);
+            step.template operator()<0, 0, false, false, false>(kt + 5);
         }
-        for (; kt < T; kt += 6) { // at most 9 steps left
+        const int  t_next = t + gridDim.x;
+        const bool more   = t_next < args.total_tiles;
+        cross_next        = kCross && more && T >= 4;
+        if (cross_next)
+            nxt = make_tile(t_next);
+        for (; kt < T; kt += 6) { // at most 9 steps left; the last three prefetch `nxt`
             refresh();
-            step.template operator()<1, 1, false, true>(kt);
-            if (kt + 1 < T) step.template operator()<0, 2, false, true>(kt + 1);
-            if (kt + 2 < T) step.template operator()<1, 0, false, true>(kt + 2);
-            if (kt + 3 < T) step.template operator()<0, 1, false, true>(kt + 3);
-            if (kt + 4 < T) step.template operator()<1, 2, false, true>(kt + 4);
-            if (kt + 5 < T) step.template operator()<0, 0, false, true>(kt + 5);
+            step.template operator()<1, 1, false, true, false>(kt);
+            if (kt + 1 < T) step.template operator()<0, 2, false, true, false>(kt + 1);
+            if (kt + 2 < T) step.template operator()<1, 0, false, true, false>(kt + 2);
+            if (kt + 3 < T) step.template operator()<0, 1, false, true, false>(kt + 3);
+            if (kt + 4 < T) step.template operator()<1, 2, false, true, false>(kt + 4);
+            if (kt + 5 < T) step.template operator()<0, 0, false, true, false>(kt + 5);
         }
-
-        // The tile's K loop is done. Register epilogue: once every wave is done reading LDS,
-        // the next tile's prologue DMAs go out first and this tile's stores overlap their
-        // latency. LDS epilogue: C is staged through LDS first, then the next prologue.
-        t += gridDim.x;
-        const bool more = t < args.total_tiles;
-        if constexpr (GG_EPILOGUE_LDS) {
-            epilogue_lds(cur.c_ptr, cur.m_valid, cur.n_valid);
-            if (!more)
-                break;
-            cur = make_tile(t);
-            issue_prologue();
-            finish_prologue.template operator()<kLoads + kEarlyA>();
-        } else {
-            wait_vm_lds_barrier<63>();
-            uint16_t *const done_c = cur.c_ptr;
-            const int       done_m = cur.m_valid, done_n = cur.n_valid;
-            if (more) {
-                cur = make_tile(t);
-                issue_prologue();
-            }
-            epilogue(done_c, done_m, done_n);
-            if (!more)
-                break;
-            // in flight after B(1): B(2), the early A(1) DMAs and the stores
-            finish_prologue.template operator()<kLoads + kEarlyA + kStores>();
+        if (cross_next) {
+            // The next tile's first steps are in flight or in LDS, B(0) of it is in the w
+            // register set T % 2 and row 0 of A(0) in fa[0]: continue without a prologue.
+            prev_crs = c_rsrc(cur);
+            prev_n   = cur.n_valid;
+            cur      = nxt;
+            t        = t_next;
+            rot_a    = (rot_a + T) & 1;
+            rot_b    = rot_b + t_mod3;
+            rot_b    = rot_b >= 3 ? rot_b - 3 : rot_b;
+            set_stages();
+            if (T & 1) // the first step reads w set 0
+                sfor<0, 8>([&](auto ni) { sfor<0, 2>([&](auto h) { fb[0][ni][h] = fb[1][ni][h]; }); });
+            continue;
         }
+        // No prefetched successor: store this tile, then start the next one cold.
+        if constexpr (GG_EPILOGUE_LDS && !kCross)
+            epilogue_lds(cur);
+        else
+            epilogue_reg(cur);
+        if (!more)
+            break;
+        t     = t_next;
+        cur   = make_tile(t);
+        rot_a = 0;
+        rot_b = 0;
+        set_stages();
+        // (any stores were issued before these DMAs and complete first)
+        issue_prologue();
+        finish_prologue.template operator()<kLoads + kEarlyA>();
+        prev_crs = null_crs;
     }
 }
 

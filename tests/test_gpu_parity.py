@@ -220,3 +220,15 @@ def test_device_fill_matches_oracle_generator(pkg, oracle):
         # one 16-bit ulp is at most 2^-7 relative (bf16); tiny values may differ absolutely
         assert (np.abs(dv - hv) <= 2.0 ** -7 * np.abs(hv) + 1e-6).all()
         assert (dev_bits == host_bits).mean() > 0.99
+
+
+@pytest.mark.parametrize("steps", [4, 5, 6, 7, 8, 9, 10, 11, 13, 14, 16, 20, 31, 32, 33, 34, 35])
+def test_k_step_counts_with_several_tiles_per_workgroup(pkg, steps):
+    """Every K-step count mod 6 (the unrolled loop and its tail) and mod 2 / mod 3 (the LDS
+    stage rotation between consecutive tiles of a workgroup), with 2 to 3 tiles per workgroup,
+    every output against torch fp32."""
+    k = 64 * steps - (8 if steps % 4 == 1 else 0)  # some partial last steps too
+    gm, n = [4096, 256], 8192
+    print(f"[parity] K steps {steps}: K={k} group_m={gm} N={n}", flush=True)
+    r = Run(pkg, pkg.DType.BF16, gm, n, k).go()
+    r.check_torch_fp32()
