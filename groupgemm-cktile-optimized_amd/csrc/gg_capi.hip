@@ -161,7 +161,8 @@ int gg_prepare(int dtype, int group_num, int64_t n, int64_t k, const int64_t *gr
                        std::string(dtype == GG_DTYPE_BF16 ? "bf16" : "fp16") +
                        " grid=" + std::to_string(plan->grid) +
                        " tiles=" + std::to_string(plan->total_tiles) +
-                       " xcd=" + std::to_string(a.n_xcd);
+                       " xcd=" + std::to_string(a.n_xcd) +
+                       (gg::uses_cross_tile(a, plan->grid) ? " cross-tile" : " per-tile");
     } else {
         plan->detail = "mi355x: no launch (" +
                        std::string(has_output ? "K = 0, zero fill" : "empty output") + ")";

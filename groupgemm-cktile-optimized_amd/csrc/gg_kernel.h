@@ -26,6 +26,10 @@ struct KernelArgs {
     int               band;        // M-tiles per band of the in-group tile order
 };
 
+// Whether a launch takes the cross-tile pipeline variant (several tiles per workgroup, enough
+// K steps) rather than a prologue and an LDS-staged epilogue per tile.
+bool uses_cross_tile(const KernelArgs &args, int grid);
+
 // Enqueue the persistent grouped GEMM: `grid` workgroups of 256 threads on `stream`.
 // fp16 selects the f16 MFMA, otherwise bf16. Returns the launch status.
 hipError_t launch_grouped_gemm(const KernelArgs &args, bool fp16, int grid, hipStream_t stream);

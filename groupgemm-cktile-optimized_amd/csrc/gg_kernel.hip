@@ -50,6 +50,7 @@ namespace {
 
 typedef int      i32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef float    f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16   bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
@@ -103,9 +104,6 @@ constexpr int kLoads    = kOpBytes / 1024 / kWaves;         // 1 KB DMAs per wav
 #define GG_DMA_CPOL "sc0 sc1"
 #elif GG_DMA_CPOL_ID == 5
 #define GG_DMA_CPOL "sc1 nt"
-#endif
-#ifndef GG_EPILOGUE_LDS
-#define GG_EPILOGUE_LDS 1 // C through LDS in whole rows (1) or straight from registers (0)
 #endif
 constexpr int kEarlyA   = GG_EARLY_A;
 constexpr int kCStride  = kTileN * 2 + 16;                  // staged C row stride (528 B)
@@ -177,6 +175,9 @@ constexpr bool one_dma_per_slot() {
 static_assert(one_dma_per_slot(), "at most one DMA per MFMA gap");
 // DMAs that may still be in flight at the barrier: those issued after the last A(kt+1) DMA.
 // Loads complete in order, so vmcnt(this) means all of A(kt+1) (and everything older) landed.
+// Stores are never counted here, wherever they sit in the step: a store may complete before an
+// older load, so counting one could let the barrier pass while an A(kt+1) DMA is in flight.
+// With loads alone counted, pending stores only make the wait longer.
 constexpr int vm_at_barrier() {
     int last_a = -1;
     for (int p = 0; p < 8 * 16; ++p)
@@ -287,36 +288,30 @@ template <bool F16> __device__ __forceinline__ u32x2 pack4(const f32x4 &v) {
 // ---------------------------------------------------------------------------------------
 // The kernel
 // ---------------------------------------------------------------------------------------
-// Cross-tile pipeline (GG_CROSS_TILE): the DMAs of a tile's last three K steps already fetch
-// the first K steps of the workgroup's next tile, and the finished tile's accumulators are
-// stored from registers inside the next tile's first step, row block by row block, just before
-// the first MFMAs of that step overwrite them. No prologue bubble and no drained pipeline at a
-// tile boundary. Needs >= 4 K steps per tile; shorter K falls back to a prologue per tile.
+// Cross-tile pipeline (kernel variant CROSS, for workgroups with several tiles of
+// >= kCrossMinSteps K steps): the DMAs of a tile's last three K steps already fetch the first K
+// steps of the workgroup's next tile, so a tile boundary has no prologue bubble and no drained
+// pipeline. The finished tile's accumulators are stored from registers inside the next tile's
+// first step, row block by row block, just before its first MFMAs overwrite them.
 #ifndef GG_CROSS_TILE
 #define GG_CROSS_TILE 1
 #endif
-constexpr bool kCross = GG_CROSS_TILE;
+#ifndef GG_STORE_CPOL
+#define GG_STORE_CPOL 2 // cache policy of the register-direct C stores: bit 0 sc0, bit 1 nt, bit 4 sc1
+#endif
+constexpr bool kCrossAllowed  = GG_CROSS_TILE;
+constexpr int  kCrossMinSteps = 4; // the three prefetching steps follow the first
+constexpr int  kStoreCpol     = GG_STORE_CPOL;
 
-// Fused epilogue slots of a tile's first step: chunk j (output blocks 2j, 2j+1) of the previous
-// tile's row block mi+1 follows MFMA 2 + 4j of row mi (row block 0 is stored before the step).
+// First step of a cross tile: store s (0-3, see store_line) of the previous tile's row block
+// mi+1 is issued after MFMA 2 + 4s of row mi (row block 0 before the step).
 constexpr int plan_epi(int mi, int idx) {
     return (mi < 7 && idx % 4 == 2) ? (idx - 2) / 4 : -1;
 }
-// vmcnt at the barrier of a fused first step: DMAs and stores issued after the last A(kt+1) DMA.
-constexpr int vm_at_barrier_fused() {
-    int last_a = -1;
-    for (int p = 0; p < 8 * 16; ++p)
-        if (plan_load_a(p / 16, p % 16) >= 0)
-            last_a = p;
-    int n = 0;
-    for (int p = last_a + 1; p < kBarRow * 16 + kBarIdx; ++p)
-        n += (plan_load_b(p / 16, p % 16) >= 0) + (plan_load_a_early(p / 16, p % 16) >= 0) +
-             (plan_epi(p / 16, p % 16) >= 0);
-    return n;
-}
-static_assert(vm_at_barrier_fused() <= 63, "vmcnt field");
 
-template <bool F16>
+// CROSS: cross-tile pipeline (needs k_tiles >= kCrossMinSteps); otherwise every tile starts
+// with a prologue and ends with the LDS-staged epilogue.
+template <bool F16, bool CROSS>
 __global__ void __launch_bounds__(kThreads, 1) __attribute__((amdgpu_waves_per_eu(1, 1)))
 grouped_gemm_kernel(const KernelArgs args) {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kLdsBytes];
@@ -350,11 +345,11 @@ grouped_gemm_kernel(const KernelArgs args) {
         frag_b[kh]    = wn * 128 * kRowBytes + off;
     });
 
-    // Register epilogue: lane (row l%16, q = l/16) stores 16 bytes at column ecol + 32 j of
-    // its row in output chunk j of a 16-row block (see store_chunk).
+    // Register epilogue: in store s = 2h + half of a 16-row block, lane l writes 16 bytes of
+    // row 8 half + l%8 at column ecol + 64 h (see pack_pair).
     const int q    = lane >> 4;
-    const int ecol = wn * 128 + (q & 1) * 16 + (q >> 1) * 8;
-    int       voffc = ((wm * 128 + (lane & 15)) * N + ecol) * 2;
+    const int ecol = wn * 128 + ((lane >> 3) & 1) * 32 + (q & 1) * 16 + (q >> 1) * 8;
+    int       voffc = ((wm * 128 + (lane & 7)) * N + ecol) * 2;
     const int blk_stride = 16 * N * 2; // bytes between 16-row blocks of C
 
     // Logical stage L of an operand (the K step's index mod 2 for A, mod 3 for B within the
@@ -435,44 +430,49 @@ grouped_gemm_kernel(const KernelArgs args) {
     Tile cur = make_tile(t), nxt = cur;
     bool cross_next = false; // the DMAs past this tile's last K step fetch `nxt`
 
-    // Source of DMA j of K step kidx of operand B_OP (false: x, true: w). CHECKED: kidx may be
-    // past the tile's last step (next tile, or nothing) or its last, partial step.
-    auto dma_src = [&](auto b_op, auto j, int kidx, auto checked, i32x4 &rs, int &vo, int &so) {
+    // Where the DMAs of K step kidx of an operand (false: x, true: w) read from: resource,
+    // K offset and the per-lane mask of a partial last step. Unchecked: kidx is a full step of
+    // the current tile. Checked: kidx may be the tile's partial last step or lie past it (the
+    // next tile's first steps, or nothing). Evaluated once per step and operand stream.
+    struct DmaSrc {
+        i32x4 rs;
+        int   so, mask;
+    };
+    auto dma_src = [&](auto b_op, int kidx, auto checked) -> DmaSrc {
         constexpr bool B  = decltype(b_op)::value;
         i32x4          rc = cur.rsrc_a, rn = nxt.rsrc_a;
         if constexpr (B) {
             rc = cur.rsrc_b;
             rn = nxt.rsrc_b;
         }
+        DmaSrc d;
         if constexpr (decltype(checked)::value) {
             const bool in_cur = kidx < T;
             const int  koff   = in_cur ? kidx : kidx - T;
-            rs                = in_cur ? rc : (cross_next ? rn : rsrc_0);
-            const int last    = koff == T - 1 ? -1 : 0; // uniform
-            vo                = voff[j] | (ktail_bad & last);
-            so                = koff * kRowBytes;
+            d.rs              = in_cur ? rc : (cross_next ? rn : rsrc_0);
+            d.so              = koff * kRowBytes;
+            d.mask            = koff == T - 1 ? ktail_bad : 0;
         } else {
-            rs = rc;
-            vo = voff[j];
-            so = kidx * kRowBytes;
+            d.rs   = rc;
+            d.so   = kidx * kRowBytes;
+            d.mask = 0;
         }
+        return d;
     };
     // DMA with its own M0 write (prologue).
     auto dma_now = [&](uint32_t dst, auto b_op, auto j, int kidx) {
         sched_fence();
-        i32x4 rs;
-        int   vo, so;
-        dma_src(b_op, j, kidx, std::true_type{}, rs, vo, so);
-        dma16(dst + j * 4096, vo, rs, so);
+        const DmaSrc d = dma_src(b_op, kidx, std::true_type{});
+        dma16(dst + j * 4096, voff[j] | d.mask, d.rs, d.so);
         sched_fence();
     };
     // DMA whose M0 was written before the slot's MFMA.
-    auto dma_go = [&](auto b_op, auto j, int kidx, auto checked) {
+    auto dma_go = [&](const DmaSrc &d, auto j, auto checked) {
         sched_fence();
-        i32x4 rs;
-        int   vo, so;
-        dma_src(b_op, j, kidx, checked, rs, vo, so);
-        dma16_m0(vo, rs, so);
+        if constexpr (decltype(checked)::value)
+            dma16_m0(voff[j] | d.mask, d.rs, d.so);
+        else
+            dma16_m0(voff[j], d.rs, d.so);
         sched_fence();
     };
     using A_OP = std::false_type;
@@ -497,31 +497,42 @@ grouped_gemm_kernel(const KernelArgs args) {
         wait_vm_lds_barrier<63>(); // every wave holds B(0): its stage may be refilled
     };
 
-    // ---- register epilogue: one 1 KB store of 16 rows x 64 B ---------------------------------
-    // Lane l holds C^T blocks: row l%16, columns 4q..4q+3 of each 16 x 16 block. One
-    // v_permlane16_swap per dword between blocks 2j and 2j+1 leaves every lane with 8
-    // consecutive columns of one row: q = 0, 2 get block 2j, q = 1, 3 block 2j+1, columns 0-7
-    // (q < 2) or 8-15. Chunks past n_valid get an out-of-range offset (N % 8 == 0).
-    auto store_chunk = [&](auto r, auto j, const __amdgpu_buffer_rsrc_t &crs, int n_valid) {
-        sched_fence();
+    // ---- register epilogue: 1 KB stores of 8 rows x 128 B (whole cache lines) ----------------
+    // Lane l holds C^T blocks: row l%16, columns 4q..4q+3 of each 16 x 16 block (q = l/16).
+    // One v_permlane16_swap per dword between blocks 2j and 2j+1 gives chunk X_j: every lane
+    // holds 8 consecutive columns of its row, q = 0, 2 from block 2j, q = 1, 3 from block 2j+1,
+    // columns 0-7 (q < 2) or 8-15; 4 lanes cover 64 bytes of a row. Two DPP row shifts then
+    // pair X_2h with X_2h+1 so that a store covers whole 128-byte rows:
+    //   Z_A: lanes l%16 < 8 keep X_2h (row l%16), lanes l%16 >= 8 take X_2h+1 of lane l-8;
+    //   Z_B: lanes l%16 >= 8 keep X_2h+1 (row l%16), lanes l%16 < 8 take X_2h of lane l+8.
+    // Z_A holds rows 0-7 and Z_B rows 8-15 of the block, columns 64h..64h+63.
+    auto pack_chunk = [&](auto r, auto j) -> u32x4 {
         // reads of these accumulators may not move above this point
         asm volatile("" : "+a"(acc[r][2 * j]), "+a"(acc[r][2 * j + 1]));
         const u32x2 p0 = pack4<F16>(acc[r][2 * j]);
         const u32x2 p1 = pack4<F16>(acc[r][2 * j + 1]);
         const auto  s0 = __builtin_amdgcn_permlane16_swap(p0[0], p1[0], false, false);
         const auto  s1 = __builtin_amdgcn_permlane16_swap(p0[1], p1[1], false, false);
-        typedef unsigned u32x4v __attribute__((ext_vector_type(4)));
-        const u32x4v d  = {s0[0], s1[0], s0[1], s1[1]};
-        const int    vo = ecol + 32 * j < n_valid ? voffc + r * blk_stride + j * 64
-                                                  : static_cast<int>(0x80000000u);
-        __builtin_amdgcn_raw_buffer_store_b128(d, crs, vo, 0, /*nt*/ 2);
-        sched_fence();
+        return u32x4{s0[0], s1[0], s0[1], s1[1]};
     };
-    constexpr int kStores = 32; // per wave and tile
-    auto epilogue_reg = [&](const Tile &tl) {
-        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" ::: "memory"); // MFMA -> VALU read distance
-        const __amdgpu_buffer_rsrc_t crs = c_rsrc(tl);
-        sfor<0, 8>([&](auto r) { sfor<0, 4>([&](auto j) { store_chunk(r, j, crs, tl.n_valid); }); });
+    auto pack_pair = [&](auto r, auto h, u32x4 &za, u32x4 &zb) {
+        const u32x4 x0 = pack_chunk(r, ic<2 * h>{});
+        const u32x4 x1 = pack_chunk(r, ic<2 * h + 1>{});
+        sfor<0, 4>([&](auto i) {
+            // row_shr:8 into banks 2-3, row_shl:8 into banks 0-1
+            za[int(i)] = __builtin_amdgcn_update_dpp(x0[int(i)], x1[int(i)], 0x118, 0xf, 0xc, false);
+            zb[int(i)] = __builtin_amdgcn_update_dpp(x1[int(i)], x0[int(i)], 0x108, 0xf, 0x3, false);
+        });
+    };
+    // Store s = 2h + half of row block r. Chunks past n_valid get an out-of-range offset
+    // (N % 8 == 0, so a 16-byte chunk is either all valid or all past N).
+    auto store_line = [&](const u32x4 &d, int r, int s_, const __amdgpu_buffer_rsrc_t &crs,
+                          int n_valid) {
+        const int h  = s_ >> 1, half = s_ & 1;
+        const int vo = ecol + 64 * h < n_valid
+                           ? voffc + r * blk_stride + half * (blk_stride >> 1) + h * 128
+                           : static_cast<int>(0x80000000u);
+        __builtin_amdgcn_raw_buffer_store_b128(d, crs, vo, 0, kStoreCpol);
     };
     // ---- epilogue through LDS: accumulators -> 16-bit -> LDS (528-byte row stride) -> every wave
     // streams 64 whole rows, two 512-byte rows per 16-byte-per-lane store. Needs all of LDS.
@@ -562,17 +573,29 @@ grouped_gemm_kernel(const KernelArgs args) {
 
     // ---- one K step ---------------------------------------------------------------------------
     // SA = kt % 2 (A logical stage, w register set), SB = kt % 3 (B logical stage).
-    // FUSE: first step of a tile whose predecessor's accumulators are still to be stored
-    // (row blocks 1-7 here; block 0 before the step), to prev_crs / prev_n.
-    // Nothing to store before the first tile: zero-length resource, the stores are dropped.
+    // FUSE: first step of a tile whose predecessor's accumulators are still to be stored (row
+    // blocks 1-7 here; block 0 before the step), to prev_crs / prev_n. Nothing to store before
+    // the first tile: zero-length resource, the stores are dropped.
     const __amdgpu_buffer_rsrc_t null_crs =
         __builtin_amdgcn_make_buffer_rsrc(cur.c_ptr, static_cast<short>(0), 0, 0x00020000);
     __amdgpu_buffer_rsrc_t prev_crs = null_crs;
     int                    prev_n   = 0;
+    u32x4                  pair[2];
+    // Store s (0-3) of the previous tile's row block r: packed with the next one for even s.
+    auto epi_store = [&](auto r, auto s_) {
+        sched_fence();
+        if constexpr (s_ % 2 == 0)
+            pack_pair(r, ic<s_ / 2>{}, pair[0], pair[1]);
+        store_line(pair[s_ % 2], r, s_, prev_crs, prev_n);
+        sched_fence();
+    };
     auto step = [&]<int SA, int SB, bool FIRST, bool CHECKED, bool FUSE>(int kt) {
         constexpr int NX = SA ^ 1;
         constexpr int SB_NEXT = (SB + 1) % 3;
         using chk = std::integral_constant<bool, CHECKED>;
+        const DmaSrc src_a1 = dma_src(A_OP{}, kt + 1, chk{}); // A(kt+1)
+        const DmaSrc src_b3 = dma_src(B_OP{}, kt + 3, chk{}); // B(kt+3)
+        const DmaSrc src_a2 = dma_src(A_OP{}, kt + 2, chk{}); // A(kt+2)
         sfor<0, 8>([&](auto mi_) {
             constexpr int mi = decltype(mi_)::value;
             sfor<0, 16>([&](auto idx_) {
@@ -592,7 +615,7 @@ grouped_gemm_kernel(const KernelArgs args) {
                     mfma<F16>(acc[mi][ni], fb[SA][ni][kh], fa[mi & 1][kh]);
                 sched_fence();
                 if constexpr (mi == kBarRow && idx == kBarIdx) {
-                    wait_vm_lds_barrier<FUSE ? vm_at_barrier_fused() : vm_at_barrier()>();
+                    wait_vm_lds_barrier<vm_at_barrier()>();
                     sched_fence();
                 }
                 if constexpr (plan_read_a_next(mi, idx) >= 0) {
@@ -611,14 +634,13 @@ grouped_gemm_kernel(const KernelArgs args) {
                     sched_fence();
                 }
                 if constexpr (FUSE && plan_epi(mi, idx) >= 0)
-                    store_chunk(ic<mi + 1>{}, ic<plan_epi(mi, idx)>{}, prev_crs, prev_n);
-                if constexpr (dk != 0) {
-                    const int kidx = dk == 1 ? kt + 1 : dk == 2 ? kt + 3 : kt + 2;
-                    if constexpr (dk == 2)
-                        dma_go(B_OP{}, ic<dj>{}, kidx, chk{});
-                    else
-                        dma_go(A_OP{}, ic<dj>{}, kidx, chk{});
-                }
+                    epi_store(ic<mi + 1>{}, ic<plan_epi(mi, idx)>{});
+                if constexpr (dk == 1)
+                    dma_go(src_a1, ic<dj>{}, chk{});
+                else if constexpr (dk == 2)
+                    dma_go(src_b3, ic<dj>{}, chk{});
+                else if constexpr (dk == 3)
+                    dma_go(src_a2, ic<dj>{}, chk{});
             });
         });
     };
@@ -629,12 +651,15 @@ grouped_gemm_kernel(const KernelArgs args) {
     finish_prologue.template operator()<kLoads + kEarlyA>();
     while (true) {
         refresh();
-        cross_next = false;
-        // First step: stores the previous tile's accumulators (to nowhere if there is none)
-        // while it overwrites them. Always the same code, so the accumulators never merge
-        // across branches and stay in AGPRs.
-        sfor<0, 4>([&](auto j) { store_chunk(ic<0>{}, j, prev_crs, prev_n); });
-        step.template operator()<0, 0, true, true, true>(0);
+        if constexpr (CROSS) {
+            // First step: stores the previous tile's accumulators while it overwrites them (to
+            // nowhere for the first tile). Always the same code, so the accumulators never
+            // merge across branches and stay in AGPRs.
+            sfor<0, 4>([&](auto s_) { epi_store(ic<0>{}, s_); });
+            step.template operator()<0, 0, true, true, true>(0);
+        } else {
+            step.template operator()<0, 0, true, true, false>(0);
+        }
         int kt = 1; // kt % 6 == 1 at the top of each block of six steps
         // Unchecked: every prefetch of the block (up to kt + 8) is a full step before T-1.
         for (; kt + 9 < T; kt += 6) {
@@ -648,10 +673,10 @@ grouped_gemm_kernel(const KernelArgs args) {
         }
         const int  t_next = t + gridDim.x;
         const bool more   = t_next < args.total_tiles;
-        cross_next        = kCross && more && T >= 4;
+        cross_next        = CROSS && more;
         if (cross_next)
             nxt = make_tile(t_next);
-        for (; kt < T; kt += 6) { // at most 9 steps left; the last three prefetch `nxt`
+        for (; kt < T; kt += 6) { // at most 9 steps left; with CROSS the last three prefetch `nxt`
             refresh();
             step.template operator()<1, 1, false, true, false>(kt);
             if (kt + 1 < T) step.template operator()<0, 2, false, true, false>(kt + 1);
@@ -660,38 +685,40 @@ grouped_gemm_kernel(const KernelArgs args) {
             if (kt + 4 < T) step.template operator()<1, 2, false, true, false>(kt + 4);
             if (kt + 5 < T) step.template operator()<0, 0, false, true, false>(kt + 5);
         }
-        if (cross_next) {
-            // The next tile's first steps are in flight or in LDS, B(0) of it is in the w
-            // register set T % 2 and row 0 of A(0) in fa[0]: continue without a prologue.
-            prev_crs = c_rsrc(cur);
-            prev_n   = cur.n_valid;
-            cur      = nxt;
-            t        = t_next;
-            rot_a    = (rot_a + T) & 1;
-            rot_b    = rot_b + t_mod3;
-            rot_b    = rot_b >= 3 ? rot_b - 3 : rot_b;
-            set_stages();
-            if (T & 1) // the first step reads w set 0
-                sfor<0, 8>([&](auto ni) { sfor<0, 2>([&](auto h) { fb[0][ni][h] = fb[1][ni][h]; }); });
-            continue;
+        if constexpr (CROSS) {
+            if (!cross_next)
+                break; // last tile of the workgroup: stored after the loop
+            {
+                // The next tile's first steps are in flight or in LDS, B(0) of it is in the w
+                // register set T % 2 and row 0 of A(0) in fa[0]: continue without a prologue.
+                prev_crs = c_rsrc(cur);
+                prev_n   = cur.n_valid;
+                cur      = nxt;
+                t        = t_next;
+                rot_a    = (rot_a + T) & 1;
+                rot_b    = rot_b + t_mod3;
+                rot_b    = rot_b >= 3 ? rot_b - 3 : rot_b;
+                set_stages();
+                if (T & 1) // the first step reads w set 0
+                    sfor<0, 8>([&](auto ni) { sfor<0, 2>([&](auto h) { fb[0][ni][h] = fb[1][ni][h]; }); });
+                continue;
+            }
         }
-        // No prefetched successor: store this tile, then start the next one cold.
-        if constexpr (GG_EPILOGUE_LDS && !kCross)
+        if constexpr (!CROSS) {
+            // Store this tile through LDS, then start the next one cold.
             epilogue_lds(cur);
-        else
-            epilogue_reg(cur);
-        if (!more)
-            break;
-        t     = t_next;
-        cur   = make_tile(t);
-        rot_a = 0;
-        rot_b = 0;
-        set_stages();
-        // (any stores were issued before these DMAs and complete first)
-        issue_prologue();
-        finish_prologue.template operator()<kLoads + kEarlyA>();
-        prev_crs = null_crs;
+            if (!more)
+                return;
+            t   = t_next;
+            cur = make_tile(t);
+            set_stages();
+            // (the stores were issued before these DMAs and complete first)
+            issue_prologue();
+            finish_prologue.template operator()<kLoads + kEarlyA>();
+        }
     }
+    if constexpr (CROSS)
+        epilogue_lds(cur);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -720,11 +747,22 @@ template <bool F16> __global__ void fill_randn_kernel(uint16_t *p, size_t n, uin
 
 } // namespace
 
+bool uses_cross_tile(const KernelArgs &args, int grid) {
+    // Workgroups with a single tile gain nothing from the cross-tile pipeline.
+    return kCrossAllowed && args.k_tiles >= kCrossMinSteps && args.total_tiles > grid;
+}
+
 hipError_t launch_grouped_gemm(const KernelArgs &args, bool fp16, int grid, hipStream_t stream) {
-    if (fp16)
-        hipLaunchKernelGGL(grouped_gemm_kernel<true>, dim3(grid), dim3(kThreads), 0, stream, args);
+    const bool cross = uses_cross_tile(args, grid);
+    const dim3 g(grid), b(kThreads);
+    if (fp16 && cross)
+        hipLaunchKernelGGL((grouped_gemm_kernel<true, true>), g, b, 0, stream, args);
+    else if (fp16)
+        hipLaunchKernelGGL((grouped_gemm_kernel<true, false>), g, b, 0, stream, args);
+    else if (cross)
+        hipLaunchKernelGGL((grouped_gemm_kernel<false, true>), g, b, 0, stream, args);
     else
-        hipLaunchKernelGGL(grouped_gemm_kernel<false>, dim3(grid), dim3(kThreads), 0, stream, args);
+        hipLaunchKernelGGL((grouped_gemm_kernel<false, false>), g, b, 0, stream, args);
     return hipGetLastError();
 }
 

@@ -232,3 +232,24 @@ def test_k_step_counts_with_several_tiles_per_workgroup(pkg, steps):
     print(f"[parity] K steps {steps}: K={k} group_m={gm} N={n}", flush=True)
     r = Run(pkg, pkg.DType.BF16, gm, n, k).go()
     r.check_torch_fp32()
+
+
+# Multi-tile workgroups (cross-tile kernel): the previous tile's outputs are written from
+# registers inside the next tile's first step. N % 256 == 8 leaves an 8-column last tile
+# column, K % 64 != 0 a partial last step; some workgroups get two or three tiles.
+CROSS_TAILS = [
+    (0, [5000, 3100, 33], 2056, 1000),
+    (1, [4100, 4100], 2568, 704),   # exactly 11 K steps, fp16
+    (0, [2000, 9, 2047, 0, 1500], 4104, 2056),
+]
+
+
+@pytest.mark.parametrize("case", range(len(CROSS_TAILS)))
+def test_register_epilogue_tails(pkg, oracle, case):
+    dt, gm, n, k = CROSS_TAILS[case]
+    print(f"[parity] register-epilogue tails {case}: dtype={dt} group_m={gm} N={n} K={k}", flush=True)
+    r = Run(pkg, pkg.DType(dt), gm, n, k).go()
+    assert "cross-tile" in r.detail, r.detail
+    r.check_sampled(oracle)
+    r.check_torch_fp32()
+
