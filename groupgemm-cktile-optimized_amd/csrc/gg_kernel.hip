@@ -16,6 +16,9 @@
 //     fragments, offsets and addresses use the 256 arch VGPRs.
 //   * grid = min(#CUs, #tiles) persistent workgroups walking the tile list of all groups
 //     (gg_schedule.h: banded in-group order + XCD remap).
+//   * Two variants: cross-tile (a workgroup's tiles run as one continuous K pipeline and a
+//     finished tile is stored from registers during the next tile's first step) and per-tile
+//     (prologue and LDS-staged epilogue around every tile, for one tile per workgroup).
 //
 // LDS (160 KB, all of it): A (x rows) 2 stages + B (w rows) 3 stages of 256 rows x 128 B.
 // Row r keeps its 16-byte chunk c at chunk position c ^ (r % 8): the eight lanes that a
