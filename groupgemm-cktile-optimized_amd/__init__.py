@@ -38,6 +38,14 @@ C_API = {
     "gg_last_error": (ctypes.c_char_p, []),
     "gg_fill_randn": (ctypes.c_int, [ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint64,
                                      ctypes.c_void_p]),
+    "gg_prepare_device_lens": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_int64,
+                                              ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
+                                              ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                              ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)]),
+    "gg_plan_device_status": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p,
+                                             ctypes.POINTER(ctypes.c_int)]),
+    "gg_compute_group_offs": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                             ctypes.c_void_p]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -156,6 +164,29 @@ class Mi355xBackend(Backend):
         _check(st)
         return ""
 
+    def prepare_device_lens(self, dtype: DType, group_num: int, total_m: int, n: int, k: int,
+                            group_lens: int, group_offs: int, x: int, w: int, out: int,
+                            stream: int = 0) -> str:
+        """Plan over device-resident group sizes (the group_lens_ptr / group_offs_ptr contract
+        of the reference's Primus-Turbo grouped GEMM, grouped_gemm.h:35-36): group_lens is the
+        device address of int64[group_num], group_offs of int64[group_num + 1] or 0. Every
+        run() re-reads them on the stream. Returns "" or the reason it cannot run (N/A)."""
+        self.release()
+        st = self._lib.gg_prepare_device_lens(int(dtype), group_num, total_m, n, k, group_lens,
+                                              group_offs or None, x, w, out, stream,
+                                              ctypes.byref(self._plan))
+        if st == GG_ERR_UNSUPPORTED:
+            return last_error()
+        _check(st)
+        return ""
+
+    def device_status(self, stream: int = 0):
+        """(status, tile count, message) of the last run's device-side size check; synchronizes
+        `stream` for device-size plans."""
+        tiles = ctypes.c_int(0)
+        st = self._lib.gg_plan_device_status(self._plan, stream, ctypes.byref(tiles))
+        return st, tiles.value, last_error() if st != GG_OK else ""
+
     def run(self, stream: int = 0) -> None:
         _check(self._lib.gg_run(self._plan, stream))
 
@@ -199,10 +230,28 @@ def fill_randn(dtype: DType, ptr: int, count: int, seed: int, stream: int = 0) -
     _check(load_library().gg_fill_randn(int(dtype), ptr, count, seed, stream))
 
 
-def grouped_gemm(x, w, group_m: Sequence[int], out=None, stream: Optional[int] = None):
+def compute_group_offs(group_lens, stream: Optional[int] = None):
+    """Device int64 offsets [B + 1] of back-to-back groups from device int64 lengths [B]
+    (primus_turbo::compute_group_offs, grouped_gemm.h:138-140), on the current stream."""
+    import torch
+
+    if not (group_lens.is_cuda and group_lens.dtype == torch.int64 and group_lens.is_contiguous()):
+        raise ValueError("group_lens must be a contiguous int64 cuda tensor")
+    offs = torch.empty(group_lens.numel() + 1, dtype=torch.int64, device=group_lens.device)
+    s = torch.cuda.current_stream(group_lens.device).cuda_stream if stream is None else stream
+    _check(load_library().gg_compute_group_offs(group_lens.data_ptr(), offs.data_ptr(),
+                                                group_lens.numel(), s))
+    return offs
+
+
+def grouped_gemm(x, w, group_m, out=None, stream: Optional[int] = None, group_offs=None):
     """out = grouped GEMM of torch tensors x [sum(M), K], w [B, N, K] (bf16 or fp16, cuda).
 
-    Convenience wrapper: prepare + run + release on the current stream.
+    group_m is a host sequence of row counts, or a device int64 tensor [B] of them (routing
+    output; never read on the host, with optional device int64 offsets `group_offs` [B + 1],
+    as the reference's Primus-Turbo grouped GEMM takes them). With device sizes, rows of x and
+    out outside every group are left alone, and a size that does not fit raises GGError after
+    the run. Convenience wrapper: prepare + run + release on the current stream.
     """
     import torch
 
@@ -211,19 +260,38 @@ def grouped_gemm(x, w, group_m: Sequence[int], out=None, stream: Optional[int] =
     if not (x.is_cuda and w.is_cuda and x.is_contiguous() and w.is_contiguous()):
         raise ValueError("x and w must be contiguous device tensors")
     b, n, k = w.shape
-    if len(group_m) != b or x.shape[1] != k or x.shape[0] != sum(group_m):
+    device_sizes = isinstance(group_m, torch.Tensor)
+    if device_sizes:
+        if not (group_m.is_cuda and group_m.dtype == torch.int64 and group_m.numel() == b
+                and group_m.is_contiguous()):
+            raise ValueError("device group sizes must be a contiguous int64 cuda tensor of B entries")
+        if group_offs is not None and not (group_offs.is_cuda and group_offs.dtype == torch.int64
+                                           and group_offs.numel() == b + 1 and group_offs.is_contiguous()):
+            raise ValueError("group_offs must be a contiguous int64 cuda tensor of B + 1 entries")
+        if x.shape[1] != k:
+            raise ValueError("shape mismatch between x and w")
+    elif len(group_m) != b or x.shape[1] != k or x.shape[0] != sum(group_m):
         raise ValueError("shape mismatch between x, w and group_m")
     if out is None:
         out = torch.empty((x.shape[0], n), dtype=x.dtype, device=x.device)
     s = torch.cuda.current_stream(x.device).cuda_stream if stream is None else stream
-    prob = GroupedGemmProblem(DType.BF16 if x.dtype == torch.bfloat16 else DType.FP16, b, n, k,
-                              list(group_m), x.data_ptr(), w.data_ptr(), out.data_ptr())
+    dt = DType.BF16 if x.dtype == torch.bfloat16 else DType.FP16
     be = Mi355xBackend()
-    why = be.prepare(prob, s)
+    if device_sizes:
+        why = be.prepare_device_lens(dt, b, x.shape[0], n, k, group_m.data_ptr(),
+                                     group_offs.data_ptr() if group_offs is not None else 0,
+                                     x.data_ptr(), w.data_ptr(), out.data_ptr(), s)
+    else:
+        why = be.prepare(GroupedGemmProblem(dt, b, n, k, list(group_m), x.data_ptr(), w.data_ptr(),
+                                            out.data_ptr()), s)
     if why:
         raise GGError(GG_ERR_UNSUPPORTED, why)
     try:
         be.run(s)
+        if device_sizes:
+            st, _, msg = be.device_status(s)
+            if st != GG_OK:
+                raise GGError(st, msg)
         # the plan's device table must outlive the launch
         torch.cuda.current_stream(x.device).synchronize()
     finally:

@@ -30,6 +30,11 @@ struct gg_plan {
     gg::GroupEntry     *d_groups    = nullptr;
     gg::KernelArgs      args{};
     std::string         detail;
+    // Device-resident group sizes (gg_prepare_device_lens): the table is rebuilt per run.
+    bool                device_lens = false;
+    const int64_t      *d_lens      = nullptr;
+    const int64_t      *d_offs      = nullptr;
+    gg::TableHeader    *d_header    = nullptr; // follows the table in the d_groups allocation
 };
 
 namespace {
@@ -56,33 +61,15 @@ int xcd_count(const hipDeviceProp_t &prop) {
     return 1;
 }
 
-} // namespace
-
-extern "C" {
-
-int gg_prepare(int dtype, int group_num, int64_t n, int64_t k, const int64_t *group_m,
-               const void *x, const void *w, void *out, void *stream, gg_plan **plan_out) {
-    g_last_error.clear();
-    if (plan_out == nullptr)
-        return fail(GG_ERR_INVALID, "plan_out is null");
-    *plan_out = nullptr;
+// Shape and pointer rules shared by both prepare entry points; returns GG_OK or a failure.
+int check_problem(int dtype, int group_num, int64_t n, int64_t k, bool has_output, const void *x,
+                  const void *w, const void *out) {
     if (dtype != GG_DTYPE_BF16 && dtype != GG_DTYPE_FP16)
         return fail(GG_ERR_INVALID, "dtype must be GG_DTYPE_BF16 or GG_DTYPE_FP16");
     if (group_num < 0 || n < 0 || k < 0)
         return fail(GG_ERR_INVALID, "group_num, n and k must be >= 0");
-    if (group_num > 0 && group_m == nullptr)
-        return fail(GG_ERR_INVALID, "group_m is null");
-
-    int64_t total_m = 0;
-    for (int g = 0; g < group_num; ++g) {
-        if (group_m[g] < 0)
-            return fail(GG_ERR_INVALID, "group_m[" + std::to_string(g) + "] < 0");
-        total_m += group_m[g];
-    }
-    const bool has_output = total_m > 0 && n > 0;
     if (has_output && (out == nullptr || (k > 0 && (x == nullptr || w == nullptr))))
         return fail(GG_ERR_INVALID, "x, w and out must be device pointers");
-
     // Shapes the kernel cannot take: reported like a non-empty Backend::prepare result.
     if (n % 8 != 0)
         return fail(GG_ERR_UNSUPPORTED, "N must be a multiple of 8 (16-byte output rows)");
@@ -93,6 +80,55 @@ int gg_prepare(int dtype, int group_num, int64_t n, int64_t k, const int64_t *gr
     // 32-bit per-tile byte offsets: a 256-row slice of x, w or out must stay below 2 GiB.
     if (k > (int64_t(1) << 21) || n > (int64_t(1) << 21))
         return fail(GG_ERR_UNSUPPORTED, "N and K must be at most 2097152");
+    return GG_OK;
+}
+
+int device_props(hipDeviceProp_t *prop) {
+    int        dev = 0;
+    hipError_t e   = hipGetDevice(&dev);
+    if (e == hipSuccess)
+        e = hipGetDeviceProperties(prop, dev);
+    return e == hipSuccess ? GG_OK : hip_fail(e, "hipGetDeviceProperties");
+}
+
+void fill_args(gg_plan *plan, int n_xcd) {
+    gg::KernelArgs &a = plan->args;
+    a.x         = plan->x;
+    a.w         = plan->w;
+    a.out       = plan->out;
+    a.groups    = plan->d_groups;
+    a.group_num = plan->group_num;
+    a.n         = static_cast<int>(plan->n);
+    a.k         = static_cast<int>(plan->k);
+    a.n_tiles   = static_cast<int>(gg::cdiv(plan->n, gg::kTileN));
+    a.k_tiles   = static_cast<int>(gg::cdiv(plan->k, gg::kTileK));
+    a.n_xcd     = plan->grid % n_xcd == 0 ? n_xcd : 1;
+    a.band      = gg::kBand;
+}
+
+} // namespace
+
+extern "C" {
+
+int gg_prepare(int dtype, int group_num, int64_t n, int64_t k, const int64_t *group_m,
+               const void *x, const void *w, void *out, void *stream, gg_plan **plan_out) {
+    g_last_error.clear();
+    if (plan_out == nullptr)
+        return fail(GG_ERR_INVALID, "plan_out is null");
+    *plan_out = nullptr;
+    if (group_num > 0 && group_m == nullptr)
+        return fail(GG_ERR_INVALID, "group_m is null");
+
+    int64_t total_m = 0;
+    for (int g = 0; g < group_num; ++g) {
+        if (group_m[g] < 0)
+            return fail(GG_ERR_INVALID, "group_m[" + std::to_string(g) + "] < 0");
+        total_m += group_m[g];
+    }
+    const bool has_output = total_m > 0 && n > 0;
+    const int  st         = check_problem(dtype, group_num, n, k, has_output, x, w, out);
+    if (st != GG_OK)
+        return st;
 
     auto *plan = new (std::nothrow) gg_plan;
     if (plan == nullptr)
@@ -119,17 +155,13 @@ int gg_prepare(int dtype, int group_num, int64_t n, int64_t k, const int64_t *gr
 
     const hipStream_t s = static_cast<hipStream_t>(stream);
     if (plan->total_tiles > 0) {
-        int dev = 0;
-        hipError_t e = hipGetDevice(&dev);
         hipDeviceProp_t prop;
-        if (e == hipSuccess)
-            e = hipGetDeviceProperties(&prop, dev);
-        if (e != hipSuccess) {
+        if (device_props(&prop) != GG_OK) {
             delete plan;
-            return hip_fail(e, "hipGetDeviceProperties");
+            return GG_ERR_HIP;
         }
         const size_t bytes = table.size() * sizeof(gg::GroupEntry);
-        e = hipMalloc(&plan->d_groups, bytes);
+        hipError_t   e     = hipMalloc(&plan->d_groups, bytes);
         if (e == hipSuccess)
             e = hipMemcpyAsync(plan->d_groups, table.data(), bytes, hipMemcpyHostToDevice, s);
         if (e == hipSuccess)
@@ -142,22 +174,11 @@ int gg_prepare(int dtype, int group_num, int64_t n, int64_t k, const int64_t *gr
         }
         // Persistent grid: one workgroup per CU (160 KB of LDS each), never more than tiles.
         plan->grid = std::min(prop.multiProcessorCount, plan->total_tiles);
-        const int n_xcd = xcd_count(prop);
-
+        fill_args(plan, xcd_count(prop));
         gg::KernelArgs &a = plan->args;
-        a.x           = x;
-        a.w           = w;
-        a.out         = out;
-        a.groups      = plan->d_groups;
-        a.group_num   = group_num;
-        a.total_tiles = plan->total_tiles;
-        a.n           = static_cast<int>(n);
-        a.k           = static_cast<int>(k);
-        a.n_tiles     = static_cast<int>(n_tiles);
-        a.k_tiles     = static_cast<int>(gg::cdiv(k, gg::kTileK));
-        a.n_xcd       = plan->grid % n_xcd == 0 ? n_xcd : 1;
-        a.band        = gg::kBand;
-        plan->detail  = "mi355x persistent 256x256x64 " +
+        a.total_tiles     = plan->total_tiles;
+        a.d_total         = nullptr;
+        plan->detail      = "mi355x persistent 256x256x64 " +
                        std::string(dtype == GG_DTYPE_BF16 ? "bf16" : "fp16") +
                        " grid=" + std::to_string(plan->grid) +
                        " tiles=" + std::to_string(plan->total_tiles) +
@@ -171,10 +192,90 @@ int gg_prepare(int dtype, int group_num, int64_t n, int64_t k, const int64_t *gr
     return GG_OK;
 }
 
+int gg_prepare_device_lens(int dtype, int group_num, int64_t total_m, int64_t n, int64_t k,
+                           const int64_t *group_lens, const int64_t *group_offs, const void *x,
+                           const void *w, void *out, void *stream, gg_plan **plan_out) {
+    g_last_error.clear();
+    if (plan_out == nullptr)
+        return fail(GG_ERR_INVALID, "plan_out is null");
+    *plan_out = nullptr;
+    if (total_m < 0)
+        return fail(GG_ERR_INVALID, "total_m must be >= 0");
+    if (group_num > 0 && group_lens == nullptr)
+        return fail(GG_ERR_INVALID, "group_lens is null");
+    const bool has_output = total_m > 0 && n > 0;
+    const int  st         = check_problem(dtype, group_num, n, k, has_output, x, w, out);
+    if (st != GG_OK)
+        return st;
+
+    auto *plan = new (std::nothrow) gg_plan;
+    if (plan == nullptr)
+        return fail(GG_ERR_INVALID, "out of host memory");
+    plan->dtype       = dtype;
+    plan->group_num   = group_num;
+    plan->n           = n;
+    plan->k           = k;
+    plan->total_m     = total_m;
+    plan->x           = x;
+    plan->w           = w;
+    plan->out         = out;
+    plan->device_lens = true;
+    plan->d_lens      = group_lens;
+    plan->d_offs      = group_offs;
+    if (!has_output || k == 0 || group_num == 0) {
+        plan->detail = "mi355x: no launch (" +
+                       std::string(!has_output || group_num == 0 ? "empty output" : "K = 0, zero fill") +
+                       ")";
+        *plan_out = plan;
+        return GG_OK;
+    }
+    hipDeviceProp_t prop;
+    if (device_props(&prop) != GG_OK) {
+        delete plan;
+        return GG_ERR_HIP;
+    }
+    // Table + header in one allocation; the header is written by every run.
+    const size_t table_bytes = static_cast<size_t>(group_num) * sizeof(gg::GroupEntry);
+    hipError_t   e           = hipMalloc(&plan->d_groups, table_bytes + sizeof(gg::TableHeader));
+    if (e != hipSuccess) {
+        delete plan;
+        return hip_fail(e, "group table allocation");
+    }
+    plan->d_header = reinterpret_cast<gg::TableHeader *>(reinterpret_cast<char *>(plan->d_groups) +
+                                                         table_bytes);
+    // Tile count is unknown here: one workgroup per CU, or fewer if even the largest routing
+    // (every group's rows tiled separately) has fewer tiles.
+    const int64_t n_tiles   = gg::cdiv(n, gg::kTileN);
+    const int64_t max_tiles = (gg::cdiv(total_m, gg::kTileM) + group_num) * n_tiles;
+    plan->grid              = static_cast<int>(std::min<int64_t>(prop.multiProcessorCount, max_tiles));
+    fill_args(plan, xcd_count(prop));
+    plan->args.total_tiles = 0;
+    plan->args.d_total     = &plan->d_header->total_tiles;
+    plan->detail = "mi355x persistent 256x256x64 " +
+                   std::string(dtype == GG_DTYPE_BF16 ? "bf16" : "fp16") +
+                   " grid=" + std::to_string(plan->grid) + " tiles=device xcd=" +
+                   std::to_string(plan->args.n_xcd) +
+                   (gg::uses_cross_tile(plan->args, plan->grid) ? " cross-tile" : " per-tile") +
+                   " (device group sizes)";
+    *plan_out = plan;
+    return GG_OK;
+}
+
 int gg_run(const gg_plan *plan, void *stream) {
     if (plan == nullptr)
         return fail(GG_ERR_INVALID, "plan is null");
     const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (plan->device_lens && plan->d_groups != nullptr) {
+        hipError_t e = gg::launch_build_group_table(plan->d_lens, plan->d_offs, plan->group_num,
+                                                    plan->total_m, plan->args.n_tiles,
+                                                    plan->d_groups, plan->d_header, s);
+        if (e != hipSuccess)
+            return hip_fail(e, "group table launch");
+        e = gg::launch_grouped_gemm(plan->args, plan->dtype == GG_DTYPE_FP16, plan->grid, s);
+        if (e != hipSuccess)
+            return hip_fail(e, "grouped GEMM launch");
+        return GG_OK;
+    }
     if (plan->total_tiles == 0) {
         // K == 0 with a non-empty output: out = 0.
         if (plan->total_m > 0 && plan->n > 0 && plan->k == 0) {
@@ -204,6 +305,47 @@ const char *gg_plan_detail(const gg_plan *plan) { return plan ? plan->detail.c_s
 int gg_plan_grid(const gg_plan *plan) { return plan ? plan->grid : 0; }
 
 int gg_plan_tiles(const gg_plan *plan) { return plan ? plan->total_tiles : 0; }
+
+int gg_plan_device_status(const gg_plan *plan, void *stream, int *total_tiles) {
+    g_last_error.clear();
+    if (plan == nullptr)
+        return fail(GG_ERR_INVALID, "plan is null");
+    if (!plan->device_lens || plan->d_header == nullptr) {
+        if (total_tiles != nullptr)
+            *total_tiles = plan->total_tiles;
+        return GG_OK;
+    }
+    gg::TableHeader h{};
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e = hipMemcpyAsync(&h, plan->d_header, sizeof(h), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess)
+        e = hipStreamSynchronize(s);
+    if (e != hipSuccess)
+        return hip_fail(e, "device status read");
+    if (total_tiles != nullptr)
+        *total_tiles = h.total_tiles;
+    if (h.overflow != 0)
+        return fail(GG_ERR_INVALID, "device group sizes: more than 2^31 tiles, nothing computed");
+    if (h.first_bad >= 0)
+        return fail(GG_ERR_INVALID, "device group sizes: group " + std::to_string(h.first_bad) +
+                                        " has a negative length or rows outside [0, total_m); "
+                                        "its rows were not written");
+    return GG_OK;
+}
+
+int gg_compute_group_offs(const int64_t *group_lens, int64_t *group_offs, int group_num,
+                          void *stream) {
+    g_last_error.clear();
+    if (group_num < 0)
+        return fail(GG_ERR_INVALID, "group_num must be >= 0");
+    if (group_offs == nullptr || (group_num > 0 && group_lens == nullptr))
+        return fail(GG_ERR_INVALID, "group_lens and group_offs must be device pointers");
+    const hipError_t e =
+        gg::launch_group_offsets(group_lens, group_offs, group_num, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess)
+        return hip_fail(e, "group offsets launch");
+    return GG_OK;
+}
 
 const char *gg_last_error(void) { return g_last_error.c_str(); }
 

@@ -24,6 +24,16 @@ struct KernelArgs {
     int               k_tiles;     // ceil(K / kTileK)
     int               n_xcd;       // XCDs the grid is spread over (1 = no remap)
     int               band;        // M-tiles per band of the in-group tile order
+    const int        *d_total;     // device tile count (device-resident group sizes), or null:
+                                   // then total_tiles holds it
+};
+
+// Header of a device-built group table (follows the group_num entries).
+struct TableHeader {
+    int total_tiles; // tiles over all groups (0 if the count overflowed)
+    int first_bad;   // first group whose length or offset was out of range, -1 if none
+    int overflow;    // 1 if the tile count exceeded 32 bits (nothing is computed then)
+    int reserved;
 };
 
 // Whether a launch takes the cross-tile pipeline variant (several tiles per workgroup, enough
@@ -33,6 +43,16 @@ bool uses_cross_tile(const KernelArgs &args, int grid);
 // Enqueue the persistent grouped GEMM: `grid` workgroups of 256 threads on `stream`.
 // fp16 selects the f16 MFMA, otherwise bf16. Returns the launch status.
 hipError_t launch_grouped_gemm(const KernelArgs &args, bool fp16, int grid, hipStream_t stream);
+
+// Build the group table on the device from device-resident group sizes: lens[group_num]
+// (int64 rows) and offs[group_num + 1] (int64 first rows) or null for back-to-back groups.
+// Groups outside [0, total_m) get no tiles and are reported in the header. One wave.
+hipError_t launch_build_group_table(const int64_t *lens, const int64_t *offs, int group_num,
+                                    int64_t total_m, int n_tiles, GroupEntry *table,
+                                    TableHeader *header, hipStream_t stream);
+
+// offs[0] = 0, offs[g + 1] = offs[g] + lens[g]: group offsets from device lengths. One wave.
+hipError_t launch_group_offsets(const int64_t *lens, int64_t *offs, int group_num, hipStream_t stream);
 
 // Seeded N(0,1) fill (benchmark input generator).
 hipError_t launch_fill_randn(void *p, size_t count, uint64_t seed, bool fp16, hipStream_t stream);

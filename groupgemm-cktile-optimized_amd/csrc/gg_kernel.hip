@@ -325,6 +325,10 @@ grouped_gemm_kernel(const KernelArgs args) {
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6) & 3;
     const int wm = wave >> 1, wn = wave & 1;
     const int K = args.k, N = args.n, T = args.k_tiles;
+    // Tile count: from the kernel arguments, or from a group table built on the device.
+    const int total_tiles = args.d_total != nullptr
+                                ? __builtin_amdgcn_readfirstlane(*args.d_total)
+                                : args.total_tiles;
 
     // DMA j of an operand step covers tile rows j*32 + wave*8 .. +8; lane -> row lane/8,
     // logical chunk (lane%8) ^ (lane/8). x and w rows have the same length K, so one set of
@@ -404,7 +408,7 @@ grouped_gemm_kernel(const KernelArgs args) {
     };
     int  g         = 0; // group hint of locate_tile (logical tiles only grow)
     auto make_tile = [&](int t) -> Tile {
-        const int L = xcd_remap(t, args.total_tiles, gridDim.x, args.n_xcd);
+        const int L = xcd_remap(t, total_tiles, gridDim.x, args.n_xcd);
         int       tm, tn;
         locate_tile(L, args.groups, args.group_num, args.n_tiles, args.band, &g, &tm, &tn);
         const GroupEntry ge = args.groups[g];
@@ -428,7 +432,7 @@ grouped_gemm_kernel(const KernelArgs args) {
     const i32x4 rsrc_0 = dma_rsrc(args.x, 0); // zero length: no traffic, the DMA writes zeros
 
     int t = blockIdx.x;
-    if (t >= args.total_tiles)
+    if (t >= total_tiles)
         return;
     Tile cur = make_tile(t), nxt = cur;
     bool cross_next = false; // the DMAs past this tile's last K step fetch `nxt`
@@ -675,7 +679,7 @@ grouped_gemm_kernel(const KernelArgs args) {
             step.template operator()<0, 0, false, false, false>(kt + 5);
         }
         const int  t_next = t + gridDim.x;
-        const bool more   = t_next < args.total_tiles;
+        const bool more   = t_next < total_tiles;
         cross_next        = CROSS && more;
         if (cross_next)
             nxt = make_tile(t_next);
@@ -725,6 +729,74 @@ grouped_gemm_kernel(const KernelArgs args) {
 }
 
 // ---------------------------------------------------------------------------------------
+// Group table from device-resident group sizes (one wave, groups in chunks of 64).
+// The same facts as the host's build_group_table: first row, rows and first tile per group.
+// ---------------------------------------------------------------------------------------
+__device__ __forceinline__ int64_t wave_inclusive_sum(int64_t v, int lane) {
+    for (int d = 1; d < 64; d <<= 1) {
+        const int64_t u = __shfl_up(v, d, 64);
+        if (lane >= d)
+            v += u;
+    }
+    return v;
+}
+
+__global__ void __launch_bounds__(64)
+build_group_table_kernel(const int64_t *lens, const int64_t *offs, int group_num, int64_t total_m,
+                         int n_tiles, GroupEntry *table, TableHeader *header) {
+    const int lane      = threadIdx.x;
+    int64_t   row_carry = 0, tile_carry = 0;
+    int       first_bad = -1;
+    for (int base = 0; base < group_num; base += 64) {
+        const int g     = base + lane;
+        const bool live = g < group_num;
+        int64_t    m    = live ? lens[g] : 0;
+        bool       ok   = m >= 0 && m <= INT32_MAX;
+        if (!ok)
+            m = 0;
+        const int64_t rows_incl = wave_inclusive_sum(m, lane);
+        const int64_t row0      = offs != nullptr ? (live ? offs[g] : 0) : row_carry + rows_incl - m;
+        ok = ok && row0 >= 0 && row0 <= total_m && m <= total_m - row0;
+        const int64_t tiles      = ok ? cdiv(m, kTileM) * n_tiles : 0;
+        const int64_t tiles_incl = wave_inclusive_sum(tiles, lane);
+        if (live) {
+            GroupEntry e;
+            e.row0   = ok ? row0 : 0;
+            e.m      = ok ? static_cast<int32_t>(m) : 0;
+            e.tile0  = static_cast<int32_t>(min<int64_t>(tile_carry + tiles_incl - tiles, INT32_MAX));
+            table[g] = e;
+        }
+        const uint64_t bad = __ballot(live && !ok);
+        if (first_bad < 0 && bad != 0)
+            first_bad = base + __builtin_ctzll(bad);
+        row_carry += __shfl(rows_incl, 63, 64);
+        tile_carry += __shfl(tiles_incl, 63, 64);
+    }
+    if (lane == 0) {
+        const bool over     = tile_carry > INT32_MAX;
+        header->total_tiles = over ? 0 : static_cast<int>(tile_carry);
+        header->first_bad   = first_bad;
+        header->overflow    = over ? 1 : 0;
+        header->reserved    = 0;
+    }
+}
+
+__global__ void __launch_bounds__(64)
+group_offsets_kernel(const int64_t *lens, int64_t *offs, int group_num) {
+    const int lane  = threadIdx.x;
+    int64_t   carry = 0;
+    if (lane == 0)
+        offs[0] = 0;
+    for (int base = 0; base < group_num; base += 64) {
+        const int     g    = base + lane;
+        const int64_t incl = wave_inclusive_sum(g < group_num ? lens[g] : 0, lane);
+        if (g < group_num)
+            offs[g + 1] = carry + incl;
+        carry += __shfl(incl, 63, 64);
+    }
+}
+
+// ---------------------------------------------------------------------------------------
 // Benchmark input generator: splitmix64 of (seed, index) -> Box-Muller N(0, 1).
 // ---------------------------------------------------------------------------------------
 __device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
@@ -752,7 +824,10 @@ template <bool F16> __global__ void fill_randn_kernel(uint16_t *p, size_t n, uin
 
 bool uses_cross_tile(const KernelArgs &args, int grid) {
     // Workgroups with a single tile gain nothing from the cross-tile pipeline.
-    return kCrossAllowed && args.k_tiles >= kCrossMinSteps && args.total_tiles > grid;
+    // (a device-built table's tile count is unknown on the host: take the cross-tile variant,
+    // which also handles workgroups with a single tile)
+    return kCrossAllowed && args.k_tiles >= kCrossMinSteps &&
+           (args.d_total != nullptr || args.total_tiles > grid);
 }
 
 hipError_t launch_grouped_gemm(const KernelArgs &args, bool fp16, int grid, hipStream_t stream) {
@@ -766,6 +841,19 @@ hipError_t launch_grouped_gemm(const KernelArgs &args, bool fp16, int grid, hipS
         hipLaunchKernelGGL((grouped_gemm_kernel<false, true>), g, b, 0, stream, args);
     else
         hipLaunchKernelGGL((grouped_gemm_kernel<false, false>), g, b, 0, stream, args);
+    return hipGetLastError();
+}
+
+hipError_t launch_build_group_table(const int64_t *lens, const int64_t *offs, int group_num,
+                                    int64_t total_m, int n_tiles, GroupEntry *table,
+                                    TableHeader *header, hipStream_t stream) {
+    hipLaunchKernelGGL(build_group_table_kernel, dim3(1), dim3(64), 0, stream, lens, offs,
+                       group_num, total_m, n_tiles, table, header);
+    return hipGetLastError();
+}
+
+hipError_t launch_group_offsets(const int64_t *lens, int64_t *offs, int group_num, hipStream_t stream) {
+    hipLaunchKernelGGL(group_offsets_kernel, dim3(1), dim3(64), 0, stream, lens, offs, group_num);
     return hipGetLastError();
 }
 

@@ -80,6 +80,45 @@ const char *gg_plan_detail(const gg_plan *plan);
 int gg_plan_grid(const gg_plan *plan);
 int gg_plan_tiles(const gg_plan *plan);
 
+/*
+ * Device-resident group sizes (the output of MoE routing, never read on the host): like
+ * gg_prepare, but the sizes stay in device memory and every gg_run re-reads them on its stream,
+ * so one plan serves every routing of a layer. Replaces the group_lens_ptr / group_offs_ptr
+ * contract of the reference's vendored Primus-Turbo grouped GEMM
+ * (third_party/primus_turbo/include/primus_turbo/grouped_gemm.h:35-36, 95-96; read per call in
+ * kernels/hipblaslt_grouped_gemm.cu:174-216).
+ *   group_lens: device int64[group_num], rows of each group.
+ *   group_offs: device int64[group_num + 1], first row of each group, or NULL: the groups are
+ *               back to back from row 0 (offsets = prefix sums of group_lens).
+ *   total_m:    rows of x and out. A group with a negative length, or rows outside
+ *               [0, total_m), gets no work (its rows are not written) and is reported by
+ *               gg_plan_device_status.
+ * Each gg_run is two launches: a one-wave table build, then the grouped GEMM. k == 0 zeroes
+ * all total_m rows of out. Same shape requirements as gg_prepare.
+ */
+int gg_prepare_device_lens(int dtype, int group_num, int64_t total_m, int64_t n, int64_t k,
+                           const int64_t *group_lens, const int64_t *group_offs, const void *x,
+                           const void *w, void *out, void *stream, gg_plan **plan_out);
+
+/*
+ * Device-side size check of the last gg_run of a gg_prepare_device_lens plan, read back with a
+ * synchronization of `stream`: GG_OK, or GG_ERR_INVALID naming the first group whose length or
+ * offset was out of range (or a tile count beyond 32 bits, when nothing was computed).
+ * *total_tiles (if not NULL) receives that run's tile count. For gg_prepare plans: GG_OK and
+ * the plan's tile count, without a synchronization. No counterpart in the reference, which
+ * does not check device-side sizes.
+ */
+int gg_plan_device_status(const gg_plan *plan, void *stream, int *total_tiles);
+
+/*
+ * offs[0] = 0, offs[g + 1] = offs[g] + lens[g] for g < group_num: the group offsets of
+ * back-to-back groups, from device int64 lengths into device int64[group_num + 1], on `stream`
+ * (one small launch, no sync). Replaces primus_turbo::compute_group_offs
+ * (third_party/primus_turbo/include/primus_turbo/grouped_gemm.h:138-140; its body is not
+ * vendored, the semantics follow the group_offs_ptr contract of group_num + 1 first rows).
+ */
+int gg_compute_group_offs(const int64_t *group_lens, int64_t *group_offs, int group_num, void *stream);
+
 /* Message of the last failed call on the calling thread ("" if none). */
 const char *gg_last_error(void);
 

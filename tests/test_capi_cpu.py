@@ -89,3 +89,54 @@ def test_backend_interface_mirrors_reference(pkg):
     assert "multiple of 8" in be.prepare(p, 0)
     with pytest.raises(KeyError):
         pkg.make_backend("ck_tile_does_not_exist")
+
+
+def _prepare_dev(lib, dtype=0, group_num=2, total_m=11, n=64, k=64, lens=16, offs=None, x=16, w=16,
+                 out=16):
+    plan = ctypes.c_void_p()
+    st = lib.gg_prepare_device_lens(dtype, group_num, total_m, n, k, lens, offs, x, w, out, None,
+                                    ctypes.byref(plan))
+    return st, plan
+
+
+@pytest.mark.parametrize("kwargs,status,msg", [
+    (dict(dtype=5), 2, "dtype"),
+    (dict(total_m=-1), 2, "total_m"),
+    (dict(group_num=-2), 2, ">= 0"),
+    (dict(lens=None), 2, "group_lens is null"),
+    (dict(w=0), 2, "device pointers"),
+    (dict(n=20), 1, "N must be a multiple of 8"),
+    (dict(k=12), 1, "K must be a multiple of 8"),
+    (dict(x=8), 1, "16-byte aligned"),
+    (dict(n=1 << 22), 1, "at most"),
+])
+def test_prepare_device_lens_rejects_without_touching_the_gpu(pkg, kwargs, status, msg):
+    """Device-resident group sizes: the same argument and shape rules as gg_prepare, checked
+    without reading the sizes (they are device memory)."""
+    lib = pkg.load_library()
+    st, plan = _prepare_dev(lib, **kwargs)
+    assert st == status
+    assert msg in pkg.last_error()
+    assert not plan.value
+
+
+def test_device_lens_plans_without_work_need_no_gpu(pkg):
+    """K == 0 or an empty output: the plan is built on the host alone; its status is OK."""
+    lib = pkg.load_library()
+    for kw, note in ((dict(k=0), "K = 0"), (dict(total_m=0), "empty output"), (dict(group_num=0), "empty")):
+        st, plan = _prepare_dev(lib, **kw)
+        assert st == pkg.GG_OK, pkg.last_error()
+        assert note in lib.gg_plan_detail(plan).decode()
+        tiles = ctypes.c_int(-1)
+        assert lib.gg_plan_device_status(plan, None, ctypes.byref(tiles)) == pkg.GG_OK
+        assert tiles.value == 0
+        lib.gg_release(plan)
+    assert lib.gg_plan_device_status(None, None, None) == pkg.GG_ERR_INVALID
+    assert lib.gg_prepare_device_lens(0, 1, 8, 8, 8, 16, None, 16, 16, 16, None, None) == pkg.GG_ERR_INVALID
+
+
+def test_compute_group_offs_rejects_bad_arguments(pkg):
+    lib = pkg.load_library()
+    assert lib.gg_compute_group_offs(None, 16, -1, None) == pkg.GG_ERR_INVALID
+    assert lib.gg_compute_group_offs(None, 16, 4, None) == pkg.GG_ERR_INVALID
+    assert lib.gg_compute_group_offs(16, None, 4, None) == pkg.GG_ERR_INVALID
