@@ -4,7 +4,7 @@
 // looked up by name in tunemax::backend_registry().
 //
 //   gg_bench --shapes shapes/configs.csv [--dtype bf16|fp16] [--backends a,b,c]
-//            [--only 1,2] [--warmup 20] [--iters 100] [--no-check] [--out results.csv]
+//            [--only 1,2] [--warmup 20] [--iters 100] [--no-check] [--out results.csv] [--verbose]
 //
 // Per case: B balanced groups of M rows, x and w ~ N(0,1) (seeds 1 and 2), output zeroed
 // before each backend, prepare() untimed, one run() + sampled fp32 check (4 corners and 256
@@ -14,6 +14,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdint>
 #include <ctime>
@@ -41,6 +42,7 @@ struct Options {
     std::set<int>            only;
     int                      warmup = 20, iters = 100;
     bool                     check = true;
+    bool                     verbose = false; // phase timestamps per backend on stderr
 };
 
 std::vector<std::string> split(const std::string &s, char sep) {
@@ -62,6 +64,7 @@ std::vector<std::string> split(const std::string &s, char sep) {
     std::cerr << "error: " << msg << "\n"
               << "usage: gg_bench --shapes FILE.csv [--dtype bf16|fp16] [--backends a,b,...]\n"
               << "                [--only TESTID,...] [--warmup N] [--iters N] [--no-check] [--out FILE.csv]\n"
+              << "                [--verbose]   (phase timestamps per backend on stderr)\n"
               << "backends:";
     for (const auto &kv : backend_registry())
         std::cerr << " " << kv.first;
@@ -98,6 +101,8 @@ Options parse_args(int argc, char **argv) {
             o.iters = std::stoi(next());
         else if (a == "--no-check")
             o.check = false;
+        else if (a == "--verbose")
+            o.verbose = true;
         else if (a == "-h" || a == "--help")
             usage("help requested");
         else
@@ -394,6 +399,13 @@ int run(const Options &opt) {
 
         for (auto &backend : backends) {
             Row row{tc, backend->name(), "", "", NAN, NAN, NAN};
+            const auto t_case = std::chrono::steady_clock::now();
+            auto       phase  = [&](const char *what) {
+                if (opt.verbose)
+                    std::cerr << "    [" << tc.id << " " << backend->name() << "] " << what << " at "
+                              << std::chrono::duration<double>(std::chrono::steady_clock::now() - t_case).count()
+                              << " s" << std::endl;
+            };
             try {
                 TUNEMAX_HIP_CHECK(hipMemsetAsync(p.out, 0, size_t(p.total_m()) * p.n * es, stream));
                 const std::string why = backend->prepare(p, stream);
@@ -402,9 +414,11 @@ int run(const Options &opt) {
                     row.detail = why;
                 } else {
                     row.detail = backend->detail();
+                    phase("prepared");
                     backend->run(stream);
                     TUNEMAX_HIP_CHECK(hipGetLastError());
                     TUNEMAX_HIP_CHECK(hipStreamSynchronize(stream));
+                    phase("first run");
                     if (opt.check) {
                         const CheckResult c = check_output(p, samples, stream);
                         row.check           = c.pass ? "PASS" : "FAIL";
@@ -415,8 +429,12 @@ int run(const Options &opt) {
                     } else {
                         row.check = "SKIP";
                     }
+                    phase("checked");
                     for (int i = 0; i < opt.warmup; ++i)
                         backend->run(stream);
+                    if (opt.verbose)
+                        TUNEMAX_HIP_CHECK(hipStreamSynchronize(stream));
+                    phase("warmed up");
                     TUNEMAX_HIP_CHECK(hipEventRecord(start, stream));
                     for (int i = 0; i < opt.iters; ++i)
                         backend->run(stream);

@@ -7,7 +7,11 @@
 //   non-empty group builds the matmul descriptors, asks the heuristic for one algorithm and
 //   calls hipblasLtMatmul, round-robin over 4 streams (64 MiB of workspace each) forked from
 //   and joined back into the caller's stream with events. All of it is inside the timed
-//   region, as it is in Primus-Turbo.
+//   region, as it is in Primus-Turbo. Every stream slot has its own hipBLASLt handle and 8
+//   slots are created although 4 are used: hipBLASLt keeps per-handle state and assumes one
+//   handle per stream, and Primus-Turbo reports multi-stream stalls on MI355X without both
+//   (hipblaslt_grouped_gemm.cu:21-27, 40-55). Unlike Primus-Turbo, the side streams keep the
+//   default priority.
 // hipblaslt_grouped: hipblaslt_ext::GroupedGemm, one launch for all groups, device-side
 //   arguments, heuristic top-1, prepared untimed; N/A when the library has no kernel for the
 //   type (the reference's backends/hipblaslt_grouped_backend.cpp:45-98).
@@ -37,26 +41,28 @@ hipDataType hip_type(DType t) { return t == DType::BF16 ? HIP_R_16BF : HIP_R_16F
 // ---------------------------------------------------------------------------------------
 class HipblasltLoopBackend final : public Backend {
 public:
-    static constexpr int     kStreams         = 4;
+    static constexpr int     kStreams         = 4; // slots used per run
+    static constexpr int     kSlots           = 8; // slots created (handle + stream + event)
     static constexpr int64_t kWorkspacePerStr = int64_t(64) << 20;
 
     HipblasltLoopBackend() {
-        blas_check(hipblasLtCreate(&handle_), "create");
+        for (int i = 0; i < kSlots; ++i)
+            blas_check(hipblasLtCreate(&handle_[i]), "create");
         TUNEMAX_HIP_CHECK(hipMalloc(&workspace_, kStreams * kWorkspacePerStr));
-        // stream-K kernels keep flags in the workspace: start from zeros
         TUNEMAX_HIP_CHECK(hipMemset(workspace_, 0, kStreams * kWorkspacePerStr));
-        for (int i = 1; i < kStreams; ++i)
+        for (int i = 1; i < kSlots; ++i)
             TUNEMAX_HIP_CHECK(hipStreamCreateWithFlags(&side_[i], hipStreamNonBlocking));
-        for (int i = 0; i < kStreams; ++i)
+        for (int i = 0; i < kSlots; ++i)
             TUNEMAX_HIP_CHECK(hipEventCreateWithFlags(&ev_[i], hipEventDisableTiming));
     }
     ~HipblasltLoopBackend() override {
-        for (int i = 0; i < kStreams; ++i)
+        for (int i = 0; i < kSlots; ++i)
             (void)hipEventDestroy(ev_[i]);
-        for (int i = 1; i < kStreams; ++i)
+        for (int i = 1; i < kSlots; ++i)
             (void)hipStreamDestroy(side_[i]);
         (void)hipFree(workspace_);
-        (void)hipblasLtDestroy(handle_);
+        for (int i = 0; i < kSlots; ++i)
+            (void)hipblasLtDestroy(handle_[i]);
     }
 
     std::string name() const override { return "hipblaslt_loop"; }
@@ -64,6 +70,12 @@ public:
     std::string prepare(const GroupedGemmProblem &p, hipStream_t) override {
         if (p.group_lens_pinned == nullptr)
             return "needs the group lengths in pinned host memory";
+        // This 4-stream loop never finished its first call on groups of 1024 x 4096 x 7168
+        // (shapes/full.csv TestID 3) on MI355X, with one shared handle and again with one
+        // handle per stream; it is not run there.
+        for (int g = 0; g < p.group_num; ++g)
+            if (p.group_m[g] == 1024 && p.n == 4096 && p.k == 7168)
+                return "skipped: the multi-stream hipBLASLt loop hung on 1024 x 4096 x 7168 groups on MI355X";
         p_ = p;
         return "";
     }
@@ -87,7 +99,7 @@ public:
             const char *x   = static_cast<const char *>(p_.x) + size_t(row) * p_.k * es;
             char       *out = static_cast<char *>(p_.out) + size_t(row) * p_.n * es;
             const int   s   = idx % kStreams;
-            gemm(t, p_.n, m, p_.k, w, x, out, &alpha, &beta,
+            gemm(handle_[s], t, p_.n, m, p_.k, w, x, out, &alpha, &beta,
                  static_cast<char *>(workspace_) + s * kWorkspacePerStr, side_[s]);
             row += m;
             ++idx;
@@ -103,8 +115,8 @@ public:
 
 private:
     // D [m, n] col-major = op_T(A: k x m col-major) * B (k x n col-major), one group.
-    void gemm(hipDataType t, int64_t m, int64_t n, int64_t k, const void *a, const void *b, void *d,
-              const float *alpha, const float *beta, void *ws, hipStream_t s) {
+    void gemm(hipblasLtHandle_t handle, hipDataType t, int64_t m, int64_t n, int64_t k, const void *a,
+              const void *b, void *d, const float *alpha, const float *beta, void *ws, hipStream_t s) {
         hipblasLtMatmulDesc_t   desc = nullptr;
         hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, lc = nullptr;
         hipblasLtMatmulPreference_t pref = nullptr;
@@ -122,11 +134,11 @@ private:
                    "workspace preference");
         hipblasLtMatmulHeuristicResult_t res{};
         int                              found = 0;
-        blas_check(hipblasLtMatmulAlgoGetHeuristic(handle_, desc, la, lb, lc, lc, pref, 1, &res, &found),
+        blas_check(hipblasLtMatmulAlgoGetHeuristic(handle, desc, la, lb, lc, lc, pref, 1, &res, &found),
                    "heuristic");
         if (found == 0)
             throw std::runtime_error("hipBLASLt heuristic found no algorithm");
-        blas_check(hipblasLtMatmul(handle_, desc, alpha, a, la, b, lb, beta, d, lc, d, lc, &res.algo, ws,
+        blas_check(hipblasLtMatmul(handle, desc, alpha, a, la, b, lb, beta, d, lc, d, lc, &res.algo, ws,
                                    kWorkspacePerStr, s),
                    "matmul");
         (void)hipblasLtMatmulPreferenceDestroy(pref);
@@ -136,10 +148,10 @@ private:
         (void)hipblasLtMatmulDescDestroy(desc);
     }
 
-    hipblasLtHandle_t  handle_    = nullptr;
+    hipblasLtHandle_t  handle_[kSlots]{};
     void              *workspace_ = nullptr;
-    hipStream_t        side_[kStreams]{};
-    hipEvent_t         ev_[kStreams]{};
+    hipStream_t        side_[kSlots]{};
+    hipEvent_t         ev_[kSlots]{};
     GroupedGemmProblem p_;
 };
 
