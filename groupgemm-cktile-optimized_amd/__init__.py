@@ -46,6 +46,12 @@ C_API = {
                                              ctypes.POINTER(ctypes.c_int)]),
     "gg_compute_group_offs": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
                                              ctypes.c_void_p]),
+    "gg_prepare_dgrad": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_int64,
+                                        ctypes.POINTER(ctypes.c_int64), ctypes.c_void_p, ctypes.c_void_p,
+                                        ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)]),
+    "gg_prepare_wgrad": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_int64,
+                                        ctypes.POINTER(ctypes.c_int64), ctypes.c_void_p, ctypes.c_void_p,
+                                        ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -211,6 +217,44 @@ class Mi355xBackend(Backend):
             pass
 
 
+class BackwardPlan:
+    """A dgrad or wgrad plan (gg_prepare_dgrad / gg_prepare_wgrad), run any number of times.
+
+    kind "dgrad": out [sum(M), k] = grad_out [sum(M), n] @ w[g] [n, k] per group.
+    kind "wgrad": out [B, n, k] = grad_out[g]^T [n, M_g] @ x[g] [M_g, k], zero for empty groups.
+    Buffers are device addresses; prepare raises GGError (status 1 = not supported).
+    """
+
+    def __init__(self, kind: str, dtype: DType, n: int, k: int, group_m: Sequence[int], grad_out: int,
+                 other: int, out: int, stream: int = 0) -> None:
+        if kind not in ("dgrad", "wgrad"):
+            raise ValueError("kind must be 'dgrad' or 'wgrad'")
+        self._lib = load_library()
+        self._plan = ctypes.c_void_p()
+        gm = (ctypes.c_int64 * max(1, len(group_m)))(*group_m)
+        fn = self._lib.gg_prepare_dgrad if kind == "dgrad" else self._lib.gg_prepare_wgrad
+        _check(fn(int(dtype), len(group_m), n, k, gm, grad_out, other, out, stream, ctypes.byref(self._plan)))
+        self.kind = kind
+        self.flop = 2.0 * float(sum(group_m)) * float(n) * float(k)
+
+    def run(self, stream: int = 0) -> None:
+        _check(self._lib.gg_run(self._plan, stream))
+
+    def detail(self) -> str:
+        return self._lib.gg_plan_detail(self._plan).decode() if self._plan else ""
+
+    def release(self) -> None:
+        if self._plan:
+            self._lib.gg_release(self._plan)
+            self._plan = ctypes.c_void_p()
+
+    def __del__(self) -> None:
+        try:
+            self.release()
+        except Exception:
+            pass
+
+
 def make_mi355x_backend() -> Backend:
     return Mi355xBackend()
 
@@ -228,6 +272,49 @@ def make_backend(name: str) -> Backend:
 def fill_randn(dtype: DType, ptr: int, count: int, seed: int, stream: int = 0) -> None:
     """Seeded N(0,1) device fill of the benchmark driver (bench/bench_main.cpp:160-176)."""
     _check(load_library().gg_fill_randn(int(dtype), ptr, count, seed, stream))
+
+
+def _backward(kind: str, grad_out, other, group_m: Sequence[int], out, stream: Optional[int]):
+    import torch
+
+    if grad_out.dtype != other.dtype or grad_out.dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError("operands must both be bfloat16 or both float16")
+    if not (grad_out.is_cuda and other.is_cuda and grad_out.is_contiguous() and other.is_contiguous()):
+        raise ValueError("operands must be contiguous device tensors")
+    n = grad_out.shape[1]
+    if grad_out.shape[0] != sum(group_m):
+        raise ValueError("grad_out must have sum(group_m) rows")
+    if kind == "dgrad":
+        if other.shape[0] != len(group_m) or other.shape[1] != n:
+            raise ValueError("w must be [B, N, K] with N = grad_out's columns")
+        k = other.shape[2]
+        shape = (grad_out.shape[0], k)
+    else:
+        if other.shape[0] != grad_out.shape[0]:
+            raise ValueError("x must have the rows of grad_out")
+        k = other.shape[1]
+        shape = (len(group_m), n, k)
+    if out is None:
+        out = torch.empty(shape, dtype=grad_out.dtype, device=grad_out.device)
+    s = torch.cuda.current_stream(grad_out.device).cuda_stream if stream is None else stream
+    dt = DType.BF16 if grad_out.dtype == torch.bfloat16 else DType.FP16
+    plan = BackwardPlan(kind, dt, n, k, list(group_m), grad_out.data_ptr(), other.data_ptr(), out.data_ptr(), s)
+    try:
+        plan.run(s)
+        torch.cuda.current_stream(grad_out.device).synchronize()
+    finally:
+        plan.release()
+    return out
+
+
+def grouped_gemm_dgrad(grad_out, w, group_m: Sequence[int], out=None, stream: Optional[int] = None):
+    """grad_x [sum(M), K] = grad_out [sum(M), N] @ w[g] [N, K] per group (torch tensors)."""
+    return _backward("dgrad", grad_out, w, group_m, out, stream)
+
+
+def grouped_gemm_wgrad(grad_out, x, group_m: Sequence[int], out=None, stream: Optional[int] = None):
+    """grad_w [B, N, K] = grad_out[g]^T @ x[g] per group, zero for empty groups (torch tensors)."""
+    return _backward("wgrad", grad_out, x, group_m, out, stream)
 
 
 def compute_group_offs(group_lens, stream: Optional[int] = None):

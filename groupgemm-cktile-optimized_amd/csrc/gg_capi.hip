@@ -17,6 +17,7 @@
 #include "gg_kernel.h"
 
 struct gg_plan {
+    int                 mode        = 0; // 0 forward, 1 dgrad, 2 wgrad (kernel terms: KernelArgs)
     int                 dtype       = GG_DTYPE_BF16;
     int                 group_num   = 0;
     int64_t             n           = 0;
@@ -104,6 +105,9 @@ void fill_args(gg_plan *plan, int n_xcd) {
     a.k_tiles   = static_cast<int>(gg::cdiv(plan->k, gg::kTileK));
     a.n_xcd     = plan->grid % n_xcd == 0 ? n_xcd : 1;
     a.band      = gg::kBand;
+    a.lda       = static_cast<int>(plan->k);
+    a.ldb       = static_cast<int>(plan->k);
+    a.m_out     = 0;
 }
 
 } // namespace
@@ -192,6 +196,130 @@ int gg_prepare(int dtype, int group_num, int64_t n, int64_t k, const int64_t *gr
     return GG_OK;
 }
 
+// Backward plans in kernel terms (see KernelArgs): out (rows x N) = A B^T per group with the
+// contraction K. dgrad: A = grad_out (K-major, row stride n), B^T = w[g] stored n x k,
+// N = k, K = n. wgrad: A^T = grad_out rows of the group (row stride n), B^T = x rows (row stride
+// k), out = grad_w[g] n x k, N = k, K = the group's rows.
+static int prepare_backward(int mode, int dtype, int group_num, int64_t n, int64_t k,
+                            const int64_t *group_m, const void *a, const void *b, void *out,
+                            void *stream, gg_plan **plan_out) {
+    g_last_error.clear();
+    if (plan_out == nullptr)
+        return fail(GG_ERR_INVALID, "plan_out is null");
+    *plan_out = nullptr;
+    if (group_num > 0 && group_m == nullptr)
+        return fail(GG_ERR_INVALID, "group_m is null");
+    int64_t total_m = 0, max_m = 0;
+    for (int g = 0; g < group_num; ++g) {
+        if (group_m[g] < 0)
+            return fail(GG_ERR_INVALID, "group_m[" + std::to_string(g) + "] < 0");
+        total_m += group_m[g];
+        max_m = std::max(max_m, group_m[g]);
+    }
+    // Output rows: grad_x has total_m, grad_w has group_num * n.
+    const int64_t out_rows   = mode == 1 ? total_m : int64_t(group_num) * n;
+    const bool    has_output = out_rows > 0 && k > 0;
+    // Both operands are read when the contraction (n for dgrad, the rows for wgrad) is non-zero.
+    const bool reads = mode == 1 ? (total_m > 0 && n > 0) : (total_m > 0);
+    if (dtype != GG_DTYPE_BF16 && dtype != GG_DTYPE_FP16)
+        return fail(GG_ERR_INVALID, "dtype must be GG_DTYPE_BF16 or GG_DTYPE_FP16");
+    if (group_num < 0 || n < 0 || k < 0)
+        return fail(GG_ERR_INVALID, "group_num, n and k must be >= 0");
+    if (has_output && (out == nullptr || (reads && (a == nullptr || b == nullptr))))
+        return fail(GG_ERR_INVALID, "grad_out, the second operand and the output must be device pointers");
+    if (n % 8 != 0)
+        return fail(GG_ERR_UNSUPPORTED, "N must be a multiple of 8 (16-byte rows)");
+    if (k % 8 != 0)
+        return fail(GG_ERR_UNSUPPORTED, "K must be a multiple of 8 (16-byte rows)");
+    if (has_output && (!aligned16(out) || (reads && (!aligned16(a) || !aligned16(b)))))
+        return fail(GG_ERR_UNSUPPORTED, "buffers must be 16-byte aligned");
+    if (k > (int64_t(1) << 21) || n > (int64_t(1) << 21))
+        return fail(GG_ERR_UNSUPPORTED, "N and K must be at most 2097152");
+    // 32-bit byte offsets inside one group's transposed operand, including the rows a partial
+    // last K step addresses past the end (up to 64 more).
+    const int64_t lim = int64_t(1) << 31;
+    if (mode == 1 && (n + gg::kTileK) * k * 2 >= lim)
+        return fail(GG_ERR_UNSUPPORTED, "one group's w must be smaller than 2 GiB");
+    if (mode == 2 && ((max_m + gg::kTileK) * n * 2 >= lim || (max_m + gg::kTileK) * k * 2 >= lim))
+        return fail(GG_ERR_UNSUPPORTED, "one group's rows of grad_out and x must be smaller than 2 GiB");
+
+    auto *plan = new (std::nothrow) gg_plan;
+    if (plan == nullptr)
+        return fail(GG_ERR_INVALID, "out of host memory");
+    plan->mode      = mode;
+    plan->dtype     = dtype;
+    plan->group_num = group_num;
+    plan->n         = k;                      // output columns
+    plan->k         = mode == 1 ? n : 0;      // contraction (wgrad: per group)
+    plan->total_m   = out_rows;               // rows zeroed when there is nothing to read
+    plan->x         = a;
+    plan->w         = b;
+    plan->out       = out;
+
+    const int64_t n_tiles = gg::cdiv(k, gg::kTileN);
+    std::vector<gg::GroupEntry> table(static_cast<size_t>(group_num));
+    const int64_t tiles = gg::build_group_table(group_m, group_num, n_tiles, table.data(), mode == 2 ? n : 0);
+    if (tiles < 0) {
+        delete plan;
+        return fail(GG_ERR_UNSUPPORTED, "too many rows or tiles for 32-bit tile indices");
+    }
+    // dgrad with n == 0: grad_x = 0 (gg_run zero-fills). wgrad with no rows: the tiles run and
+    // store zeros (each group's K steps read nothing).
+    plan->total_tiles = has_output && (mode == 2 || n > 0) ? static_cast<int>(tiles) : 0;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const char *what = mode == 1 ? "dgrad" : "wgrad";
+    if (plan->total_tiles > 0) {
+        hipDeviceProp_t prop;
+        if (device_props(&prop) != GG_OK) {
+            delete plan;
+            return GG_ERR_HIP;
+        }
+        const size_t bytes = table.size() * sizeof(gg::GroupEntry);
+        hipError_t   e     = hipMalloc(&plan->d_groups, bytes);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(plan->d_groups, table.data(), bytes, hipMemcpyHostToDevice, s);
+        if (e == hipSuccess)
+            e = hipStreamSynchronize(s);
+        if (e != hipSuccess) {
+            if (plan->d_groups != nullptr)
+                (void)hipFree(plan->d_groups);
+            delete plan;
+            return hip_fail(e, "group table upload");
+        }
+        plan->grid = std::min(prop.multiProcessorCount, plan->total_tiles);
+        fill_args(plan, xcd_count(prop));
+        gg::KernelArgs &ka = plan->args;
+        ka.total_tiles     = plan->total_tiles;
+        ka.d_total         = nullptr;
+        ka.lda             = static_cast<int>(n);
+        ka.ldb             = static_cast<int>(k);
+        ka.m_out           = mode == 2 ? static_cast<int>(n) : 0;
+        ka.k_tiles         = mode == 1 ? static_cast<int>(gg::cdiv(n, gg::kTileK)) : 1;
+        plan->detail       = std::string("mi355x ") + what + " persistent 256x256x64 " +
+                       std::string(dtype == GG_DTYPE_BF16 ? "bf16" : "fp16") +
+                       " grid=" + std::to_string(plan->grid) + " tiles=" + std::to_string(plan->total_tiles) +
+                       " xcd=" + std::to_string(ka.n_xcd) +
+                       (gg::uses_cross_tile(ka, plan->grid, mode) ? " cross-tile" : " per-tile");
+    } else {
+        plan->detail = std::string("mi355x ") + what + ": no launch (" +
+                       (has_output ? "empty contraction, zero fill" : "empty output") + ")";
+        if (!has_output)
+            plan->total_m = 0;
+    }
+    *plan_out = plan;
+    return GG_OK;
+}
+
+int gg_prepare_dgrad(int dtype, int group_num, int64_t n, int64_t k, const int64_t *group_m,
+                     const void *grad_out, const void *w, void *grad_x, void *stream, gg_plan **plan_out) {
+    return prepare_backward(1, dtype, group_num, n, k, group_m, grad_out, w, grad_x, stream, plan_out);
+}
+
+int gg_prepare_wgrad(int dtype, int group_num, int64_t n, int64_t k, const int64_t *group_m,
+                     const void *grad_out, const void *x, void *grad_w, void *stream, gg_plan **plan_out) {
+    return prepare_backward(2, dtype, group_num, n, k, group_m, grad_out, x, grad_w, stream, plan_out);
+}
+
 int gg_prepare_device_lens(int dtype, int group_num, int64_t total_m, int64_t n, int64_t k,
                            const int64_t *group_lens, const int64_t *group_offs, const void *x,
                            const void *w, void *out, void *stream, gg_plan **plan_out) {
@@ -271,7 +399,7 @@ int gg_run(const gg_plan *plan, void *stream) {
                                                     plan->d_groups, plan->d_header, s);
         if (e != hipSuccess)
             return hip_fail(e, "group table launch");
-        e = gg::launch_grouped_gemm(plan->args, plan->dtype == GG_DTYPE_FP16, plan->grid, s);
+        e = gg::launch_grouped_gemm(plan->args, plan->dtype == GG_DTYPE_FP16, plan->grid, s, plan->mode);
         if (e != hipSuccess)
             return hip_fail(e, "grouped GEMM launch");
         return GG_OK;
@@ -286,7 +414,7 @@ int gg_run(const gg_plan *plan, void *stream) {
         return GG_OK;
     }
     const hipError_t e =
-        gg::launch_grouped_gemm(plan->args, plan->dtype == GG_DTYPE_FP16, plan->grid, s);
+        gg::launch_grouped_gemm(plan->args, plan->dtype == GG_DTYPE_FP16, plan->grid, s, plan->mode);
     if (e != hipSuccess)
         return hip_fail(e, "grouped GEMM launch");
     return GG_OK;

@@ -11,10 +11,14 @@ namespace gg {
 
 // Kernel arguments, passed by value in the kernarg segment. Everything a workgroup needs
 // to find its tiles: the device group table plus the problem-wide sizes.
+// Kernel terms: out (rows x N) = A (rows x K) B^T (N x K) per group, K the contraction.
+//   forward: A = x [sum(M), K], B = w [B, N, K], out [sum(M), N]
+//   dgrad:   A = grad_out [sum(M), K], B^T = w[g] [K, N] (stored K x N), out = grad_x [sum(M), N]
+//   wgrad:   A^T = grad_out [M_g, m_out], B^T = x [M_g, N], out = grad_w [B, m_out, N], K = M_g
 struct KernelArgs {
-    const void       *x;      // [sum(M), K] row-major
-    const void       *w;      // [B, N, K] row-major
-    void             *out;    // [sum(M), N] row-major
+    const void       *x;      // A operand storage (x, or grad_out for dgrad / wgrad)
+    const void       *w;      // B operand storage (w, or x for wgrad)
+    void             *out;    // output, row stride N
     const GroupEntry *groups; // [group_num], device memory
     int               group_num;
     int               total_tiles; // output tiles over all groups
@@ -24,6 +28,8 @@ struct KernelArgs {
     int               k_tiles;     // ceil(K / kTileK)
     int               n_xcd;       // XCDs the grid is spread over (1 = no remap)
     int               band;        // M-tiles per band of the in-group tile order
+    int               lda, ldb;    // row strides (elements) of the A and B storage
+    int               m_out;       // wgrad: output rows per group (0 otherwise)
     const int        *d_total;     // device tile count (device-resident group sizes), or null:
                                    // then total_tiles holds it
 };
@@ -38,11 +44,13 @@ struct TableHeader {
 
 // Whether a launch takes the cross-tile pipeline variant (several tiles per workgroup, enough
 // K steps) rather than a prologue and an LDS-staged epilogue per tile.
-bool uses_cross_tile(const KernelArgs &args, int grid);
+bool uses_cross_tile(const KernelArgs &args, int grid, int mode = 0);
 
 // Enqueue the persistent grouped GEMM: `grid` workgroups of 256 threads on `stream`.
-// fp16 selects the f16 MFMA, otherwise bf16. Returns the launch status.
-hipError_t launch_grouped_gemm(const KernelArgs &args, bool fp16, int grid, hipStream_t stream);
+// fp16 selects the f16 MFMA, otherwise bf16; mode 0 forward, 1 dgrad, 2 wgrad.
+// Returns the launch status.
+hipError_t launch_grouped_gemm(const KernelArgs &args, bool fp16, int grid, hipStream_t stream,
+                               int mode = 0);
 
 // Build the group table on the device from device-resident group sizes: lens[group_num]
 // (int64 rows) and offs[group_num + 1] (int64 first rows) or null for back-to-back groups.

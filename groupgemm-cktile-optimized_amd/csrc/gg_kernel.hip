@@ -117,90 +117,121 @@ constexpr int a_stage(int s) { return s * kOpBytes; }
 constexpr int b_stage(int s) { return (kAStages + s) * kOpBytes; }
 
 // ---------------------------------------------------------------------------------------
+// Operand layouts. K-major: the contraction index runs along each stored row (x and w of the
+// forward op, grad_out of dgrad); a 16-row fragment k-half is one ds_read_b128. MN-major: the
+// contraction index is the stored row index (w of dgrad, grad_out and x of wgrad); a fragment
+// k-half is two ds_read_b64_tr_b16, each giving 4 consecutive contraction values per lane.
+// ---------------------------------------------------------------------------------------
+enum Mode : int {
+    kFwd   = 0, // out[g] = x[g] @ w[g]^T                       A = x (K-major),  B = w (K-major)
+    kDgrad = 1, // grad_x[g] = grad_out[g] @ w[g]               A = grad_out (K), B = w (MN)
+    kWgrad = 2  // grad_w[g] = grad_out[g]^T @ x[g], K = M_g    A = grad_out (MN), B = x (MN)
+};
+constexpr bool mode_a_mn(int m) { return m == kWgrad; }
+constexpr bool mode_b_mn(int m) { return m != kFwd; }
+// LDS reads of one 16-row fragment over both k-halves.
+constexpr int reads_per_frag(bool mn) { return mn ? 4 : 2; }
+
+// ---------------------------------------------------------------------------------------
 // Slot plan of one K step. Row mi (0..7) issues 16 MFMAs, idx = kh * 8 + ni; each function
 // says which memory operation follows MFMA idx of row mi (-1: none). LDS reads sit after odd
 // MFMAs, DMAs after even ones, so no MFMA gap holds more than one memory operation.
+// NA / NB: LDS reads per fragment of A / B (2 K-major, 4 MN-major); a read op index r is the
+// k-half (K-major) or k-half * 2 + half (MN-major).
 // ---------------------------------------------------------------------------------------
-constexpr int kBarRow = 7, kBarIdx = GG_BAR_IDX; // the step's barrier follows this MFMA
-static_assert(kBarIdx >= 4 && kBarIdx <= 11 && kBarIdx % 2 == 1, "barrier slot");
+constexpr int kBarRow = 7; // the step's barrier follows MFMA Plan::bar of this row
+static_assert(GG_BAR_IDX >= 5 && GG_BAR_IDX <= 11 && GG_BAR_IDX % 2 == 1, "barrier slot");
 
-// x fragments of row mi+1 (k-half kh) into the register ring.
-constexpr int plan_read_a_next(int mi, int idx) {
-    return (mi < 7 && (idx == 1 || idx == 3)) ? idx / 2 : -1;
-}
-// w fragments of step kt+1, column block ni = mi, k-half kh (rows 0-6 after MFMAs 5 and 7,
-// row 7 after 1 and 3 so they are complete before the barrier).
-constexpr int plan_read_b_next(int mi, int idx) {
-    if (mi < 7)
-        return idx == 5 ? 0 : idx == 7 ? 1 : -1;
-    return idx == 1 ? 0 : idx == 3 ? 1 : -1;
-}
-// x fragments of row 0 of step kt+1, right after the barrier.
-constexpr int plan_read_a_row0(int mi, int idx) {
-    constexpr int first = GG_ROW0_AT_BAR ? kBarIdx : kBarIdx + 2;
-    return (mi == 7 && (idx == first || idx == first + 2)) ? (idx - first) / 2 : -1;
-}
-// DMA j of A(kt+1), j = kEarlyA..7: GG_A_PER_ROW per row from row 0.
-constexpr int plan_load_a(int mi, int idx) {
-    constexpr int per = GG_A_PER_ROW, step = 16 / per;
-    if (idx % step != 0)
-        return -1;
-    const int j = kEarlyA + mi * per + idx / step;
-    return j < kLoads ? j : -1;
-}
-// DMA j of B(kt+3): two per row in rows GG_B_ROW0 .. +3.
-constexpr int plan_load_b(int mi, int idx) {
-    return (mi >= GG_B_ROW0 && mi < GG_B_ROW0 + 4 && (idx == GG_B_SLOT0 || idx == GG_B_SLOT0 + 8))
-               ? (mi - GG_B_ROW0) * 2 + (idx - GG_B_SLOT0) / 8
-               : -1;
-}
-// DMA j < kEarlyA of A(kt+2): the first even slots of row 7 after the barrier (A(kt)'s
-// stage is free once every wave passed it).
-constexpr int plan_load_a_early(int mi, int idx) {
-    const int j = (idx - (kBarIdx + 1)) / 2;
-    return (mi == 7 && idx > kBarIdx && idx % 2 == 0 && j < kEarlyA) ? j : -1;
-}
-// The DMA that follows MFMA idx of row mi: 0 none, 1 A(kt+1), 2 B(kt+3), 3 A(kt+2).
-constexpr int plan_dma_kind(int mi, int idx) {
-    return plan_load_a(mi, idx) >= 0 ? 1 : plan_load_b(mi, idx) >= 0 ? 2 : plan_load_a_early(mi, idx) >= 0 ? 3 : 0;
-}
-constexpr int plan_dma_j(int mi, int idx) {
-    return plan_load_a(mi, idx) >= 0 ? plan_load_a(mi, idx)
-           : plan_load_b(mi, idx) >= 0 ? plan_load_b(mi, idx) : plan_load_a_early(mi, idx);
-}
-constexpr bool one_dma_per_slot() {
-    for (int p = 0; p < 8 * 16; ++p)
-        if ((plan_load_a(p / 16, p % 16) >= 0) + (plan_load_b(p / 16, p % 16) >= 0) +
-                (plan_load_a_early(p / 16, p % 16) >= 0) > 1)
-            return false;
-    return true;
-}
-static_assert(one_dma_per_slot(), "at most one DMA per MFMA gap");
-// DMAs that may still be in flight at the barrier: those issued after the last A(kt+1) DMA.
-// Loads complete in order, so vmcnt(this) means all of A(kt+1) (and everything older) landed.
-// Stores are never counted here, wherever they sit in the step: a store may complete before an
-// older load, so counting one could let the barrier pass while an A(kt+1) DMA is in flight.
-// With loads alone counted, pending stores only make the wait longer.
-constexpr int vm_at_barrier() {
-    int last_a = -1;
-    for (int p = 0; p < 8 * 16; ++p)
-        if (plan_load_a(p / 16, p % 16) >= 0)
-            last_a = p;
-    int n = 0;
-    for (int p = last_a + 1; p < kBarRow * 16 + kBarIdx; ++p)
-        n += (plan_load_b(p / 16, p % 16) >= 0) + (plan_load_a_early(p / 16, p % 16) >= 0);
-    return n;
-}
-constexpr int count_plan(int (*f)(int, int)) {
-    int n = 0;
-    for (int p = 0; p < 8 * 16; ++p)
-        n += f(p / 16, p % 16) >= 0;
-    return n;
-}
-static_assert(count_plan(plan_load_a) == kLoads - kEarlyA, "A DMAs");
-static_assert(count_plan(plan_load_b) == kLoads, "B DMAs");
-static_assert(count_plan(plan_load_a_early) == kEarlyA, "early A DMAs");
-static_assert(count_plan(plan_read_b_next) == 16, "w fragments of the next step");
+template <int NA, int NB> struct Plan {
+    // The w fragments of row 7 are read before the barrier, at MFMAs 1 .. 2 NB - 1.
+    static constexpr int bar = GG_BAR_IDX > 2 * NB + 1 ? GG_BAR_IDX : 2 * NB + 1;
+    static constexpr int row0_first = GG_ROW0_AT_BAR ? bar : bar + 2;
+    static_assert(row0_first + 2 * (NA - 1) <= 15, "row-0 reads fit in row 7");
+
+    // x fragments of row mi+1 into the register ring: the first NA odd slots of rows 0-6.
+    static constexpr int read_a_next(int mi, int idx) {
+        return (mi < 7 && idx % 2 == 1 && idx < 2 * NA) ? idx / 2 : -1;
+    }
+    // w fragments of step kt+1, column block ni = mi: the next NB odd slots of rows 0-6; in
+    // row 7 the first NB odd slots, so they are complete before the barrier.
+    static constexpr int read_b_next(int mi, int idx) {
+        if (idx % 2 == 0)
+            return -1;
+        if (mi < 7)
+            return (idx >= 2 * NA && idx < 2 * (NA + NB)) ? (idx - 2 * NA) / 2 : -1;
+        return idx < 2 * NB ? idx / 2 : -1;
+    }
+    // x fragments of row 0 of step kt+1, right after the barrier.
+    static constexpr int read_a_row0(int mi, int idx) {
+        return (mi == 7 && idx % 2 == 1 && idx >= row0_first && idx < row0_first + 2 * NA)
+                   ? (idx - row0_first) / 2
+                   : -1;
+    }
+    // DMA j of A(kt+1), j = kEarlyA..7: GG_A_PER_ROW per row from row 0.
+    static constexpr int load_a(int mi, int idx) {
+        constexpr int per = GG_A_PER_ROW, step = 16 / per;
+        if (idx % step != 0)
+            return -1;
+        const int j = kEarlyA + mi * per + idx / step;
+        return j < kLoads ? j : -1;
+    }
+    // DMA j of B(kt+3): two per row in rows GG_B_ROW0 .. +3.
+    static constexpr int load_b(int mi, int idx) {
+        return (mi >= GG_B_ROW0 && mi < GG_B_ROW0 + 4 && (idx == GG_B_SLOT0 || idx == GG_B_SLOT0 + 8))
+                   ? (mi - GG_B_ROW0) * 2 + (idx - GG_B_SLOT0) / 8
+                   : -1;
+    }
+    // DMA j < kEarlyA of A(kt+2): the first even slots of row 7 after the barrier (A(kt)'s
+    // stage is free once every wave passed it).
+    static constexpr int load_a_early(int mi, int idx) {
+        const int j = (idx - (bar + 1)) / 2;
+        return (mi == 7 && idx > bar && idx % 2 == 0 && j < kEarlyA) ? j : -1;
+    }
+    // The DMA that follows MFMA idx of row mi: 0 none, 1 A(kt+1), 2 B(kt+3), 3 A(kt+2).
+    static constexpr int dma_kind(int mi, int idx) {
+        return load_a(mi, idx) >= 0 ? 1 : load_b(mi, idx) >= 0 ? 2 : load_a_early(mi, idx) >= 0 ? 3 : 0;
+    }
+    static constexpr int dma_j(int mi, int idx) {
+        return load_a(mi, idx) >= 0 ? load_a(mi, idx) : load_b(mi, idx) >= 0 ? load_b(mi, idx) : load_a_early(mi, idx);
+    }
+    // DMAs that may still be in flight at the barrier: those issued after the last A(kt+1)
+    // DMA. Loads complete in order, so vmcnt(this) means all of A(kt+1) (and everything older)
+    // landed. Stores are never counted here, wherever they sit in the step: a store may
+    // complete before an older load, so counting one could let the barrier pass while an
+    // A(kt+1) DMA is in flight. With loads alone counted, pending stores only make the wait
+    // longer.
+    static constexpr int vm_at_barrier() {
+        int last_a = -1;
+        for (int p = 0; p < 8 * 16; ++p)
+            if (load_a(p / 16, p % 16) >= 0)
+                last_a = p;
+        int n = 0;
+        for (int p = last_a + 1; p < kBarRow * 16 + bar; ++p)
+            n += (load_b(p / 16, p % 16) >= 0) + (load_a_early(p / 16, p % 16) >= 0);
+        return n;
+    }
+    template <typename F> static constexpr int count(F f) {
+        int n = 0;
+        for (int p = 0; p < 8 * 16; ++p)
+            n += f(p / 16, p % 16) >= 0;
+        return n;
+    }
+    static constexpr bool check() {
+        for (int p = 0; p < 8 * 16; ++p) {
+            const int mi = p / 16, idx = p % 16;
+            const int dmas  = (load_a(mi, idx) >= 0) + (load_b(mi, idx) >= 0) + (load_a_early(mi, idx) >= 0);
+            const int reads = (read_a_next(mi, idx) >= 0) + (read_b_next(mi, idx) >= 0) +
+                              (read_a_row0(mi, idx) >= 0);
+            if (dmas > 1 || reads > 1 || (dmas && reads))
+                return false;
+        }
+        return count(load_a) == kLoads - kEarlyA && count(load_b) == kLoads &&
+               count(load_a_early) == kEarlyA && count(read_b_next) == 8 * NB &&
+               count(read_a_next) == 7 * NA && count(read_a_row0) == NA;
+    }
+};
+static_assert(Plan<2, 2>::check() && Plan<2, 4>::check() && Plan<4, 4>::check(), "slot plans");
+static_assert(Plan<2, 2>::bar == GG_BAR_IDX, "forward plan keeps the tuned barrier slot");
 
 // ---------------------------------------------------------------------------------------
 // Device primitives
@@ -312,11 +343,15 @@ constexpr int plan_epi(int mi, int idx) {
     return (mi < 7 && idx % 4 == 2) ? (idx - 2) / 4 : -1;
 }
 
+// MODE: forward, dgrad or wgrad (operand layouts and tile mapping, see Mode and KernelArgs).
 // CROSS: cross-tile pipeline (needs k_tiles >= kCrossMinSteps); otherwise every tile starts
 // with a prologue and ends with the LDS-staged epilogue.
-template <bool F16, bool CROSS>
+template <bool F16, bool CROSS, int MODE>
 __global__ void __launch_bounds__(kThreads, 1) __attribute__((amdgpu_waves_per_eu(1, 1)))
 grouped_gemm_kernel(const KernelArgs args) {
+    constexpr bool A_MN = mode_a_mn(MODE), B_MN = mode_b_mn(MODE);
+    using P = Plan<reads_per_frag(A_MN), reads_per_frag(B_MN)>;
+    static_assert(!(CROSS && MODE == kWgrad), "wgrad has a K-step count per group");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kLdsBytes];
     typedef __attribute__((address_space(3))) uint8_t lds_u8;
     const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8 *)smem));
@@ -324,32 +359,53 @@ grouped_gemm_kernel(const KernelArgs args) {
     const int lane = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6) & 3;
     const int wm = wave >> 1, wn = wave & 1;
-    const int K = args.k, N = args.n, T = args.k_tiles;
+    const int K = args.k, N = args.n;
+    int       T = args.k_tiles; // K steps of the current tile (per group for wgrad)
     // Tile count: from the kernel arguments, or from a group table built on the device.
     const int total_tiles = args.d_total != nullptr
                                 ? __builtin_amdgcn_readfirstlane(*args.d_total)
                                 : args.total_tiles;
 
-    // DMA j of an operand step covers tile rows j*32 + wave*8 .. +8; lane -> row lane/8,
-    // logical chunk (lane%8) ^ (lane/8). x and w rows have the same length K, so one set of
-    // offsets serves both operands and every tile.
+    // DMA lane offsets within a tile's K step (the tile origin is in the buffer resource).
+    // K-major operand, row stride ld: DMA j covers tile rows j*32 + wave*8 .. +8; lane -> row
+    // lane/8, logical chunk (lane%8) ^ (lane/8).
+    // MN-major operand, row stride ld, stored rows = contraction index: DMA j covers
+    // contraction rows 4 (2j + wave/2) .. +4 and tile columns 128 (wave%2) .. +128. In LDS the
+    // step is 128-byte blocks of 4 rows x 16 columns, block (row/4, column/16) at byte
+    // 128 (16 (row/4) + column/16), so the DMA's 1 KB lands at 1024 (4j + wave) as for a
+    // K-major operand; lane -> block column 8 (wave%2) + lane/8, row (lane%8)/2, 8 columns
+    // at 8 (lane%2). A lane's column does not depend on j.
     const int ld_row   = lane >> 3;
     const int ld_chunk = (lane & 7) ^ ld_row;
-    int voff[kLoads];
+    const int mn_col   = ((wave & 1) * 8 + (lane >> 3)) * 16 + (lane & 1) * 8;
+    auto      dma_off  = [&](bool mn, int j, int ld) {
+        return mn ? ((4 * (2 * j + (wave >> 1)) + ((lane & 7) >> 1)) * ld + mn_col) * 2
+                  : ((j * 32 + wave * 8 + ld_row) * ld + ld_chunk * 8) * 2;
+    };
+    // voff[0]: A's offsets; voff[1]: B's (the forward op shares A's: both row strides are K).
+    constexpr bool kSameOff = MODE == kFwd;
+    int            voff[kSameOff ? 1 : 2][kLoads];
     sfor<0, kLoads>([&](auto j) {
-        voff[j] = ((j * 32 + wave * 8 + ld_row) * K + ld_chunk * 8) * 2;
+        voff[0][j] = dma_off(A_MN, j, args.lda);
+        if constexpr (!kSameOff)
+            voff[1][j] = dma_off(B_MN, j, args.ldb);
     });
     // Last K step when K % 64 != 0: chunks at k >= K get an offset past every bound.
     const int k_last    = K - (T - 1) * kTileK; // valid K of the last step, 8..64
     int       ktail_bad = (ld_chunk * 8 >= k_last) ? static_cast<int>(0x80000000u) : 0;
 
-    // Fragment reads: lane -> row lane%16 of a 16-row block, logical chunk kh*4 + lane/16.
+    // Fragment reads. K-major: lane -> row lane%16 of a 16-row block, logical chunk
+    // kh*4 + lane/16 (one base per k-half). MN-major: ds_read_b64_tr_b16 gives lane i of each
+    // 16-lane group column i of 4 consecutive rows when source lane s of the group points at
+    // row s/4, column 4 (s%4): lane l reads block (row 8 (l/16) + 4 half + 32 kh, column
+    // 16 blk) at byte 8 (l%16) of it, i.e. base + 16384 kh + 2048 half + 128 blk.
     const int fr_row = lane & 15, fr_q = lane >> 4;
     int frag_a[2], frag_b[2];
     sfor<0, 2>([&](auto kh) {
         const int off = fr_row * kRowBytes + (((kh * 4 + fr_q) ^ (fr_row & 7)) * 16);
-        frag_a[kh]    = wm * 128 * kRowBytes + off;
-        frag_b[kh]    = wn * 128 * kRowBytes + off;
+        const int mn  = (lane >> 4) * 4096 + (lane & 15) * 8;
+        frag_a[kh]    = A_MN ? wm * 1024 + mn : wm * 128 * kRowBytes + off;
+        frag_b[kh]    = B_MN ? wn * 1024 + mn : wn * 128 * kRowBytes + off;
     });
 
     // Register epilogue: in store s = 2h + half of a 16-row block, lane l writes 16 bytes of
@@ -382,7 +438,11 @@ grouped_gemm_kernel(const KernelArgs args) {
     };
     // Re-materialise loop-invariant offsets at the top of every loop body (see fresh_v).
     auto refresh = [&]() {
-        sfor<0, kLoads>([&](auto j) { fresh_v(voff[j]); });
+        sfor<0, kLoads>([&](auto j) {
+            fresh_v(voff[0][j]);
+            if constexpr (!kSameOff)
+                fresh_v(voff[1][j]);
+        });
         fresh_v(ktail_bad);
         fresh_v(voffc);
         sfor<0, 2>([&](auto L) {
@@ -395,6 +455,23 @@ grouped_gemm_kernel(const KernelArgs args) {
         });
     };
     auto lds_read = [&](int off) -> i32x4 { return *reinterpret_cast<const i32x4 *>(smem + off); };
+    typedef short i16x4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+    auto lds_read_tr = [&](int off) -> u32x2 {
+        return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(smem + off)));
+    };
+    // LDS read op r (Plan numbering) of the fragment of 16-row block blk into f (per k-half),
+    // from the logical stage whose read bases are rd.
+    auto read_frag = [&]<bool MN, int R>(i32x4(&f)[2], const int(&rd)[2], auto blk) {
+        if constexpr (!MN) {
+            f[R] = lds_read(rd[R] + blk * 16 * kRowBytes);
+        } else {
+            constexpr int kh = R >> 1, half = R & 1;
+            const u32x2   v  = lds_read_tr(rd[0] + kh * 16384 + half * 2048 + blk * 128);
+            f[kh][2 * half]     = static_cast<int>(v[0]);
+            f[kh][2 * half + 1] = static_cast<int>(v[1]);
+        }
+    };
 
     f32x4 acc[8][8];
     i32x4 fa[2][2];    // x fragments: row ring x k-half
@@ -402,26 +479,55 @@ grouped_gemm_kernel(const KernelArgs args) {
 
     // One output tile: its DMA sources and where its C block goes.
     struct Tile {
-        i32x4     rsrc_a, rsrc_b; // x rows / w rows of the tile, bounded to the valid rows
+        i32x4     rsrc_a, rsrc_b; // A / B storage of the tile, bounded to its valid rows
         uint16_t *c_ptr;          // output block origin
         int       m_valid, n_valid;
+        int       o0a, o0b;       // MN-major operands: first stored column of the tile
+        int       T;              // K steps (wgrad: of the tile's group, at least 1)
     };
-    int  g         = 0; // group hint of locate_tile (logical tiles only grow)
-    auto make_tile = [&](int t) -> Tile {
+    const int bad_off = static_cast<int>(0x80000000u);
+    int       g       = 0; // group hint of locate_tile (logical tiles only grow)
+    auto      make_tile = [&](int t) -> Tile {
         const int L = xcd_remap(t, total_tiles, gridDim.x, args.n_xcd);
         int       tm, tn;
-        locate_tile(L, args.groups, args.group_num, args.n_tiles, args.band, &g, &tm, &tn);
+        locate_tile(L, args.groups, args.group_num, args.n_tiles, args.band, &g, &tm, &tn,
+                    MODE == kWgrad ? args.m_out : 0);
         const GroupEntry ge = args.groups[g];
+        const uint16_t  *xa = static_cast<const uint16_t *>(args.x);
+        const uint16_t  *wb = static_cast<const uint16_t *>(args.w);
         Tile             tl;
-        tl.m_valid         = min(kTileM, ge.m - tm * kTileM);
         tl.n_valid         = min(kTileN, N - tn * kTileN);
-        const int64_t row0 = ge.row0 + static_cast<int64_t>(tm) * kTileM;
         const int64_t col0 = static_cast<int64_t>(tn) * kTileN;
-        tl.rsrc_a = dma_rsrc(static_cast<const uint16_t *>(args.x) + row0 * K,
-                             static_cast<uint32_t>(tl.m_valid) * K * 2);
-        tl.rsrc_b = dma_rsrc(static_cast<const uint16_t *>(args.w) + (static_cast<int64_t>(g) * N + col0) * K,
-                             static_cast<uint32_t>(tl.n_valid) * K * 2);
-        tl.c_ptr  = static_cast<uint16_t *>(args.out) + row0 * N + col0;
+        tl.o0a = tl.o0b = 0;
+        tl.T            = T;
+        if constexpr (MODE == kWgrad) {
+            // A^T = grad_out rows of the group, columns tm*256..; B^T = x rows, columns tn*256..
+            const int64_t o0a = static_cast<int64_t>(tm) * kTileM;
+            const int64_t ma  = static_cast<int64_t>(ge.m) * args.lda - o0a;
+            const int64_t mb  = static_cast<int64_t>(ge.m) * args.ldb - col0;
+            tl.m_valid = min(kTileM, args.m_out - tm * kTileM);
+            tl.rsrc_a  = dma_rsrc(xa + ge.row0 * args.lda + o0a, static_cast<uint32_t>(ma > 0 ? ma * 2 : 0));
+            tl.rsrc_b  = dma_rsrc(wb + ge.row0 * args.ldb + col0, static_cast<uint32_t>(mb > 0 ? mb * 2 : 0));
+            tl.o0a     = static_cast<int>(o0a);
+            tl.o0b     = static_cast<int>(col0);
+            tl.c_ptr   = static_cast<uint16_t *>(args.out) +
+                       (static_cast<int64_t>(g) * args.m_out + o0a) * N + col0;
+            tl.T = max(1, static_cast<int>(cdiv(ge.m, kTileK)));
+        } else {
+            tl.m_valid         = min(kTileM, ge.m - tm * kTileM);
+            const int64_t row0 = ge.row0 + static_cast<int64_t>(tm) * kTileM;
+            tl.rsrc_a = dma_rsrc(xa + row0 * args.lda, static_cast<uint32_t>(tl.m_valid) * args.lda * 2);
+            if constexpr (MODE == kFwd) {
+                tl.rsrc_b = dma_rsrc(wb + (static_cast<int64_t>(g) * N + col0) * args.ldb,
+                                     static_cast<uint32_t>(tl.n_valid) * args.ldb * 2);
+            } else {
+                // w[g] stored K x N: columns col0.. of all K rows (the end of w[g] bounds it)
+                const int64_t per_g = static_cast<int64_t>(K) * args.ldb;
+                tl.rsrc_b = dma_rsrc(wb + g * per_g + col0, static_cast<uint32_t>((per_g - col0) * 2));
+                tl.o0b = static_cast<int>(col0);
+            }
+            tl.c_ptr = static_cast<uint16_t *>(args.out) + row0 * N + col0;
+        }
         return tl;
     };
     auto c_rsrc = [&](const Tile &tl) {
@@ -435,51 +541,85 @@ grouped_gemm_kernel(const KernelArgs args) {
     if (t >= total_tiles)
         return;
     Tile cur = make_tile(t), nxt = cur;
+    if constexpr (MODE == kWgrad)
+        T = __builtin_amdgcn_readfirstlane(cur.T);
     bool cross_next = false; // the DMAs past this tile's last K step fetch `nxt`
 
     // Where the DMAs of K step kidx of an operand (false: x, true: w) read from: resource,
     // K offset and the per-lane mask of a partial last step. Unchecked: kidx is a full step of
     // the current tile. Checked: kidx may be the tile's partial last step or lie past it (the
     // next tile's first steps, or nothing). Evaluated once per step and operand stream.
+    // MN-major operands: a K step is 64 stored rows, added to the lane offset (not soffset)
+    // so that rows past the contraction length fall outside the resource; lane columns past
+    // the row get an out-of-range offset (mask). K-major: the K step is soffset, and the
+    // partial last step's chunks past K get the out-of-range offset.
     struct DmaSrc {
         i32x4 rs;
-        int   so, mask;
+        int   so, vadd, mask;
     };
     auto dma_src = [&](auto b_op, int kidx, auto checked) -> DmaSrc {
         constexpr bool B  = decltype(b_op)::value;
+        constexpr bool MN = B ? B_MN : A_MN;
+        const int      ld = B ? args.ldb : args.lda;
         i32x4          rc = cur.rsrc_a, rn = nxt.rsrc_a;
+        int            oc = cur.o0a, on = nxt.o0a;
         if constexpr (B) {
             rc = cur.rsrc_b;
             rn = nxt.rsrc_b;
+            oc = cur.o0b;
+            on = nxt.o0b;
         }
         DmaSrc d;
         if constexpr (decltype(checked)::value) {
             const bool in_cur = kidx < T;
             const int  koff   = in_cur ? kidx : kidx - T;
             d.rs              = in_cur ? rc : (cross_next ? rn : rsrc_0);
-            d.so              = koff * kRowBytes;
-            d.mask            = koff == T - 1 ? ktail_bad : 0;
+            if constexpr (MN) {
+                d.so   = 0;
+                d.vadd = koff * kTileK * ld * 2;
+                d.mask = (in_cur ? oc : on) + mn_col >= ld ? bad_off : 0;
+            } else {
+                d.so   = koff * kRowBytes;
+                d.vadd = 0;
+                d.mask = koff == T - 1 ? ktail_bad : 0;
+            }
         } else {
-            d.rs   = rc;
-            d.so   = kidx * kRowBytes;
-            d.mask = 0;
+            d.rs = rc;
+            if constexpr (MN) {
+                d.so   = 0;
+                d.vadd = kidx * kTileK * ld * 2;
+                d.mask = oc + mn_col >= ld ? bad_off : 0;
+            } else {
+                d.so   = kidx * kRowBytes;
+                d.vadd = 0;
+                d.mask = 0;
+            }
         }
         return d;
+    };
+    // Lane offset of DMA j of operand b_op for source d.
+    auto dma_voff = [&](auto b_op, auto j, const DmaSrc &d, auto checked) -> int {
+        constexpr bool B  = decltype(b_op)::value;
+        constexpr bool MN = B ? B_MN : A_MN;
+        const int      vo = voff[(B && !kSameOff) ? 1 : 0][j];
+        if constexpr (MN)
+            return (vo + d.vadd) | d.mask;
+        else if constexpr (decltype(checked)::value)
+            return vo | d.mask;
+        else
+            return vo;
     };
     // DMA with its own M0 write (prologue).
     auto dma_now = [&](uint32_t dst, auto b_op, auto j, int kidx) {
         sched_fence();
         const DmaSrc d = dma_src(b_op, kidx, std::true_type{});
-        dma16(dst + j * 4096, voff[j] | d.mask, d.rs, d.so);
+        dma16(dst + j * 4096, dma_voff(b_op, j, d, std::true_type{}), d.rs, d.so);
         sched_fence();
     };
     // DMA whose M0 was written before the slot's MFMA.
-    auto dma_go = [&](const DmaSrc &d, auto j, auto checked) {
+    auto dma_go = [&](auto b_op, const DmaSrc &d, auto j, auto checked) {
         sched_fence();
-        if constexpr (decltype(checked)::value)
-            dma16_m0(voff[j] | d.mask, d.rs, d.so);
-        else
-            dma16_m0(voff[j], d.rs, d.so);
+        dma16_m0(dma_voff(b_op, j, d, checked), d.rs, d.so);
         sched_fence();
     };
     using A_OP = std::false_type;
@@ -498,9 +638,13 @@ grouped_gemm_kernel(const KernelArgs args) {
     auto finish_prologue = [&]<int VM>() {
         wait_vm_lds_barrier<VM>(); // A(0), B(0), B(1) landed everywhere
         sfor<0, 8>([&](auto ni) {
-            sfor<0, 2>([&](auto kh) { fb[0][ni][kh] = lds_read(b_rd[0][kh] + ni * 16 * kRowBytes); });
+            sfor<0, reads_per_frag(B_MN)>([&](auto r) {
+                read_frag.template operator()<B_MN, r>(fb[0][ni], b_rd[0], ni);
+            });
         });
-        sfor<0, 2>([&](auto kh) { fa[0][kh] = lds_read(a_rd[0][kh]); });
+        sfor<0, reads_per_frag(A_MN)>([&](auto r) {
+            read_frag.template operator()<A_MN, r>(fa[0], a_rd[0], ic<0>{});
+        });
         wait_vm_lds_barrier<63>(); // every wave holds B(0): its stage may be refilled
     };
 
@@ -597,6 +741,9 @@ grouped_gemm_kernel(const KernelArgs args) {
         sched_fence();
     };
     auto step = [&]<int SA, int SB, bool FIRST, bool CHECKED, bool FUSE>(int kt) {
+        // kt is uniform; saying so keeps the checked tail's comparisons and resource selects
+        // scalar when the compiler would otherwise carry kt through a branch merge in a VGPR.
+        kt = __builtin_amdgcn_readfirstlane(kt);
         constexpr int NX = SA ^ 1;
         constexpr int SB_NEXT = (SB + 1) % 3;
         using chk = std::integral_constant<bool, CHECKED>;
@@ -608,7 +755,7 @@ grouped_gemm_kernel(const KernelArgs args) {
             sfor<0, 16>([&](auto idx_) {
                 constexpr int idx = decltype(idx_)::value;
                 constexpr int kh = idx / 8, ni = idx % 8;
-                constexpr int dk = plan_dma_kind(mi, idx), dj = plan_dma_j(mi, idx);
+                constexpr int dk = P::dma_kind(mi, idx), dj = P::dma_j(mi, idx);
                 if constexpr (dk == 1)
                     set_m0<dj * 4096>(a_dst[NX]); // the MFMA below is the wait state
                 else if constexpr (dk == 2)
@@ -621,42 +768,50 @@ grouped_gemm_kernel(const KernelArgs args) {
                 else
                     mfma<F16>(acc[mi][ni], fb[SA][ni][kh], fa[mi & 1][kh]);
                 sched_fence();
-                if constexpr (mi == kBarRow && idx == kBarIdx) {
-                    wait_vm_lds_barrier<vm_at_barrier()>();
+                if constexpr (mi == kBarRow && idx == P::bar) {
+                    wait_vm_lds_barrier<P::vm_at_barrier()>();
                     sched_fence();
                 }
-                if constexpr (plan_read_a_next(mi, idx) >= 0) {
-                    constexpr int h = plan_read_a_next(mi, idx);
-                    fa[(mi + 1) & 1][h] = lds_read(a_rd[SA][h] + (mi + 1) * 16 * kRowBytes);
+                if constexpr (P::read_a_next(mi, idx) >= 0) {
+                    read_frag.template operator()<A_MN, P::read_a_next(mi, idx)>(fa[(mi + 1) & 1], a_rd[SA],
+                                                                                 ic<mi + 1>{});
                     sched_fence();
                 }
-                if constexpr (plan_read_b_next(mi, idx) >= 0) {
-                    constexpr int h = plan_read_b_next(mi, idx);
-                    fb[NX][mi][h] = lds_read(b_rd[SB_NEXT][h] + mi * 16 * kRowBytes);
+                if constexpr (P::read_b_next(mi, idx) >= 0) {
+                    read_frag.template operator()<B_MN, P::read_b_next(mi, idx)>(fb[NX][mi], b_rd[SB_NEXT],
+                                                                                 ic<mi>{});
                     sched_fence();
                 }
-                if constexpr (plan_read_a_row0(mi, idx) >= 0) {
-                    constexpr int h = plan_read_a_row0(mi, idx);
-                    fa[0][h] = lds_read(a_rd[NX][h]);
+                if constexpr (P::read_a_row0(mi, idx) >= 0) {
+                    read_frag.template operator()<A_MN, P::read_a_row0(mi, idx)>(fa[0], a_rd[NX], ic<0>{});
                     sched_fence();
                 }
                 if constexpr (FUSE && plan_epi(mi, idx) >= 0)
                     epi_store(ic<mi + 1>{}, ic<plan_epi(mi, idx)>{});
                 if constexpr (dk == 1)
-                    dma_go(src_a1, ic<dj>{}, chk{});
+                    dma_go(A_OP{}, src_a1, ic<dj>{}, chk{});
                 else if constexpr (dk == 2)
-                    dma_go(src_b3, ic<dj>{}, chk{});
+                    dma_go(B_OP{}, src_b3, ic<dj>{}, chk{});
                 else if constexpr (dk == 3)
-                    dma_go(src_a2, ic<dj>{}, chk{});
+                    dma_go(A_OP{}, src_a2, ic<dj>{}, chk{});
             });
         });
     };
 
     // ---- the persistent loop ------------------------------------------------------------------
-    set_stages();
-    issue_prologue();
-    finish_prologue.template operator()<kLoads + kEarlyA>();
+    // Cross-tile: one prologue, before the first tile. Per-tile: a prologue at the top of every
+    // tile (a single copy of it, so the fragment registers have one definition in the loop).
+    if constexpr (CROSS) {
+        set_stages();
+        issue_prologue();
+        finish_prologue.template operator()<kLoads + kEarlyA>();
+    }
     while (true) {
+        if constexpr (!CROSS) {
+            set_stages();
+            issue_prologue();
+            finish_prologue.template operator()<kLoads + kEarlyA>();
+        }
         refresh();
         if constexpr (CROSS) {
             // First step: stores the previous tile's accumulators while it overwrites them (to
@@ -712,16 +867,15 @@ grouped_gemm_kernel(const KernelArgs args) {
             }
         }
         if constexpr (!CROSS) {
-            // Store this tile through LDS, then start the next one cold.
+            // Store this tile through LDS; the next one starts cold at the top of the loop (the
+            // stores were issued before its DMAs and complete first).
             epilogue_lds(cur);
             if (!more)
                 return;
             t   = t_next;
             cur = make_tile(t);
-            set_stages();
-            // (the stores were issued before these DMAs and complete first)
-            issue_prologue();
-            finish_prologue.template operator()<kLoads + kEarlyA>();
+            if constexpr (MODE == kWgrad)
+                T = __builtin_amdgcn_readfirstlane(cur.T);
         }
     }
     if constexpr (CROSS)
@@ -822,7 +976,9 @@ template <bool F16> __global__ void fill_randn_kernel(uint16_t *p, size_t n, uin
 
 } // namespace
 
-bool uses_cross_tile(const KernelArgs &args, int grid) {
+bool uses_cross_tile(const KernelArgs &args, int grid, int mode) {
+    if (mode == kWgrad)
+        return false;
     // Workgroups with a single tile gain nothing from the cross-tile pipeline.
     // (a device-built table's tile count is unknown on the host: take the cross-tile variant,
     // which also handles workgroups with a single tile)
@@ -830,17 +986,33 @@ bool uses_cross_tile(const KernelArgs &args, int grid) {
            (args.d_total != nullptr || args.total_tiles > grid);
 }
 
-hipError_t launch_grouped_gemm(const KernelArgs &args, bool fp16, int grid, hipStream_t stream) {
-    const bool cross = uses_cross_tile(args, grid);
-    const dim3 g(grid), b(kThreads);
-    if (fp16 && cross)
-        hipLaunchKernelGGL((grouped_gemm_kernel<true, true>), g, b, 0, stream, args);
-    else if (fp16)
-        hipLaunchKernelGGL((grouped_gemm_kernel<true, false>), g, b, 0, stream, args);
+template <bool F16, int MODE>
+void launch_mode(const KernelArgs &args, bool cross, dim3 g, dim3 b, hipStream_t stream) {
+    if constexpr (MODE == kWgrad)
+        hipLaunchKernelGGL((grouped_gemm_kernel<F16, false, MODE>), g, b, 0, stream, args);
     else if (cross)
-        hipLaunchKernelGGL((grouped_gemm_kernel<false, true>), g, b, 0, stream, args);
+        hipLaunchKernelGGL((grouped_gemm_kernel<F16, true, MODE>), g, b, 0, stream, args);
     else
-        hipLaunchKernelGGL((grouped_gemm_kernel<false, false>), g, b, 0, stream, args);
+        hipLaunchKernelGGL((grouped_gemm_kernel<F16, false, MODE>), g, b, 0, stream, args);
+}
+
+template <bool F16>
+void launch_dtype(const KernelArgs &args, bool cross, int mode, dim3 g, dim3 b, hipStream_t stream) {
+    if (mode == kDgrad)
+        launch_mode<F16, kDgrad>(args, cross, g, b, stream);
+    else if (mode == kWgrad)
+        launch_mode<F16, kWgrad>(args, cross, g, b, stream);
+    else
+        launch_mode<F16, kFwd>(args, cross, g, b, stream);
+}
+
+hipError_t launch_grouped_gemm(const KernelArgs &args, bool fp16, int grid, hipStream_t stream, int mode) {
+    const bool cross = uses_cross_tile(args, grid, mode);
+    const dim3 g(grid), b(kThreads);
+    if (fp16)
+        launch_dtype<true>(args, cross, mode, g, b, stream);
+    else
+        launch_dtype<false>(args, cross, mode, g, b, stream);
     return hipGetLastError();
 }
 

@@ -78,9 +78,11 @@ struct GroupEntry {
 };
 
 // Fill `table` (group_num entries) from the group sizes; returns the total tile count, or
-// -1 if a size is negative or a count overflows 32 bits.
+// -1 if a size is negative or a count overflows 32 bits. out_rows > 0: every group's output
+// has out_rows rows whatever its size (the weight gradient, one [out_rows, N] block per group,
+// zero for an empty group); otherwise a group's output rows are its own rows.
 inline int64_t build_group_table(const int64_t *group_m, int group_num, int64_t n_tiles,
-                                 GroupEntry *table) {
+                                 GroupEntry *table, int64_t out_rows = 0) {
     int64_t row = 0, tiles = 0;
     for (int g = 0; g < group_num; ++g) {
         if (group_m[g] < 0 || group_m[g] > INT32_MAX)
@@ -88,7 +90,7 @@ inline int64_t build_group_table(const int64_t *group_m, int group_num, int64_t 
         table[g].row0  = row;
         table[g].m     = static_cast<int32_t>(group_m[g]);
         table[g].tile0 = static_cast<int32_t>(tiles);
-        tiles += cdiv(group_m[g], kTileM) * n_tiles;
+        tiles += cdiv(out_rows > 0 ? out_rows : group_m[g], kTileM) * n_tiles;
         row += group_m[g];
         if (tiles > INT32_MAX)
             return -1;
@@ -98,14 +100,14 @@ inline int64_t build_group_table(const int64_t *group_m, int group_num, int64_t 
 
 // Group and (M-tile, N-tile) of logical tile L. *g is a hint: the group of a smaller L seen
 // before (0 at the start); logical tiles only grow for one workgroup, so the scan only moves
-// forward. Empty groups own no tiles and are stepped over.
+// forward. Empty groups own no tiles and are stepped over. out_rows as in build_group_table.
 GG_HD void locate_tile(int L, const GroupEntry *groups, int group_num, int n_tiles, int band,
-                       int *g, int *tm, int *tn) {
+                       int *g, int *tm, int *tn, int out_rows = 0) {
     int gi = *g;
     while (gi + 1 < group_num && groups[gi + 1].tile0 <= L)
         ++gi;
     *g                = gi;
-    const int m_tiles = (groups[gi].m + kTileM - 1) / kTileM;
+    const int m_tiles = ((out_rows > 0 ? out_rows : groups[gi].m) + kTileM - 1) / kTileM;
     band_coords(L - groups[gi].tile0, m_tiles, n_tiles, band, tm, tn);
 }
 

@@ -68,6 +68,27 @@ int gg_prepare(int dtype, int group_num, int64_t n, int64_t k, const int64_t *gr
  */
 int gg_run(const gg_plan *plan, void *stream);
 
+/*
+ * Backward GEMMs of the same op, for the MoE layer's backward pass (the reference's driver
+ * times the forward only, README.md:35-36; the vendored Primus-Turbo grouped GEMM has both with
+ * these shapes, third_party/primus_turbo/kernels/hipblaslt_grouped_gemm.cu:80-97, 206-214, and
+ * a variable-K CK entry point for the weight gradient,
+ * third_party/primus_turbo/include/primus_turbo/grouped_gemm.h:115-116).
+ *
+ * gg_prepare_dgrad: grad_x[rows of g] [M_g, k] = grad_out[rows of g] [M_g, n] @ w[g] [n, k]
+ *   grad_out [sum(group_m), n], w [group_num, n, k] (the forward's w), grad_x [sum(group_m), k].
+ * gg_prepare_wgrad: grad_w[g] [n, k] = grad_out[rows of g]^T [n, M_g] @ x[rows of g] [M_g, k],
+ *   grad_out [sum(group_m), n], x [sum(group_m), k], grad_w [group_num, n, k]; zero for an empty
+ *   group (the contraction length of each group is its row count).
+ * Same conventions as gg_prepare (host group_m, status codes, gg_run / gg_release), and the
+ * same N/A rules: n and k multiples of 8 and at most 2097152, 16-byte aligned buffers; further
+ * N/A: one group's w (dgrad) or one group's rows of grad_out or x (wgrad) of 2 GiB or more.
+ */
+int gg_prepare_dgrad(int dtype, int group_num, int64_t n, int64_t k, const int64_t *group_m,
+                     const void *grad_out, const void *w, void *grad_x, void *stream, gg_plan **plan_out);
+int gg_prepare_wgrad(int dtype, int group_num, int64_t n, int64_t k, const int64_t *group_m,
+                     const void *grad_out, const void *x, void *grad_w, void *stream, gg_plan **plan_out);
+
 /* Free the plan and its device table. Replaces CkTileBackend::release
  * (ck_kernel/ck_grouped_gemm.cpp:142-146). NULL is accepted. */
 void gg_release(gg_plan *plan);

@@ -168,6 +168,53 @@ void gg_oracle_grouped_gemm(int dtype, int group_num, int64_t n, int64_t k, cons
     }
 }
 
+static inline float dec(int dtype, uint16_t h) {
+    return dtype == 0 ? gg_oracle_bf16_to_f32(h) : gg_oracle_f16_to_f32(h);
+}
+
+void gg_oracle_grouped_dgrad(int dtype, int group_num, int64_t n, int64_t k, const int64_t *group_m,
+                             const uint16_t *grad_out, const uint16_t *w, float *out) {
+    int64_t row0 = 0;
+    for (int g = 0; g < group_num; ++g) {
+        const int64_t   m  = group_m[g];
+        const uint16_t *wg = w + (int64_t)g * n * k;
+#pragma omp parallel for schedule(static)
+        for (int64_t r = row0; r < row0 + m; ++r) {
+            float *o = out + r * k;
+            for (int64_t c = 0; c < k; ++c)
+                o[c] = 0.f;
+            for (int64_t j = 0; j < n; ++j) {
+                const float a = dec(dtype, grad_out[r * n + j]);
+                const uint16_t *wr = wg + j * k;
+                for (int64_t c = 0; c < k; ++c)
+                    o[c] += a * dec(dtype, wr[c]);
+            }
+        }
+        row0 += m;
+    }
+}
+
+void gg_oracle_grouped_wgrad(int dtype, int group_num, int64_t n, int64_t k, const int64_t *group_m,
+                             const uint16_t *grad_out, const uint16_t *x, float *out) {
+    int64_t row0 = 0;
+    for (int g = 0; g < group_num; ++g) {
+        const int64_t m = group_m[g];
+#pragma omp parallel for schedule(static)
+        for (int64_t i = 0; i < n; ++i) {
+            float *o = out + ((int64_t)g * n + i) * k;
+            for (int64_t c = 0; c < k; ++c)
+                o[c] = 0.f;
+            for (int64_t r = row0; r < row0 + m; ++r) {
+                const float a = dec(dtype, grad_out[r * n + i]);
+                const uint16_t *xr = x + r * k;
+                for (int64_t c = 0; c < k; ++c)
+                    o[c] += a * dec(dtype, xr[c]);
+            }
+        }
+        row0 += m;
+    }
+}
+
 void gg_oracle_sampled(int dtype, int64_t n, int64_t k, const uint16_t *x, const uint16_t *w,
                        const int64_t *samples, int64_t count, float *ref) {
 #pragma omp parallel for schedule(static)

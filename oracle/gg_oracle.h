@@ -10,6 +10,12 @@
  *                           (fp32 dot of x[row,:] and w[g][col,:]); ck_grouped_gemm.cpp:166-188
  *                           (group row offsets, w[g] at g*N*K)
  *   gg_oracle_sampled       bench/bench_main.cpp:185-206 (one fp32 dot per sample)
+ *   gg_oracle_grouped_dgrad / gg_oracle_grouped_wgrad
+ *                           the backward GEMMs of the same op, with the shapes of the vendored
+ *                           Primus-Turbo grouped GEMM's check() (third_party/primus_turbo/kernels/
+ *                           hipblaslt_grouped_gemm.cu:80-97: grad_c * b = grad_a, a^T * grad_c =
+ *                           grad_b) and its zero output for an empty group's weight gradient
+ *                           (:206-214); fp32 sums like gg_oracle_grouped_gemm
  *   gg_oracle_make_samples  bench/bench_main.cpp:210-227 (4 corners + 256 random per group,
  *                           one std::mt19937_64(1234) engine for all groups)
  *   gg_oracle_check         bench/bench_main.cpp:235-271 (|got-ref| <= atol + rtol*|ref|, NaN is a
@@ -49,6 +55,17 @@ void     gg_oracle_encode(int dtype, const float *src, uint16_t *dst, size_t cou
  * x: [sum(group_m), k], w: [group_num, n, k], out: [sum(group_m), n]. OpenMP over rows. */
 void gg_oracle_grouped_gemm(int dtype, int group_num, int64_t n, int64_t k, const int64_t *group_m,
                             const uint16_t *x, const uint16_t *w, float *out);
+
+/* Input gradient: out[row, c] (fp32) = sum_j grad_out[row, j] * w[g, j, c] for every row of
+ * every group. grad_out: [sum(group_m), n], w: [group_num, n, k], out: [sum(group_m), k]. */
+void gg_oracle_grouped_dgrad(int dtype, int group_num, int64_t n, int64_t k, const int64_t *group_m,
+                             const uint16_t *grad_out, const uint16_t *w, float *out);
+
+/* Weight gradient: out[g, i, c] (fp32) = sum over the rows r of group g of grad_out[r, i] *
+ * x[r, c]; zero for an empty group. grad_out: [sum(group_m), n], x: [sum(group_m), k],
+ * out: [group_num, n, k]. */
+void gg_oracle_grouped_wgrad(int dtype, int group_num, int64_t n, int64_t k, const int64_t *group_m,
+                             const uint16_t *grad_out, const uint16_t *x, float *out);
 
 /* Same dot products for rows [row_begin, row_end) of one group only (out: [rows, n]).
  * The bounded CPU baseline sample. */

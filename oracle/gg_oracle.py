@@ -34,6 +34,12 @@ def lib() -> ctypes.CDLL:
             "gg_oracle_f32_to_f16": (ctypes.c_uint16, [ctypes.c_float]),
             "gg_oracle_decode": (None, [ctypes.c_int, _P16, _PF, ctypes.c_size_t]),
             "gg_oracle_encode": (None, [ctypes.c_int, _PF, _P16, ctypes.c_size_t]),
+            "gg_oracle_grouped_dgrad": (None, [ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_int64,
+                                               ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                               ctypes.c_void_p]),
+            "gg_oracle_grouped_wgrad": (None, [ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_int64,
+                                               ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                               ctypes.c_void_p]),
             "gg_oracle_grouped_gemm": (None, [ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_int64,
                                               _PI64, _P16, _P16, _PF]),
             "gg_oracle_group_rows": (None, [ctypes.c_int, ctypes.c_int64, ctypes.c_int64, _P16, _P16,
@@ -84,6 +90,30 @@ def grouped_gemm(dtype: int, x: np.ndarray, w: np.ndarray, group_m) -> np.ndarra
     out = np.zeros((int(gm.sum()), n), dtype=np.float32)
     lib().gg_oracle_grouped_gemm(dtype, b, n, k, _ptr(gm, ctypes.c_int64), _ptr(x, ctypes.c_uint16),
                                  _ptr(w, ctypes.c_uint16), _ptr(out, ctypes.c_float))
+    return out
+
+
+def grouped_dgrad(dtype: int, grad_out: np.ndarray, w: np.ndarray, group_m) -> np.ndarray:
+    """fp32 grad_x [sum(M), K] = grad_out [sum(M), N] @ w[g] [N, K] per group (bit patterns in)."""
+    grad_out = np.ascontiguousarray(grad_out, dtype=np.uint16)
+    w = np.ascontiguousarray(w, dtype=np.uint16)
+    b, n, k = w.shape
+    gm = np.ascontiguousarray(group_m, dtype=np.int64)
+    out = np.zeros((int(gm.sum()), k), dtype=np.float32)
+    lib().gg_oracle_grouped_dgrad(dtype, b, n, k, gm.ctypes.data, grad_out.ctypes.data, w.ctypes.data,
+                                  out.ctypes.data)
+    return out
+
+
+def grouped_wgrad(dtype: int, grad_out: np.ndarray, x: np.ndarray, group_m) -> np.ndarray:
+    """fp32 grad_w [B, N, K] = grad_out[g]^T [N, M_g] @ x[g] [M_g, K] per group; zero if M_g = 0."""
+    grad_out = np.ascontiguousarray(grad_out, dtype=np.uint16)
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    gm = np.ascontiguousarray(group_m, dtype=np.int64)
+    n, k = grad_out.shape[1], x.shape[1]
+    out = np.zeros((len(gm), n, k), dtype=np.float32)
+    lib().gg_oracle_grouped_wgrad(dtype, len(gm), n, k, gm.ctypes.data, grad_out.ctypes.data, x.ctypes.data,
+                                  out.ctypes.data)
     return out
 
 

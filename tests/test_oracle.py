@@ -146,6 +146,69 @@ def test_grouped_gemm_exact_integers(oracle):
         row += m
 
 
+@pytest.mark.parametrize("dt,group_m,n,k", [
+    (0, [5, 0, 17, 1], 24, 40),
+    (1, [33, 2], 8, 72),
+    (0, [0, 0], 16, 16),
+    (0, [64, 64, 64], 72, 129),
+])
+def test_grouped_dgrad_vs_numpy_float64(oracle, dt, group_m, n, k):
+    """grad_x_g = grad_out_g @ w_g (w_g used as stored, N x K: a transposed w would fail)."""
+    rng = np.random.default_rng(n * 7 + k)
+    go = oracle_encode_np(dt, rng.standard_normal((sum(group_m), n)).astype(np.float32))
+    w = oracle_encode_np(dt, rng.standard_normal((len(group_m), n, k)).astype(np.float32))
+    got = oracle.grouped_dgrad(dt, go, w, group_m)
+    gof, wf = _decode_np(dt, go).astype(np.float64), _decode_np(dt, w).astype(np.float64)
+    assert got.shape == (sum(group_m), k)
+    row = 0
+    for g, m in enumerate(group_m):
+        np.testing.assert_allclose(got[row:row + m], gof[row:row + m] @ wf[g], rtol=1e-4,
+                                   atol=1e-4 * np.sqrt(n))
+        row += m
+
+
+@pytest.mark.parametrize("dt,group_m,n,k", [
+    (0, [5, 0, 17, 1], 24, 40),
+    (1, [33, 2], 8, 72),
+    (0, [0, 0], 16, 16),
+    (0, [64, 3, 100], 72, 129),
+])
+def test_grouped_wgrad_vs_numpy_float64(oracle, dt, group_m, n, k):
+    """grad_w_g = grad_out_g^T @ x_g over the group's own rows; zero for an empty group."""
+    rng = np.random.default_rng(n * 5 + k)
+    go = oracle_encode_np(dt, rng.standard_normal((sum(group_m), n)).astype(np.float32))
+    x = oracle_encode_np(dt, rng.standard_normal((sum(group_m), k)).astype(np.float32))
+    got = oracle.grouped_wgrad(dt, go, x, group_m)
+    gof, xf = _decode_np(dt, go).astype(np.float64), _decode_np(dt, x).astype(np.float64)
+    assert got.shape == (len(group_m), n, k)
+    row = 0
+    for g, m in enumerate(group_m):
+        want = gof[row:row + m].T @ xf[row:row + m] if m else np.zeros((n, k))
+        np.testing.assert_allclose(got[g], want, rtol=1e-4, atol=1e-4 * np.sqrt(max(m, 1)))
+        row += m
+
+
+def test_backward_exact_integers(oracle):
+    """Small integers: every fp32 partial sum is exact, so dgrad and wgrad equal int64 matmuls;
+    dgrad of the forward's own w and wgrad agree with the forward by the product rule
+    sum(grad_out * (x @ w^T)) = sum(grad_w * w) = sum(grad_x * x)."""
+    rng = np.random.default_rng(5)
+    group_m, n, k = [9, 0, 14, 3], 24, 40
+    gi = rng.integers(-4, 5, (sum(group_m), n))
+    xi = rng.integers(-4, 5, (sum(group_m), k))
+    wi = rng.integers(-4, 5, (len(group_m), n, k))
+    enc = lambda a: oracle_encode_np(0, a.astype(np.float32))
+    gx = oracle.grouped_dgrad(0, enc(gi), enc(wi), group_m).astype(np.int64)
+    gw = oracle.grouped_wgrad(0, enc(gi), enc(xi), group_m).astype(np.int64)
+    out = oracle.grouped_gemm(0, enc(xi), enc(wi), group_m).astype(np.int64)
+    row = 0
+    for g, m in enumerate(group_m):
+        assert np.array_equal(gx[row:row + m], gi[row:row + m] @ wi[g])
+        assert np.array_equal(gw[g], gi[row:row + m].T @ xi[row:row + m])
+        row += m
+    assert (gi * out).sum() == (gw * wi).sum() == (gx * xi).sum()
+
+
 def test_group_rows_and_sampled_agree_with_full(oracle):
     dt, group_m, n, k = 0, [40, 9, 33], 56, 200
     x, w = _rand_problem(dt, group_m, n, k, seed=5)
