@@ -85,11 +85,14 @@ static void check_band(int m_tiles, int n_tiles, int band) {
         }
 }
 
-static void check_walk(const std::vector<int64_t> &group_m, int64_t n, int grid, int n_xcd) {
+// out_rows > 0: the weight-gradient walk, where every group (empty ones included) owns an
+// out_rows x n output.
+static void check_walk(const std::vector<int64_t> &group_m, int64_t n, int grid, int n_xcd,
+                       int64_t out_rows = 0) {
     const int64_t n_tiles = gg::cdiv(n, gg::kTileN);
     std::vector<gg::GroupEntry> table(group_m.size());
     const int64_t total = gg::build_group_table(group_m.data(), (int)group_m.size(), n_tiles,
-                                                table.data());
+                                                table.data(), out_rows);
     CHECK(total >= 0, "table build failed");
     std::set<std::tuple<int, int, int>> seen;
     for (int wg = 0; wg < grid; ++wg) {
@@ -100,15 +103,16 @@ static void check_walk(const std::vector<int64_t> &group_m, int64_t n, int grid,
             prevL = L;
             int tm, tn;
             gg::locate_tile(L, table.data(), (int)group_m.size(), (int)n_tiles, gg::kBand, &g, &tm,
-                            &tn);
-            CHECK(group_m[g] > 0, "tile assigned to empty group %d", g);
-            CHECK(tm * gg::kTileM < group_m[g] && tn * gg::kTileN < n, "tile outside group");
+                            &tn, (int)out_rows);
+            const int64_t rows = out_rows > 0 ? out_rows : group_m[g];
+            CHECK(rows > 0, "tile assigned to empty group %d", g);
+            CHECK(tm * gg::kTileM < rows && tn * gg::kTileN < n, "tile outside group");
             CHECK(seen.insert({g, tm, tn}).second, "tile (%d,%d,%d) twice", g, tm, tn);
         }
     }
     int64_t want = 0;
     for (int64_t m : group_m)
-        want += gg::cdiv(m, gg::kTileM) * n_tiles;
+        want += gg::cdiv(out_rows > 0 ? out_rows : m, gg::kTileM) * n_tiles;
     CHECK((int64_t)seen.size() == want && want == total, "walk covers %zu of %lld tiles",
           seen.size(), (long long)want);
 }
@@ -135,6 +139,11 @@ int main() {
     check_walk({0, 300, 0, 0, 1, 2000, 0}, 1000, 17, 1);
     check_walk({0, 300, 0, 0, 1, 2000, 0}, 1000, 24, 8);
     check_walk({257, 0, 255, 4096, 3}, 264, 256, 8);
+    // weight gradient: every group owns out_rows x n, empty groups included
+    check_walk(std::vector<int64_t>(8, 4096), 7168, 256, 8, 4096);
+    check_walk({0, 300, 0, 0, 1, 2000, 0}, 1000, 24, 8, 776);
+    check_walk({0, 0, 0}, 64, 3, 1, 64);
+    check_walk({520, 0, 520}, 2880, 256, 8, 2880);
     if (failures) {
         std::printf("%d failures\n", failures);
         return 1;
