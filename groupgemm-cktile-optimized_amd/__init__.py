@@ -46,6 +46,10 @@ C_API = {
                                              ctypes.POINTER(ctypes.c_int)]),
     "gg_compute_group_offs": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
                                              ctypes.c_void_p]),
+    "gg_prepare_fp8": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_int64,
+                                      ctypes.POINTER(ctypes.c_int64), ctypes.c_void_p, ctypes.c_void_p,
+                                      ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                      ctypes.POINTER(ctypes.c_void_p)]),
     "gg_prepare_dgrad": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_int64,
                                         ctypes.POINTER(ctypes.c_int64), ctypes.c_void_p, ctypes.c_void_p,
                                         ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)]),
@@ -93,9 +97,11 @@ def _check(status: int) -> None:
 
 
 class DType(enum.IntEnum):
-    """tunemax::DType (common/backend.hpp:27)."""
+    """tunemax::DType (common/backend.hpp:27), plus the fp8 input types of gg_prepare_fp8."""
     BF16 = 0
     FP16 = 1
+    FP8_E4M3 = 2
+    FP8_E5M2 = 3
 
 
 def dtype_name(t: DType) -> str:
@@ -253,6 +259,63 @@ class BackwardPlan:
             self.release()
         except Exception:
             pass
+
+
+class Fp8Plan:
+    """An fp8 forward plan (gg_prepare_fp8): out (bf16) = (x[g] @ w[g]^T) * x_scale[0] *
+    w_scale[g], tensor-wise scales in device memory (float32). Run any number of times."""
+
+    def __init__(self, dtype: DType, n: int, k: int, group_m: Sequence[int], x: int, w: int, x_scale: int,
+                 w_scale: int, out: int, stream: int = 0) -> None:
+        self._lib = load_library()
+        self._plan = ctypes.c_void_p()
+        gm = (ctypes.c_int64 * max(1, len(group_m)))(*group_m)
+        _check(self._lib.gg_prepare_fp8(int(dtype), len(group_m), n, k, gm, x, w, x_scale, w_scale, out, stream,
+                                        ctypes.byref(self._plan)))
+        self.flop = 2.0 * float(sum(group_m)) * float(n) * float(k)
+
+    def run(self, stream: int = 0) -> None:
+        _check(self._lib.gg_run(self._plan, stream))
+
+    def detail(self) -> str:
+        return self._lib.gg_plan_detail(self._plan).decode() if self._plan else ""
+
+    def release(self) -> None:
+        if self._plan:
+            self._lib.gg_release(self._plan)
+            self._plan = ctypes.c_void_p()
+
+    def __del__(self) -> None:
+        try:
+            self.release()
+        except Exception:
+            pass
+
+
+def grouped_gemm_fp8(x, w, group_m: Sequence[int], x_scale, w_scale, out=None, stream: Optional[int] = None):
+    """bf16 out = (x[g] @ w[g]^T) * x_scale * w_scale[g] for torch float8_e4m3fn or float8_e5m2
+    tensors x [sum(M), K], w [B, N, K] and float32 device scales x_scale [1], w_scale [B]."""
+    import torch
+
+    kinds = {torch.float8_e4m3fn: DType.FP8_E4M3, torch.float8_e5m2: DType.FP8_E5M2}
+    if x.dtype != w.dtype or x.dtype not in kinds:
+        raise TypeError("x and w must both be float8_e4m3fn or both float8_e5m2")
+    if not (x_scale.dtype == w_scale.dtype == torch.float32 and x_scale.is_cuda and w_scale.is_cuda):
+        raise TypeError("scales must be float32 device tensors")
+    b, n, k = w.shape
+    if len(group_m) != b or x.shape[1] != k or x.shape[0] != sum(group_m) or w_scale.numel() != b:
+        raise ValueError("shape mismatch between x, w, group_m and the scales")
+    if out is None:
+        out = torch.empty((x.shape[0], n), dtype=torch.bfloat16, device=x.device)
+    s = torch.cuda.current_stream(x.device).cuda_stream if stream is None else stream
+    plan = Fp8Plan(kinds[x.dtype], n, k, list(group_m), x.data_ptr(), w.data_ptr(), x_scale.data_ptr(),
+                   w_scale.data_ptr(), out.data_ptr(), s)
+    try:
+        plan.run(s)
+        torch.cuda.current_stream(x.device).synchronize()
+    finally:
+        plan.release()
+    return out
 
 
 def make_mi355x_backend() -> Backend:

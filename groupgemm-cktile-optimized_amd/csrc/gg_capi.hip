@@ -108,6 +108,8 @@ void fill_args(gg_plan *plan, int n_xcd) {
     a.lda       = static_cast<int>(plan->k);
     a.ldb       = static_cast<int>(plan->k);
     a.m_out     = 0;
+    a.x_scale   = nullptr;
+    a.w_scale   = nullptr;
 }
 
 } // namespace
@@ -305,6 +307,97 @@ static int prepare_backward(int mode, int dtype, int group_num, int64_t n, int64
                        (has_output ? "empty contraction, zero fill" : "empty output") + ")";
         if (!has_output)
             plan->total_m = 0;
+    }
+    *plan_out = plan;
+    return GG_OK;
+}
+
+int gg_prepare_fp8(int dtype, int group_num, int64_t n, int64_t k, const int64_t *group_m,
+                   const void *x, const void *w, const float *x_scale, const float *w_scale, void *out,
+                   void *stream, gg_plan **plan_out) {
+    g_last_error.clear();
+    if (plan_out == nullptr)
+        return fail(GG_ERR_INVALID, "plan_out is null");
+    *plan_out = nullptr;
+    if (dtype != GG_DTYPE_FP8_E4M3 && dtype != GG_DTYPE_FP8_E5M2)
+        return fail(GG_ERR_INVALID, "dtype must be GG_DTYPE_FP8_E4M3 or GG_DTYPE_FP8_E5M2");
+    if (group_num > 0 && group_m == nullptr)
+        return fail(GG_ERR_INVALID, "group_m is null");
+    int64_t total_m = 0;
+    for (int g = 0; g < group_num; ++g) {
+        if (group_m[g] < 0)
+            return fail(GG_ERR_INVALID, "group_m[" + std::to_string(g) + "] < 0");
+        total_m += group_m[g];
+    }
+    if (group_num < 0 || n < 0 || k < 0)
+        return fail(GG_ERR_INVALID, "group_num, n and k must be >= 0");
+    const bool has_output = total_m > 0 && n > 0;
+    if (has_output && (out == nullptr || (k > 0 && (x == nullptr || w == nullptr || x_scale == nullptr ||
+                                                    w_scale == nullptr))))
+        return fail(GG_ERR_INVALID, "x, w, the scales and out must be device pointers");
+    if (n % 8 != 0)
+        return fail(GG_ERR_UNSUPPORTED, "N must be a multiple of 8 (16-byte output rows)");
+    if (k % 16 != 0)
+        return fail(GG_ERR_UNSUPPORTED, "K must be a multiple of 16 for fp8 (16-byte input rows)");
+    if (has_output && (!aligned16(out) || (k > 0 && (!aligned16(x) || !aligned16(w)))))
+        return fail(GG_ERR_UNSUPPORTED, "x, w and out must be 16-byte aligned");
+    if (k > (int64_t(1) << 21) || n > (int64_t(1) << 21))
+        return fail(GG_ERR_UNSUPPORTED, "N and K must be at most 2097152");
+
+    auto *plan = new (std::nothrow) gg_plan;
+    if (plan == nullptr)
+        return fail(GG_ERR_INVALID, "out of host memory");
+    plan->mode      = dtype == GG_DTYPE_FP8_E4M3 ? 3 : 4;
+    plan->dtype     = GG_DTYPE_BF16; // output
+    plan->group_num = group_num;
+    plan->n         = n;
+    plan->k         = k;
+    plan->total_m   = total_m;
+    plan->x         = x;
+    plan->w         = w;
+    plan->out       = out;
+    const int64_t n_tiles = gg::cdiv(n, gg::kTileN);
+    std::vector<gg::GroupEntry> table(static_cast<size_t>(group_num));
+    const int64_t tiles = gg::build_group_table(group_m, group_num, n_tiles, table.data());
+    if (tiles < 0) {
+        delete plan;
+        return fail(GG_ERR_UNSUPPORTED, "too many rows or tiles for 32-bit tile indices");
+    }
+    plan->total_tiles = has_output && k > 0 ? static_cast<int>(tiles) : 0;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (plan->total_tiles > 0) {
+        hipDeviceProp_t prop;
+        if (device_props(&prop) != GG_OK) {
+            delete plan;
+            return GG_ERR_HIP;
+        }
+        const size_t bytes = table.size() * sizeof(gg::GroupEntry);
+        hipError_t   e     = hipMalloc(&plan->d_groups, bytes);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(plan->d_groups, table.data(), bytes, hipMemcpyHostToDevice, s);
+        if (e == hipSuccess)
+            e = hipStreamSynchronize(s);
+        if (e != hipSuccess) {
+            if (plan->d_groups != nullptr)
+                (void)hipFree(plan->d_groups);
+            delete plan;
+            return hip_fail(e, "group table upload");
+        }
+        plan->grid = std::min(prop.multiProcessorCount, plan->total_tiles);
+        fill_args(plan, xcd_count(prop));
+        gg::KernelArgs &a = plan->args;
+        a.total_tiles     = plan->total_tiles;
+        a.d_total         = nullptr;
+        a.k_tiles         = static_cast<int>(gg::cdiv(k, 128)); // 128 fp8 values per K step
+        a.x_scale         = x_scale;
+        a.w_scale         = w_scale;
+        plan->detail = std::string("mi355x fp8 ") + (dtype == GG_DTYPE_FP8_E4M3 ? "e4m3" : "e5m2") +
+                       " persistent 256x256x128 bf16-out grid=" + std::to_string(plan->grid) +
+                       " tiles=" + std::to_string(plan->total_tiles) + " xcd=" + std::to_string(a.n_xcd) +
+                       " per-tile";
+    } else {
+        plan->detail = std::string("mi355x fp8: no launch (") +
+                       (has_output ? "K = 0, zero fill" : "empty output") + ")";
     }
     *plan_out = plan;
     return GG_OK;

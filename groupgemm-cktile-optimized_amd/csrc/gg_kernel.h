@@ -30,6 +30,8 @@ struct KernelArgs {
     int               band;        // M-tiles per band of the in-group tile order
     int               lda, ldb;    // row strides (elements) of the A and B storage
     int               m_out;       // wgrad: output rows per group (0 otherwise)
+    const float      *x_scale;     // fp8: device scale of x (1 value)
+    const float      *w_scale;     // fp8: device scale of each group's w (group_num values)
     const int        *d_total;     // device tile count (device-resident group sizes), or null:
                                    // then total_tiles holds it
 };
@@ -47,7 +49,8 @@ struct TableHeader {
 bool uses_cross_tile(const KernelArgs &args, int grid, int mode = 0);
 
 // Enqueue the persistent grouped GEMM: `grid` workgroups of 256 threads on `stream`.
-// fp16 selects the f16 MFMA, otherwise bf16; mode 0 forward, 1 dgrad, 2 wgrad.
+// fp16 selects the f16 MFMA, otherwise bf16; mode 0 forward, 1 dgrad, 2 wgrad, 3 / 4 forward
+// with fp8 e4m3 / e5m2 inputs (bf16 out, fp16 must be false).
 // Returns the launch status.
 hipError_t launch_grouped_gemm(const KernelArgs &args, bool fp16, int grid, hipStream_t stream,
                                int mode = 0);

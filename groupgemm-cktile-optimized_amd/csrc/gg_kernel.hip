@@ -125,10 +125,13 @@ constexpr int b_stage(int s) { return (kAStages + s) * kOpBytes; }
 enum Mode : int {
     kFwd   = 0, // out[g] = x[g] @ w[g]^T                       A = x (K-major),  B = w (K-major)
     kDgrad = 1, // grad_x[g] = grad_out[g] @ w[g]               A = grad_out (K), B = w (MN)
-    kWgrad = 2  // grad_w[g] = grad_out[g]^T @ x[g], K = M_g    A = grad_out (MN), B = x (MN)
+    kWgrad = 2, // grad_w[g] = grad_out[g]^T @ x[g], K = M_g    A = grad_out (MN), B = x (MN)
+    kFwdE4M3 = 3, // forward with fp8 e4m3 x and w, bf16 out = (x[g] @ w[g]^T) * sx * sw[g]
+    kFwdE5M2 = 4  // the same with fp8 e5m2
 };
+constexpr bool mode_f8(int m) { return m == kFwdE4M3 || m == kFwdE5M2; }
 constexpr bool mode_a_mn(int m) { return m == kWgrad; }
-constexpr bool mode_b_mn(int m) { return m != kFwd; }
+constexpr bool mode_b_mn(int m) { return m == kDgrad || m == kWgrad; }
 // LDS reads of one 16-row fragment over both k-halves.
 constexpr int reads_per_frag(bool mn) { return mn ? 4 : 2; }
 
@@ -143,6 +146,7 @@ constexpr int kBarRow = 7; // the step's barrier follows MFMA Plan::bar of this 
 static_assert(GG_BAR_IDX >= 5 && GG_BAR_IDX <= 11 && GG_BAR_IDX % 2 == 1, "barrier slot");
 
 template <int NA, int NB> struct Plan {
+    static constexpr int slots = 16, early = kEarlyA;
     // The w fragments of row 7 are read before the barrier, at MFMAs 1 .. 2 NB - 1.
     static constexpr int bar = GG_BAR_IDX > 2 * NB + 1 ? GG_BAR_IDX : 2 * NB + 1;
     static constexpr int row0_first = GG_ROW0_AT_BAR ? bar : bar + 2;
@@ -231,6 +235,63 @@ template <int NA, int NB> struct Plan {
     }
 };
 static_assert(Plan<2, 2>::check() && Plan<2, 4>::check() && Plan<4, 4>::check(), "slot plans");
+
+// fp8 K step: 128 fp8 values per 128-byte row; v_mfma_f32_16x16x128_f8f6f4 takes 32 bytes of a
+// row per lane (two ds_read_b128, read op r = half), so a row mi of the step is 8 MFMAs of twice
+// the length. Reads after odd MFMAs, DMAs after even ones: A(kt+1) DMAs 1-7 in rows 0-2 (after
+// MFMAs 0 and 4) and row 3 (after MFMA 2), B(kt+3) in rows 3-6 (after 0 and 4), the barrier
+// after MFMA 5 of row 7, then row 0 of the next step's x (5, 7) and the early A DMA 0 (6).
+struct Plan8 {
+    static constexpr int slots = 8, early = 1, bar = 5;
+    static constexpr int read_a_next(int mi, int idx) { return (mi < 7 && (idx == 1 || idx == 3)) ? idx / 2 : -1; }
+    static constexpr int read_b_next(int mi, int idx) {
+        if (mi < 7)
+            return (idx == 5 || idx == 7) ? (idx - 5) / 2 : -1;
+        return (idx == 1 || idx == 3) ? idx / 2 : -1;
+    }
+    static constexpr int read_a_row0(int mi, int idx) { return (mi == 7 && (idx == 5 || idx == 7)) ? (idx - 5) / 2 : -1; }
+    static constexpr int load_a(int mi, int idx) {
+        if (mi < 3 && (idx == 0 || idx == 4))
+            return 1 + 2 * mi + idx / 4;
+        return (mi == 3 && idx == 2) ? 7 : -1;
+    }
+    static constexpr int load_b(int mi, int idx) {
+        return (mi >= 3 && mi < 7 && (idx == 0 || idx == 4)) ? 2 * (mi - 3) + idx / 4 : -1;
+    }
+    static constexpr int load_a_early(int mi, int idx) { return (mi == 7 && idx == 6) ? 0 : -1; }
+    static constexpr int dma_kind(int mi, int idx) {
+        return load_a(mi, idx) >= 0 ? 1 : load_b(mi, idx) >= 0 ? 2 : load_a_early(mi, idx) >= 0 ? 3 : 0;
+    }
+    static constexpr int dma_j(int mi, int idx) {
+        return load_a(mi, idx) >= 0 ? load_a(mi, idx) : load_b(mi, idx) >= 0 ? load_b(mi, idx) : load_a_early(mi, idx);
+    }
+    static constexpr int vm_at_barrier() { // loads issued after A(kt+1)'s last DMA, as in Plan
+        int last_a = -1;
+        for (int p = 0; p < 8 * slots; ++p)
+            if (load_a(p / slots, p % slots) >= 0)
+                last_a = p;
+        int n = 0;
+        for (int p = last_a + 1; p < kBarRow * slots + bar; ++p)
+            n += (load_b(p / slots, p % slots) >= 0) + (load_a_early(p / slots, p % slots) >= 0);
+        return n;
+    }
+    static constexpr bool check() {
+        int na = 0, nb = 0, ne = 0, rb = 0;
+        for (int p = 0; p < 8 * slots; ++p) {
+            const int mi = p / slots, idx = p % slots;
+            const int ops = (load_a(mi, idx) >= 0) + (load_b(mi, idx) >= 0) + (load_a_early(mi, idx) >= 0) +
+                            (read_a_next(mi, idx) >= 0) + (read_b_next(mi, idx) >= 0) + (read_a_row0(mi, idx) >= 0);
+            if (ops > 1)
+                return false;
+            na += load_a(mi, idx) >= 0;
+            nb += load_b(mi, idx) >= 0;
+            ne += load_a_early(mi, idx) >= 0;
+            rb += read_b_next(mi, idx) >= 0;
+        }
+        return na == kLoads - early && nb == kLoads && ne == early && rb == 16;
+    }
+};
+static_assert(Plan8::check(), "fp8 slot plan");
 static_assert(Plan<2, 2>::bar == GG_BAR_IDX, "forward plan keeps the tuned barrier slot");
 
 // ---------------------------------------------------------------------------------------
@@ -306,6 +367,21 @@ __device__ __forceinline__ void mfma_first(f32x4 &c, const i32x4 &a, const i32x4
         asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=a"(c) : "v"(a), "v"(b));
 }
 
+// fp8 x fp8 -> fp32, 16 x 16 x 128 (gfx950): A and B are 32 bytes of a row per lane.
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+template <bool E5M2> __device__ __forceinline__ void mfma8(f32x4 &c, const i32x8 &a, const i32x8 &b) {
+    if constexpr (E5M2)
+        asm volatile("v_mfma_f32_16x16x128_f8f6f4 %0, %1, %2, %0 cbsz:1 blgp:1" : "+a"(c) : "v"(a), "v"(b));
+    else
+        asm volatile("v_mfma_f32_16x16x128_f8f6f4 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+}
+template <bool E5M2> __device__ __forceinline__ void mfma8_first(f32x4 &c, const i32x8 &a, const i32x8 &b) {
+    if constexpr (E5M2)
+        asm volatile("v_mfma_f32_16x16x128_f8f6f4 %0, %1, %2, 0 cbsz:1 blgp:1" : "=a"(c) : "v"(a), "v"(b));
+    else
+        asm volatile("v_mfma_f32_16x16x128_f8f6f4 %0, %1, %2, 0" : "=a"(c) : "v"(a), "v"(b));
+}
+
 // Four fp32 accumulators -> four 16-bit outputs (RNE), as two packed dwords.
 template <bool F16> __device__ __forceinline__ u32x2 pack4(const f32x4 &v) {
     u32x2 r;
@@ -350,8 +426,13 @@ template <bool F16, bool CROSS, int MODE>
 __global__ void __launch_bounds__(kThreads, 1) __attribute__((amdgpu_waves_per_eu(1, 1)))
 grouped_gemm_kernel(const KernelArgs args) {
     constexpr bool A_MN = mode_a_mn(MODE), B_MN = mode_b_mn(MODE);
-    using P = Plan<reads_per_frag(A_MN), reads_per_frag(B_MN)>;
+    constexpr bool F8   = mode_f8(MODE);
+    constexpr int  ES   = F8 ? 1 : 2;        // input bytes per element
+    constexpr int  KS   = kRowBytes / ES;    // contraction values per K step
+    using P = std::conditional_t<F8, Plan8, Plan<reads_per_frag(A_MN), reads_per_frag(B_MN)>>;
     static_assert(!(CROSS && MODE == kWgrad), "wgrad has a K-step count per group");
+    static_assert(!(CROSS && F8), "fp8 runs the per-tile variant");
+    static_assert(!(F8 && F16), "fp8 writes bf16");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kLdsBytes];
     typedef __attribute__((address_space(3))) uint8_t lds_u8;
     const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8 *)smem));
@@ -380,7 +461,7 @@ grouped_gemm_kernel(const KernelArgs args) {
     const int mn_col   = ((wave & 1) * 8 + (lane >> 3)) * 16 + (lane & 1) * 8;
     auto      dma_off  = [&](bool mn, int j, int ld) {
         return mn ? ((4 * (2 * j + (wave >> 1)) + ((lane & 7) >> 1)) * ld + mn_col) * 2
-                  : ((j * 32 + wave * 8 + ld_row) * ld + ld_chunk * 8) * 2;
+                  : (j * 32 + wave * 8 + ld_row) * ld * ES + ld_chunk * 16;
     };
     // voff[0]: A's offsets; voff[1]: B's (the forward op shares A's: both row strides are K).
     constexpr bool kSameOff = MODE == kFwd;
@@ -391,8 +472,8 @@ grouped_gemm_kernel(const KernelArgs args) {
             voff[1][j] = dma_off(B_MN, j, args.ldb);
     });
     // Last K step when K % 64 != 0: chunks at k >= K get an offset past every bound.
-    const int k_last    = K - (T - 1) * kTileK; // valid K of the last step, 8..64
-    int       ktail_bad = (ld_chunk * 8 >= k_last) ? static_cast<int>(0x80000000u) : 0;
+    const int k_last    = K - (T - 1) * KS; // valid K of the last step
+    int       ktail_bad = (ld_chunk * (16 / ES) >= k_last) ? static_cast<int>(0x80000000u) : 0;
 
     // Fragment reads. K-major: lane -> row lane%16 of a 16-row block, logical chunk
     // kh*4 + lane/16 (one base per k-half). MN-major: ds_read_b64_tr_b16 gives lane i of each
@@ -402,7 +483,8 @@ grouped_gemm_kernel(const KernelArgs args) {
     const int fr_row = lane & 15, fr_q = lane >> 4;
     int frag_a[2], frag_b[2];
     sfor<0, 2>([&](auto kh) {
-        const int off = fr_row * kRowBytes + (((kh * 4 + fr_q) ^ (fr_row & 7)) * 16);
+        // fp8: the 32 bytes of a lane are chunks 2q and 2q+1 (op kh = which one)
+        const int off = fr_row * kRowBytes + (((F8 ? 2 * fr_q + kh : kh * 4 + fr_q) ^ (fr_row & 7)) * 16);
         const int mn  = (lane >> 4) * 4096 + (lane & 15) * 8;
         frag_a[kh]    = A_MN ? wm * 1024 + mn : wm * 128 * kRowBytes + off;
         frag_b[kh]    = B_MN ? wn * 1024 + mn : wn * 128 * kRowBytes + off;
@@ -484,6 +566,7 @@ grouped_gemm_kernel(const KernelArgs args) {
         int       m_valid, n_valid;
         int       o0a, o0b;       // MN-major operands: first stored column of the tile
         int       T;              // K steps (wgrad: of the tile's group, at least 1)
+        float     scale;          // fp8: x scale * w[g] scale (1 otherwise)
     };
     const int bad_off = static_cast<int>(0x80000000u);
     int       g       = 0; // group hint of locate_tile (logical tiles only grow)
@@ -495,11 +578,14 @@ grouped_gemm_kernel(const KernelArgs args) {
         const GroupEntry ge = args.groups[g];
         const uint16_t  *xa = static_cast<const uint16_t *>(args.x);
         const uint16_t  *wb = static_cast<const uint16_t *>(args.w);
+        const uint8_t   *x8 = static_cast<const uint8_t *>(args.x);
+        const uint8_t   *w8 = static_cast<const uint8_t *>(args.w);
         Tile             tl;
         tl.n_valid         = min(kTileN, N - tn * kTileN);
         const int64_t col0 = static_cast<int64_t>(tn) * kTileN;
         tl.o0a = tl.o0b = 0;
         tl.T            = T;
+        tl.scale        = 1.0f;
         if constexpr (MODE == kWgrad) {
             // A^T = grad_out rows of the group, columns tm*256..; B^T = x rows, columns tn*256..
             const int64_t o0a = static_cast<int64_t>(tm) * kTileM;
@@ -517,7 +603,12 @@ grouped_gemm_kernel(const KernelArgs args) {
             tl.m_valid         = min(kTileM, ge.m - tm * kTileM);
             const int64_t row0 = ge.row0 + static_cast<int64_t>(tm) * kTileM;
             tl.rsrc_a = dma_rsrc(xa + row0 * args.lda, static_cast<uint32_t>(tl.m_valid) * args.lda * 2);
-            if constexpr (MODE == kFwd) {
+            if constexpr (F8) {
+                tl.rsrc_a = dma_rsrc(x8 + row0 * args.lda, static_cast<uint32_t>(tl.m_valid) * args.lda);
+                tl.rsrc_b = dma_rsrc(w8 + (static_cast<int64_t>(g) * N + col0) * args.ldb,
+                                     static_cast<uint32_t>(tl.n_valid) * args.ldb);
+                tl.scale = args.x_scale[0] * args.w_scale[g];
+            } else if constexpr (MODE == kFwd) {
                 tl.rsrc_b = dma_rsrc(wb + (static_cast<int64_t>(g) * N + col0) * args.ldb,
                                      static_cast<uint32_t>(tl.n_valid) * args.ldb * 2);
             } else {
@@ -632,7 +723,7 @@ grouped_gemm_kernel(const KernelArgs args) {
         sfor<0, kLoads>([&](auto j) { dma_now(b_dst[0], B_OP{}, j, 0); });
         sfor<0, kLoads>([&](auto j) { dma_now(b_dst[1], B_OP{}, j, 1); });
         sfor<0, kLoads>([&](auto j) { dma_now(b_dst[2], B_OP{}, j, 2); });
-        sfor<0, kEarlyA>([&](auto j) { dma_now(a_dst[1], A_OP{}, j, 1); });
+        sfor<0, P::early>([&](auto j) { dma_now(a_dst[1], A_OP{}, j, 1); });
     };
     // Then B(0) and A(0) row 0 into registers. VM: DMAs/stores issued after B(1)'s last.
     auto finish_prologue = [&]<int VM>() {
@@ -698,8 +789,10 @@ grouped_gemm_kernel(const KernelArgs args) {
             sfor<0, 8>([&](auto mi) {
                 sfor<0, 8>([&](auto ni) {
                     asm volatile("" : "+a"(acc[mi][ni]));
-                    *reinterpret_cast<u32x2 *>(smem + off + mi * 16 * kCStride + ni * 16 * 2) =
-                        pack4<F16>(acc[mi][ni]);
+                    f32x4 v = acc[mi][ni];
+                    if constexpr (F8)
+                        v *= tl.scale;
+                    *reinterpret_cast<u32x2 *>(smem + off + mi * 16 * kCStride + ni * 16 * 2) = pack4<F16>(v);
                 });
             });
         }
@@ -752,9 +845,9 @@ grouped_gemm_kernel(const KernelArgs args) {
         const DmaSrc src_a2 = dma_src(A_OP{}, kt + 2, chk{}); // A(kt+2)
         sfor<0, 8>([&](auto mi_) {
             constexpr int mi = decltype(mi_)::value;
-            sfor<0, 16>([&](auto idx_) {
+            sfor<0, P::slots>([&](auto idx_) {
                 constexpr int idx = decltype(idx_)::value;
-                constexpr int kh = idx / 8, ni = idx % 8;
+                constexpr int kh = idx / 8, ni = idx % 8; // fp8: one MFMA per (mi, ni), kh = 0
                 constexpr int dk = P::dma_kind(mi, idx), dj = P::dma_j(mi, idx);
                 if constexpr (dk == 1)
                     set_m0<dj * 4096>(a_dst[NX]); // the MFMA below is the wait state
@@ -763,7 +856,14 @@ grouped_gemm_kernel(const KernelArgs args) {
                 else if constexpr (dk == 3)
                     set_m0<dj * 4096>(a_dst[SA]);
                 sched_fence();
-                if constexpr (FIRST && kh == 0)
+                if constexpr (F8) {
+                    const i32x8 bw = __builtin_shufflevector(fb[SA][ni][0], fb[SA][ni][1], 0, 1, 2, 3, 4, 5, 6, 7);
+                    const i32x8 ax = __builtin_shufflevector(fa[mi & 1][0], fa[mi & 1][1], 0, 1, 2, 3, 4, 5, 6, 7);
+                    if constexpr (FIRST)
+                        mfma8_first<MODE == kFwdE5M2>(acc[mi][ni], bw, ax);
+                    else
+                        mfma8<MODE == kFwdE5M2>(acc[mi][ni], bw, ax);
+                } else if constexpr (FIRST && kh == 0)
                     mfma_first<F16>(acc[mi][ni], fb[SA][ni][0], fa[mi & 1][0]);
                 else
                     mfma<F16>(acc[mi][ni], fb[SA][ni][kh], fa[mi & 1][kh]);
@@ -804,13 +904,13 @@ grouped_gemm_kernel(const KernelArgs args) {
     if constexpr (CROSS) {
         set_stages();
         issue_prologue();
-        finish_prologue.template operator()<kLoads + kEarlyA>();
+        finish_prologue.template operator()<kLoads + P::early>();
     }
     while (true) {
         if constexpr (!CROSS) {
             set_stages();
             issue_prologue();
-            finish_prologue.template operator()<kLoads + kEarlyA>();
+            finish_prologue.template operator()<kLoads + P::early>();
         }
         refresh();
         if constexpr (CROSS) {
@@ -977,7 +1077,7 @@ template <bool F16> __global__ void fill_randn_kernel(uint16_t *p, size_t n, uin
 } // namespace
 
 bool uses_cross_tile(const KernelArgs &args, int grid, int mode) {
-    if (mode == kWgrad)
+    if (mode == kWgrad || mode_f8(mode))
         return false;
     // Workgroups with a single tile gain nothing from the cross-tile pipeline.
     // (a device-built table's tile count is unknown on the host: take the cross-tile variant,
@@ -988,7 +1088,7 @@ bool uses_cross_tile(const KernelArgs &args, int grid, int mode) {
 
 template <bool F16, int MODE>
 void launch_mode(const KernelArgs &args, bool cross, dim3 g, dim3 b, hipStream_t stream) {
-    if constexpr (MODE == kWgrad)
+    if constexpr (MODE == kWgrad || mode_f8(MODE))
         hipLaunchKernelGGL((grouped_gemm_kernel<F16, false, MODE>), g, b, 0, stream, args);
     else if (cross)
         hipLaunchKernelGGL((grouped_gemm_kernel<F16, true, MODE>), g, b, 0, stream, args);
@@ -998,6 +1098,12 @@ void launch_mode(const KernelArgs &args, bool cross, dim3 g, dim3 b, hipStream_t
 
 template <bool F16>
 void launch_dtype(const KernelArgs &args, bool cross, int mode, dim3 g, dim3 b, hipStream_t stream) {
+    if constexpr (!F16) {
+        if (mode == kFwdE4M3)
+            return launch_mode<false, kFwdE4M3>(args, cross, g, b, stream);
+        if (mode == kFwdE5M2)
+            return launch_mode<false, kFwdE5M2>(args, cross, g, b, stream);
+    }
     if (mode == kDgrad)
         launch_mode<F16, kDgrad>(args, cross, g, b, stream);
     else if (mode == kWgrad)

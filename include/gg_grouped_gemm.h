@@ -27,8 +27,14 @@
 extern "C" {
 #endif
 
-/* Element type of x, w and out. Same values as tunemax::DType (common/backend.hpp:27). */
-typedef enum gg_dtype { GG_DTYPE_BF16 = 0, GG_DTYPE_FP16 = 1 } gg_dtype;
+/* Element type of x, w and out. BF16 and FP16: same values as tunemax::DType
+ * (common/backend.hpp:27). The fp8 types are inputs of gg_prepare_fp8 only (out is bf16). */
+typedef enum gg_dtype {
+    GG_DTYPE_BF16     = 0,
+    GG_DTYPE_FP16     = 1,
+    GG_DTYPE_FP8_E4M3 = 2, /* OCP e4m3 (finite, max 448) */
+    GG_DTYPE_FP8_E5M2 = 3  /* OCP e5m2 */
+} gg_dtype;
 
 typedef enum gg_status {
     GG_OK = 0,
@@ -88,6 +94,18 @@ int gg_prepare_dgrad(int dtype, int group_num, int64_t n, int64_t k, const int64
                      const void *grad_out, const void *w, void *grad_x, void *stream, gg_plan **plan_out);
 int gg_prepare_wgrad(int dtype, int group_num, int64_t n, int64_t k, const int64_t *group_m,
                      const void *grad_out, const void *x, void *grad_w, void *stream, gg_plan **plan_out);
+
+/*
+ * fp8 forward with tensor-wise scales: out[rows of g] (bf16) = (x[rows of g] @ w[g]^T) *
+ * x_scale[0] * w_scale[g], x and w fp8 (dtype GG_DTYPE_FP8_E4M3 or GG_DTYPE_FP8_E5M2, both the
+ * same), fp32 accumulation; x_scale (1 float) and w_scale (group_num floats) are device memory,
+ * read by every run. Replaces primus_turbo::ck_grouped_gemm_fp8 with its aq_ptr / bq_ptr scales
+ * (third_party/primus_turbo/include/primus_turbo/grouped_gemm.h:72-74, 120-123). Same plan
+ * life cycle as gg_prepare; N/A unless k % 16 == 0 (16-byte input rows) and n % 8 == 0.
+ */
+int gg_prepare_fp8(int dtype, int group_num, int64_t n, int64_t k, const int64_t *group_m,
+                   const void *x, const void *w, const float *x_scale, const float *w_scale, void *out,
+                   void *stream, gg_plan **plan_out);
 
 /* Free the plan and its device table. Replaces CkTileBackend::release
  * (ck_kernel/ck_grouped_gemm.cpp:142-146). NULL is accepted. */

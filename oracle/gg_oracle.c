@@ -168,6 +168,48 @@ void gg_oracle_grouped_gemm(int dtype, int group_num, int64_t n, int64_t k, cons
     }
 }
 
+float gg_oracle_fp8_to_f32(int fmt, uint8_t b) {
+    const int   sign = b >> 7;
+    const int   eb   = fmt == 0 ? 4 : 5, mb = fmt == 0 ? 3 : 2, bias = fmt == 0 ? 7 : 15;
+    const int   e    = (b >> mb) & ((1 << eb) - 1), m = b & ((1 << mb) - 1);
+    float       v;
+    if (fmt == 0 && e == 15 && m == 7)
+        v = NAN; /* e4m3: the only NaN, no infinities */
+    else if (fmt == 1 && e == 31)
+        v = m == 0 ? INFINITY : NAN;
+    else if (e == 0)
+        v = ldexpf((float)m, 1 - bias - mb); /* subnormal: m * 2^(1 - bias - mb) */
+    else
+        v = ldexpf((float)((1 << mb) + m), e - bias - mb);
+    return sign ? -v : v;
+}
+
+void gg_oracle_grouped_gemm_fp8(int fmt, int group_num, int64_t n, int64_t k, const int64_t *group_m,
+                                const uint8_t *x, const uint8_t *w, float x_scale, const float *w_scale,
+                                float *out) {
+    float lut[256];
+    for (int i = 0; i < 256; ++i)
+        lut[i] = gg_oracle_fp8_to_f32(fmt, (uint8_t)i);
+    int64_t row0 = 0;
+    for (int g = 0; g < group_num; ++g) {
+        const int64_t  m  = group_m[g];
+        const uint8_t *wg = w + (int64_t)g * n * k;
+        const float    sc = x_scale * w_scale[g];
+#pragma omp parallel for schedule(static)
+        for (int64_t r = row0; r < row0 + m; ++r) {
+            const uint8_t *xr = x + r * k;
+            for (int64_t c = 0; c < n; ++c) {
+                const uint8_t *wr = wg + c * k;
+                float          s  = 0.f;
+                for (int64_t t = 0; t < k; ++t)
+                    s += lut[xr[t]] * lut[wr[t]];
+                out[r * n + c] = s * sc;
+            }
+        }
+        row0 += m;
+    }
+}
+
 static inline float dec(int dtype, uint16_t h) {
     return dtype == 0 ? gg_oracle_bf16_to_f32(h) : gg_oracle_f16_to_f32(h);
 }

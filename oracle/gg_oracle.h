@@ -16,6 +16,11 @@
  *                           hipblaslt_grouped_gemm.cu:80-97: grad_c * b = grad_a, a^T * grad_c =
  *                           grad_b) and its zero output for an empty group's weight gradient
  *                           (:206-214); fp32 sums like gg_oracle_grouped_gemm
+ *   gg_oracle_fp8_to_f32 / gg_oracle_grouped_gemm_fp8
+ *                           the fp8 grouped GEMM with tensor-wise scales of the vendored
+ *                           Primus-Turbo (third_party/primus_turbo/include/primus_turbo/
+ *                           grouped_gemm.h:72-74, 120-123: aq_ptr / bq_ptr); fp8 formats are the
+ *                           OCP e4m3 (bias 7, no infinities, 0x7f/0xff NaN) and e5m2 (bias 15)
  *   gg_oracle_make_samples  bench/bench_main.cpp:210-227 (4 corners + 256 random per group,
  *                           one std::mt19937_64(1234) engine for all groups)
  *   gg_oracle_check         bench/bench_main.cpp:235-271 (|got-ref| <= atol + rtol*|ref|, NaN is a
@@ -24,7 +29,8 @@
  *   gg_mt19937_64_*         the C++ standard's std::mt19937_64 ([rand.predef]), which the
  *                           reference's sampler uses
  *
- * Pinning (tests/test_oracle.py): mt19937_64 against the standard's known answer and against
+ * Pinning (tests/test_oracle.py): fp8 decode against torch's float8_e4m3fn / float8_e5m2 on
+ * all 256 patterns; mt19937_64 against the standard's known answer and against
  * libstdc++'s engine (tests/golden/); 16-bit decode/encode against numpy/torch; the GEMM
  * against numpy float64 matmul per group and against exact integer known answers; the
  * sampler and the check by their specification's invariants and hand-built cases.
@@ -66,6 +72,14 @@ void gg_oracle_grouped_dgrad(int dtype, int group_num, int64_t n, int64_t k, con
  * out: [group_num, n, k]. */
 void gg_oracle_grouped_wgrad(int dtype, int group_num, int64_t n, int64_t k, const int64_t *group_m,
                              const uint16_t *grad_out, const uint16_t *x, float *out);
+
+/* fp8 (fmt 0: e4m3, 1: e5m2) -> fp32, exact. */
+float gg_oracle_fp8_to_f32(int fmt, uint8_t b);
+
+/* out[row, col] (fp32) = (sum_k x[row, k] * w[g, col, k]) * x_scale * w_scale[g], fp8 inputs. */
+void gg_oracle_grouped_gemm_fp8(int fmt, int group_num, int64_t n, int64_t k, const int64_t *group_m,
+                                const uint8_t *x, const uint8_t *w, float x_scale, const float *w_scale,
+                                float *out);
 
 /* Same dot products for rows [row_begin, row_end) of one group only (out: [rows, n]).
  * The bounded CPU baseline sample. */

@@ -34,6 +34,10 @@ def lib() -> ctypes.CDLL:
             "gg_oracle_f32_to_f16": (ctypes.c_uint16, [ctypes.c_float]),
             "gg_oracle_decode": (None, [ctypes.c_int, _P16, _PF, ctypes.c_size_t]),
             "gg_oracle_encode": (None, [ctypes.c_int, _PF, _P16, ctypes.c_size_t]),
+            "gg_oracle_fp8_to_f32": (ctypes.c_float, [ctypes.c_int, ctypes.c_uint8]),
+            "gg_oracle_grouped_gemm_fp8": (None, [ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_int64,
+                                                  ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                                  ctypes.c_float, ctypes.c_void_p, ctypes.c_void_p]),
             "gg_oracle_grouped_dgrad": (None, [ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_int64,
                                                ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                                ctypes.c_void_p]),
@@ -90,6 +94,26 @@ def grouped_gemm(dtype: int, x: np.ndarray, w: np.ndarray, group_m) -> np.ndarra
     out = np.zeros((int(gm.sum()), n), dtype=np.float32)
     lib().gg_oracle_grouped_gemm(dtype, b, n, k, _ptr(gm, ctypes.c_int64), _ptr(x, ctypes.c_uint16),
                                  _ptr(w, ctypes.c_uint16), _ptr(out, ctypes.c_float))
+    return out
+
+
+def fp8_decode(fmt: int, b: np.ndarray) -> np.ndarray:
+    """fp8 bytes (fmt 0: e4m3, 1: e5m2) -> fp32."""
+    lut = np.array([lib().gg_oracle_fp8_to_f32(fmt, i) for i in range(256)], dtype=np.float32)
+    return lut[np.asarray(b, dtype=np.uint8)]
+
+
+def grouped_gemm_fp8(fmt: int, x: np.ndarray, w: np.ndarray, group_m, x_scale: float, w_scale) -> np.ndarray:
+    """fp32 out [sum(M), N] = (x_g @ w_g^T) * x_scale * w_scale[g] from fp8 bytes x [sum(M), K],
+    w [B, N, K]."""
+    x = np.ascontiguousarray(x, dtype=np.uint8)
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    b, n, k = w.shape
+    gm = np.ascontiguousarray(group_m, dtype=np.int64)
+    ws = np.ascontiguousarray(w_scale, dtype=np.float32)
+    out = np.zeros((int(gm.sum()), n), dtype=np.float32)
+    lib().gg_oracle_grouped_gemm_fp8(fmt, b, n, k, gm.ctypes.data, x.ctypes.data, w.ctypes.data, float(x_scale),
+                                     ws.ctypes.data, out.ctypes.data)
     return out
 
 

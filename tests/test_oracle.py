@@ -209,6 +209,34 @@ def test_backward_exact_integers(oracle):
     assert (gi * out).sum() == (gw * wi).sum() == (gx * xi).sum()
 
 
+@pytest.mark.parametrize("fmt,tdt", [(0, torch.float8_e4m3fn), (1, torch.float8_e5m2)])
+def test_fp8_decode_all_patterns(oracle, fmt, tdt):
+    """Every fp8 byte against torch's OCP float8 types (NaN patterns included)."""
+    b = np.arange(256, dtype=np.uint8)
+    got = oracle.fp8_decode(fmt, b)
+    want = torch.from_numpy(b).view(tdt).float().numpy()
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.array_equal(got[~np.isnan(got)], want[~np.isnan(want)])
+
+
+@pytest.mark.parametrize("fmt", [0, 1])
+def test_grouped_gemm_fp8_vs_numpy_float64(oracle, fmt):
+    """fp8 GEMM with tensor-wise scales vs numpy float64 on the decoded inputs."""
+    rng = np.random.default_rng(3 + fmt)
+    group_m, n, k = [5, 0, 40, 17], 24, 160
+    tdt = torch.float8_e4m3fn if fmt == 0 else torch.float8_e5m2
+    x = torch.from_numpy(rng.standard_normal((sum(group_m), k)).astype(np.float32)).to(tdt).view(torch.uint8).numpy()
+    w = torch.from_numpy(rng.standard_normal((len(group_m), n, k)).astype(np.float32)).to(tdt).view(torch.uint8).numpy()
+    ws = np.array([0.5, 2.0, 0.25, 3.0], dtype=np.float32)
+    got = oracle.grouped_gemm_fp8(fmt, x, w, group_m, 1.5, ws)
+    xf, wf = oracle.fp8_decode(fmt, x).astype(np.float64), oracle.fp8_decode(fmt, w).astype(np.float64)
+    row = 0
+    for g, m in enumerate(group_m):
+        want = (xf[row:row + m] @ wf[g].T) * 1.5 * ws[g]
+        np.testing.assert_allclose(got[row:row + m], want, rtol=1e-4, atol=1e-4 * np.sqrt(k))
+        row += m
+
+
 def test_group_rows_and_sampled_agree_with_full(oracle):
     dt, group_m, n, k = 0, [40, 9, 33], 56, 200
     x, w = _rand_problem(dt, group_m, n, k, seed=5)
