@@ -394,7 +394,7 @@ int gg_prepare_fp8(int dtype, int group_num, int64_t n, int64_t k, const int64_t
         plan->detail = std::string("mi355x fp8 ") + (dtype == GG_DTYPE_FP8_E4M3 ? "e4m3" : "e5m2") +
                        " persistent 256x256x128 bf16-out grid=" + std::to_string(plan->grid) +
                        " tiles=" + std::to_string(plan->total_tiles) + " xcd=" + std::to_string(a.n_xcd) +
-                       " per-tile";
+                       (gg::uses_cross_tile(a, plan->grid, plan->mode) ? " cross-tile" : " per-tile");
     } else {
         plan->detail = std::string("mi355x fp8: no launch (") +
                        (has_output ? "K = 0, zero fill" : "empty output") + ")";

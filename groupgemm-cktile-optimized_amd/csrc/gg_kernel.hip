@@ -145,8 +145,10 @@ constexpr int reads_per_frag(bool mn) { return mn ? 4 : 2; }
 constexpr int kBarRow = 7; // the step's barrier follows MFMA Plan::bar of this row
 static_assert(GG_BAR_IDX >= 5 && GG_BAR_IDX <= 11 && GG_BAR_IDX % 2 == 1, "barrier slot");
 
+constexpr int plan_epi(int mi, int idx);
 template <int NA, int NB> struct Plan {
     static constexpr int slots = 16, early = kEarlyA;
+    static constexpr int epi(int mi, int idx) { return plan_epi(mi, idx); }
     // The w fragments of row 7 are read before the barrier, at MFMAs 1 .. 2 NB - 1.
     static constexpr int bar = GG_BAR_IDX > 2 * NB + 1 ? GG_BAR_IDX : 2 * NB + 1;
     static constexpr int row0_first = GG_ROW0_AT_BAR ? bar : bar + 2;
@@ -259,6 +261,11 @@ struct Plan8 {
         return (mi >= 3 && mi < 7 && (idx == 0 || idx == 4)) ? 2 * (mi - 3) + idx / 4 : -1;
     }
     static constexpr int load_a_early(int mi, int idx) { return (mi == 7 && idx == 6) ? 0 : -1; }
+    // Cross-tile first step: store s of the previous tile's row block mi+1 after MFMA 2, 3, 6, 7
+    // of row mi (a 32-cycle fp8 MFMA leaves room for a store next to a read).
+    static constexpr int epi(int mi, int idx) {
+        return mi < 7 ? (idx == 2 ? 0 : idx == 3 ? 1 : idx == 6 ? 2 : idx == 7 ? 3 : -1) : -1;
+    }
     static constexpr int dma_kind(int mi, int idx) {
         return load_a(mi, idx) >= 0 ? 1 : load_b(mi, idx) >= 0 ? 2 : load_a_early(mi, idx) >= 0 ? 3 : 0;
     }
@@ -431,7 +438,6 @@ grouped_gemm_kernel(const KernelArgs args) {
     constexpr int  KS   = kRowBytes / ES;    // contraction values per K step
     using P = std::conditional_t<F8, Plan8, Plan<reads_per_frag(A_MN), reads_per_frag(B_MN)>>;
     static_assert(!(CROSS && MODE == kWgrad), "wgrad has a K-step count per group");
-    static_assert(!(CROSS && F8), "fp8 runs the per-tile variant");
     static_assert(!(F8 && F16), "fp8 writes bf16");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kLdsBytes];
     typedef __attribute__((address_space(3))) uint8_t lds_u8;
@@ -748,11 +754,17 @@ grouped_gemm_kernel(const KernelArgs args) {
     //   Z_A: lanes l%16 < 8 keep X_2h (row l%16), lanes l%16 >= 8 take X_2h+1 of lane l-8;
     //   Z_B: lanes l%16 >= 8 keep X_2h+1 (row l%16), lanes l%16 < 8 take X_2h of lane l+8.
     // Z_A holds rows 0-7 and Z_B rows 8-15 of the block, columns 64h..64h+63.
-    auto pack_chunk = [&](auto r, auto j) -> u32x4 {
+    float prev_scale = 1.0f; // fp8: scale of the tile whose accumulators the fused stores take
+    auto  pack_chunk = [&](auto r, auto j) -> u32x4 {
         // reads of these accumulators may not move above this point
         asm volatile("" : "+a"(acc[r][2 * j]), "+a"(acc[r][2 * j + 1]));
-        const u32x2 p0 = pack4<F16>(acc[r][2 * j]);
-        const u32x2 p1 = pack4<F16>(acc[r][2 * j + 1]);
+        f32x4 v0 = acc[r][2 * j], v1 = acc[r][2 * j + 1];
+        if constexpr (F8) {
+            v0 *= prev_scale;
+            v1 *= prev_scale;
+        }
+        const u32x2 p0 = pack4<F16>(v0);
+        const u32x2 p1 = pack4<F16>(v1);
         const auto  s0 = __builtin_amdgcn_permlane16_swap(p0[0], p1[0], false, false);
         const auto  s1 = __builtin_amdgcn_permlane16_swap(p0[1], p1[1], false, false);
         return u32x4{s0[0], s1[0], s0[1], s1[1]};
@@ -886,8 +898,8 @@ grouped_gemm_kernel(const KernelArgs args) {
                     read_frag.template operator()<A_MN, P::read_a_row0(mi, idx)>(fa[0], a_rd[NX], ic<0>{});
                     sched_fence();
                 }
-                if constexpr (FUSE && plan_epi(mi, idx) >= 0)
-                    epi_store(ic<mi + 1>{}, ic<plan_epi(mi, idx)>{});
+                if constexpr (FUSE && P::epi(mi, idx) >= 0)
+                    epi_store(ic<mi + 1>{}, ic<P::epi(mi, idx)>{});
                 if constexpr (dk == 1)
                     dma_go(A_OP{}, src_a1, ic<dj>{}, chk{});
                 else if constexpr (dk == 2)
@@ -953,8 +965,9 @@ grouped_gemm_kernel(const KernelArgs args) {
             {
                 // The next tile's first steps are in flight or in LDS, B(0) of it is in the w
                 // register set T % 2 and row 0 of A(0) in fa[0]: continue without a prologue.
-                prev_crs = c_rsrc(cur);
-                prev_n   = cur.n_valid;
+                prev_crs   = c_rsrc(cur);
+                prev_n     = cur.n_valid;
+                prev_scale = cur.scale;
                 cur      = nxt;
                 t        = t_next;
                 rot_a    = (rot_a + T) & 1;
@@ -1077,7 +1090,7 @@ template <bool F16> __global__ void fill_randn_kernel(uint16_t *p, size_t n, uin
 } // namespace
 
 bool uses_cross_tile(const KernelArgs &args, int grid, int mode) {
-    if (mode == kWgrad || mode_f8(mode))
+    if (mode == kWgrad)
         return false;
     // Workgroups with a single tile gain nothing from the cross-tile pipeline.
     // (a device-built table's tile count is unknown on the host: take the cross-tile variant,
@@ -1088,7 +1101,7 @@ bool uses_cross_tile(const KernelArgs &args, int grid, int mode) {
 
 template <bool F16, int MODE>
 void launch_mode(const KernelArgs &args, bool cross, dim3 g, dim3 b, hipStream_t stream) {
-    if constexpr (MODE == kWgrad || mode_f8(MODE))
+    if constexpr (MODE == kWgrad)
         hipLaunchKernelGGL((grouped_gemm_kernel<F16, false, MODE>), g, b, 0, stream, args);
     else if (cross)
         hipLaunchKernelGGL((grouped_gemm_kernel<F16, true, MODE>), g, b, 0, stream, args);

@@ -50,7 +50,7 @@ SMALL = [
     (1, [256, 256], 512, 256),          # e5m2
     (0, [1, 7, 64, 65], 8, 16),         # tiny: N = 8, K = 16 (one partial step)
     (0, [700, 300], 1000, 144),         # K % 128 = 16
-    (1, [2000, 30, 900], 776, 1040),    # several tiles per workgroup, K % 128 = 16
+    (1, [2000, 30, 900], 776, 1040),    # M tails, K % 128 = 16
 ]
 
 
@@ -100,6 +100,30 @@ def test_fp8_large_vs_torch_fp32(pkg, fmt, b, m, n, k):
         assert not torch.isnan(got).any(), f"group {g}: unwritten outputs"
         nbad = int(((got - ref).abs() > ATOL + RTOL * ref.abs()).sum())
         assert nbad == 0, f"group {g}: {nbad} outputs off"
+
+
+@pytest.mark.parametrize("fmt", [0, 1])
+def test_fp8_cross_tile_ragged(pkg, fmt):
+    """More tiles than workgroups (the cross-tile variant: a tile's stores are issued in the next
+    tile's first K step, scaled by the finished tile's scales) with ragged and empty groups, an N
+    tail and a partial last K step; per-group scales change at every group boundary."""
+    gm, n, k = [1500, 0, 77, 3000, 2513], 2056, 1040
+    print(f"[fp8] cross ragged: fmt={fmt} group_m={gm} N={n} K={k}", flush=True)
+    x = _fp8((sum(gm), k), fmt, 7)
+    w = _fp8((len(gm), n, k), fmt, 8)
+    ws = [0.25 * (g + 1) for g in range(len(gm))]
+    out, detail = _run(pkg, fmt, gm, x, w, 1.5, ws)
+    assert "cross-tile" in detail, detail
+    xd, wd = x.to(DEV).float(), w.to(DEV).float()
+    row = 0
+    for g, m in enumerate(gm):
+        if m:
+            ref = (xd[row:row + m] @ wd[g].t().contiguous()) * (1.5 * ws[g])
+            got = out[row:row + m].float()
+            assert not torch.isnan(got).any(), f"group {g}: unwritten outputs"
+            nbad = int(((got - ref).abs() > ATOL + RTOL * ref.abs()).sum())
+            assert nbad == 0, f"group {g}: {nbad} outputs off"
+        row += m
 
 
 def test_fp8_torch_wrapper(pkg):
