@@ -5,6 +5,10 @@ MoE gate+up projection config: B=8 groups x M=4096 tokens, N=4096, K=7168, bf16,
 groups, x and w ~ N(0,1) from the seeded generator (x seed 1, w seed 2), inputs resident in
 HBM before timing (the reference's protocol, bench/bench_main.cpp:436-501).
 
+--op runs another pass of the same workload instead of the forward GEMM (default: forward, the
+headline): dgrad (grad_x = grad_out @ w[g]), wgrad (grad_w[g] = grad_out[g]^T @ x[g]), or the
+fp8 forward (e4m3 / e5m2 inputs, unit tensor-wise scales, bf16 out). Same FLOPs, 2 sum(M) N K.
+
 Prints ONE JSON line on stdout. Besides the driver's fields it carries:
   roofline     the kernel against the dense bf16 MFMA peak (2.5 PFLOP/s): achieved = FLOPs
                per launch / mean launch duration from HIP events on the launch stream;
@@ -39,6 +43,8 @@ WORKLOADS = {
 }
 HEADLINE = "moe_gate_up_b8_m4096_n4096_k7168_bf16"
 MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16/fp16
+FP8_PEAK_TFLOPS = 5000.0  # MI355X dense fp8
+OPS = ("fwd", "dgrad", "wgrad", "fp8_e4m3", "fp8_e5m2")
 
 
 def log(*a):
@@ -90,12 +96,55 @@ def cpu_baseline(oracle, x, w, group_m, dtype, n, k, target_s):
     }
 
 
+def other_pass(pkg, op, dtype, b, m, n, k, sh, dev):
+    """Plan for a non-headline pass over the workload's forward shapes (x [sum(M), K],
+    w [B, N, K], grad_out [sum(M), N]). Returns (plan, flops, buffers to keep alive)."""
+    import torch
+
+    td = torch.bfloat16 if dtype == 0 else torch.float16
+    rows = b * m
+    group_m = [m] * b
+
+    def randn(shape, seed):
+        t = torch.empty(shape, dtype=td, device=dev)
+        pkg.fill_randn(pkg.DType(dtype), t.data_ptr(), t.numel(), seed, sh)
+        return t
+
+    if op == "dgrad":  # grad_x [sum(M), K] = grad_out [sum(M), N] @ w[g] [N, K]
+        gy, w = randn((rows, n), 3), randn((b, n, k), 2)
+        out = torch.zeros((rows, k), dtype=td, device=dev)
+        plan = pkg.BackwardPlan("dgrad", pkg.DType(dtype), n, k, group_m, gy.data_ptr(), w.data_ptr(),
+                                out.data_ptr(), sh)
+        keep = (gy, w, out)
+    elif op == "wgrad":  # grad_w [B, N, K] = grad_out[g]^T [N, M] @ x[g] [M, K]
+        gy, x = randn((rows, n), 3), randn((rows, k), 1)
+        out = torch.zeros((b, n, k), dtype=td, device=dev)
+        plan = pkg.BackwardPlan("wgrad", pkg.DType(dtype), n, k, group_m, gy.data_ptr(), x.data_ptr(),
+                                out.data_ptr(), sh)
+        keep = (gy, x, out)
+    else:  # fp8 forward: N(0,1) inputs rounded to the fp8 format, unit scales, bf16 out
+        fdt = torch.float8_e4m3fn if op == "fp8_e4m3" else torch.float8_e5m2
+        x = randn((rows, k), 1).to(fdt)
+        w = randn((b, n, k), 2).to(fdt)
+        xs = torch.ones(1, dtype=torch.float32, device=dev)
+        ws = torch.ones(b, dtype=torch.float32, device=dev)
+        out = torch.zeros((rows, n), dtype=torch.bfloat16, device=dev)
+        fmt = pkg.DType.FP8_E4M3 if op == "fp8_e4m3" else pkg.DType.FP8_E5M2
+        plan = pkg.Fp8Plan(fmt, n, k, group_m, x.data_ptr(), w.data_ptr(), xs.data_ptr(), ws.data_ptr(),
+                           out.data_ptr(), sh)
+        keep = (x, w, xs, ws, out)
+    torch.cuda.synchronize(dev)
+    return plan, plan.flop, keep
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default=HEADLINE, choices=sorted(WORKLOADS))
+    ap.add_argument("--op", default="fwd", choices=OPS,
+                    help="pass to time (fwd is the headline; the others print no cpu_baseline)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
@@ -125,20 +174,24 @@ def main():
     torch.cuda.set_device(dev)
     td = torch.bfloat16 if dtype == 0 else torch.float16
     group_m = [m] * b
-    x = torch.empty((b * m, k), dtype=td, device=dev)
-    w = torch.empty((b, n, k), dtype=td, device=dev)
-    out = torch.zeros((b * m, n), dtype=td, device=dev)
     stream = torch.cuda.current_stream(dev)
     sh = stream.cuda_stream
-    pkg.fill_randn(pkg.DType(dtype), x.data_ptr(), x.numel(), 1, sh)
-    pkg.fill_randn(pkg.DType(dtype), w.data_ptr(), w.numel(), 2, sh)
-    prob = pkg.GroupedGemmProblem(pkg.DType(dtype), b, n, k, group_m, x.data_ptr(), w.data_ptr(),
-                                  out.data_ptr())
-    be = pkg.make_mi355x_backend()
-    why = be.prepare(prob, sh)
-    if why:
-        raise SystemExit(f"mi355x backend cannot run {args.workload}: {why}")
-    log(f"[bench] {args.workload}: {be.detail()}")
+    if args.op == "fwd":
+        x = torch.empty((b * m, k), dtype=td, device=dev)
+        w = torch.empty((b, n, k), dtype=td, device=dev)
+        out = torch.zeros((b * m, n), dtype=td, device=dev)
+        pkg.fill_randn(pkg.DType(dtype), x.data_ptr(), x.numel(), 1, sh)
+        pkg.fill_randn(pkg.DType(dtype), w.data_ptr(), w.numel(), 2, sh)
+        prob = pkg.GroupedGemmProblem(pkg.DType(dtype), b, n, k, group_m, x.data_ptr(), w.data_ptr(),
+                                      out.data_ptr())
+        be = pkg.make_mi355x_backend()
+        why = be.prepare(prob, sh)
+        if why:
+            raise SystemExit(f"mi355x backend cannot run {args.workload}: {why}")
+        flops = prob.flops()
+    else:
+        be, flops, keep = other_pass(pkg, args.op, dtype, b, m, n, k, sh, dev)
+    log(f"[bench] {args.workload} {args.op}: {be.detail()}")
 
     for _ in range(args.warmup):
         be.run(sh)
@@ -151,25 +204,30 @@ def main():
     stop.record(stream)
     torch.cuda.synchronize(dev)
     ms = start.elapsed_time(stop) / args.steps
-    flops = prob.flops()
     tflops = flops / (ms * 1e-3) / 1e12
     log(f"[bench] {args.steps} steps, {ms:.4f} ms/step, {tflops:.1f} TFLOPS")
 
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", f"hbm_traffic_{args.workload}.json")
+    suffix = "" if args.op == "fwd" else f"_{args.op}"
+    tpath = os.path.join(ROOT, "profiles", f"hbm_traffic_{args.workload}{suffix}.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
 
     cpu = None
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and args.op == "fwd":
         log(f"[bench] cpu baseline (~{args.cpu_seconds:.0f} s of CPU work)...")
         cpu = cpu_baseline(entry.load_oracle(), x, w, group_m, dtype, n, k, args.cpu_seconds)
         log(f"[bench] cpu baseline: {cpu['value']} TFLOPS on {cpu['cores']} threads")
     be.release()
 
+    fp8 = args.op.startswith("fp8")
+    peak = FP8_PEAK_TFLOPS if fp8 else MFMA_PEAK_TFLOPS
+    metric = "grouped-GEMM TFLOPS (bf16) + % of MFMA peak, 1 MI355X, per config"
+    if args.op != "fwd":
+        metric = f"grouped-GEMM {args.op} TFLOPS + % of MFMA peak, 1 MI355X"
     line = {
-        "metric": "grouped-GEMM TFLOPS (bf16) + % of MFMA peak, 1 MI355X, per config",
+        "metric": metric,
         "value": round(tflops, 2),
         "unit": "TFLOPS",
         "n_gpus": 1,
@@ -179,13 +237,13 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16" if dtype == 0 else "fp16",
+        "dtype": args.op[4:] if fp8 else "bf16" if dtype == 0 else "fp16",
         "data": "synthetic (seeded N(0,1), balanced groups)",
-        "config": {"workload": args.workload, "groups": b, "m_per_group": m, "n": n, "k": k,
-                   "layout": "RCR", "parallelism": "single GPU"},
-        "pct_of_mfma_peak": round(100.0 * tflops / MFMA_PEAK_TFLOPS, 2),
-        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
+        "config": {"workload": args.workload, "op": args.op, "groups": b, "m_per_group": m, "n": n,
+                   "k": k, "layout": "RCR", "parallelism": "single GPU"},
+        "pct_of_mfma_peak": round(100.0 * tflops / peak, 2),
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": peak,
+                     "unit": "TFLOP/s", "frac": round(tflops / peak, 4),
                      "traffic": traffic},
         "cpu_baseline": cpu,
     }
