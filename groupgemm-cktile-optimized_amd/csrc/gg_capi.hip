@@ -9,6 +9,7 @@
 #include <algorithm>
 #include <cstdint>
 #include <cstdio>
+#include <cstdlib>
 #include <new>
 #include <string>
 #include <vector>
@@ -36,6 +37,7 @@ struct gg_plan {
     const int64_t      *d_lens      = nullptr;
     const int64_t      *d_offs      = nullptr;
     gg::TableHeader    *d_header    = nullptr; // follows the table in the d_groups allocation
+    float              *d_ws        = nullptr; // split-K partial sums (args.ws)
 };
 
 namespace {
@@ -110,6 +112,69 @@ void fill_args(gg_plan *plan, int n_xcd) {
     a.m_out     = 0;
     a.x_scale   = nullptr;
     a.w_scale   = nullptr;
+    a.splits    = 1;
+    a.ws        = nullptr;
+}
+
+// Split-K for problems whose tiles cannot fill the GPU (fewer than half as many tiles as CUs):
+// each tile's K steps are cut into S ranges computed by different workgroups, which write fp32
+// partial sums (256 KB per unit) that a second kernel adds in split order (deterministic) and
+// converts. S minimises a launch-time model, in microseconds, fitted to MI355X timings of
+// one-round problems (24-64 tiles, 22-256 K steps):
+//   S = 1: k_tiles * kStepUs (one round of tiles)
+//   S > 1: ceil(k_tiles / S) * kStepUs + kSplitUs + S * tiles * kSlabUs
+// within one round (S * tiles <= CUs) and at least kMinSplitSteps K steps per range, taken only
+// when it predicts at least kMinSplitGain (the cost of the partial sums grows faster than
+// linearly near a full round of units, so small predicted gains are often losses).
+// GG_SPLIT_K=<S> in the environment forces S (clamped to [1, k_tiles]; 1 turns split-K off).
+constexpr double kStepUs        = 1.2;  // one K step of a 256 x 256 tile
+constexpr double kSplitUs       = 3.0;  // second launch and its latency
+constexpr double kSlabUs        = 0.15; // one unit's 256 KB of partial sums, written and read back
+constexpr int    kMinSplitSteps = 4;
+constexpr double kMinSplitGain  = 0.15;
+
+int choose_splits(int tiles, int k_tiles, int cus) {
+    if (const char *env = std::getenv("GG_SPLIT_K")) {
+        const long v = std::strtol(env, nullptr, 10);
+        if (v >= 1)
+            return static_cast<int>(std::min<long>(v, k_tiles));
+    }
+    const int max_s = std::min(cus / std::max(tiles, 1), k_tiles / kMinSplitSteps);
+    const double unsplit = k_tiles * kStepUs;
+    int          best    = 1;
+    double       cost    = unsplit;
+    for (int sp = 2; sp <= max_s; ++sp) {
+        const double c = ((k_tiles + sp - 1) / sp) * kStepUs + kSplitUs + double(sp) * tiles * kSlabUs;
+        if (c < cost) {
+            cost = c;
+            best = sp;
+        }
+    }
+    return cost <= (1.0 - kMinSplitGain) * unsplit ? best : 1;
+}
+
+// Picks the plan's split count (plan->args filled, k_tiles set) and allocates the partial sums.
+int setup_split_k(gg_plan *plan, const hipDeviceProp_t &prop) {
+    gg::KernelArgs &a  = plan->args;
+    const int       sp = choose_splits(plan->total_tiles, a.k_tiles, prop.multiProcessorCount);
+    if (sp <= 1)
+        return GG_OK;
+    const size_t bytes = size_t(sp) * size_t(plan->total_tiles) * 262144;
+    const hipError_t e = hipMalloc(&plan->d_ws, bytes);
+    if (e != hipSuccess)
+        return hip_fail(e, "split-K workspace allocation");
+    a.splits    = sp;
+    a.ws        = plan->d_ws;
+    plan->grid  = static_cast<int>(std::min<int64_t>(prop.multiProcessorCount, int64_t(sp) * plan->total_tiles));
+    return GG_OK;
+}
+
+void free_plan(gg_plan *plan) {
+    if (plan->d_groups != nullptr)
+        (void)hipFree(plan->d_groups);
+    if (plan->d_ws != nullptr)
+        (void)hipFree(plan->d_ws);
+    delete plan;
 }
 
 } // namespace
@@ -184,12 +249,17 @@ int gg_prepare(int dtype, int group_num, int64_t n, int64_t k, const int64_t *gr
         gg::KernelArgs &a = plan->args;
         a.total_tiles     = plan->total_tiles;
         a.d_total         = nullptr;
+        if (setup_split_k(plan, prop) != GG_OK) {
+            free_plan(plan);
+            return GG_ERR_HIP;
+        }
         plan->detail      = "mi355x persistent 256x256x64 " +
                        std::string(dtype == GG_DTYPE_BF16 ? "bf16" : "fp16") +
                        " grid=" + std::to_string(plan->grid) +
                        " tiles=" + std::to_string(plan->total_tiles) +
                        " xcd=" + std::to_string(a.n_xcd) +
-                       (gg::uses_cross_tile(a, plan->grid) ? " cross-tile" : " per-tile");
+                       (gg::uses_cross_tile(a, plan->grid) ? " cross-tile" : " per-tile") +
+                       (a.splits > 1 ? " split-k=" + std::to_string(a.splits) : "");
     } else {
         plan->detail = "mi355x: no launch (" +
                        std::string(has_output ? "K = 0, zero fill" : "empty output") + ")";
@@ -297,11 +367,17 @@ static int prepare_backward(int mode, int dtype, int group_num, int64_t n, int64
         ka.ldb             = static_cast<int>(k);
         ka.m_out           = mode == 2 ? static_cast<int>(n) : 0;
         ka.k_tiles         = mode == 1 ? static_cast<int>(gg::cdiv(n, gg::kTileK)) : 1;
+        // wgrad's K steps differ per group: no split
+        if (mode == 1 && setup_split_k(plan, prop) != GG_OK) {
+            free_plan(plan);
+            return GG_ERR_HIP;
+        }
         plan->detail       = std::string("mi355x ") + what + " persistent 256x256x64 " +
                        std::string(dtype == GG_DTYPE_BF16 ? "bf16" : "fp16") +
                        " grid=" + std::to_string(plan->grid) + " tiles=" + std::to_string(plan->total_tiles) +
                        " xcd=" + std::to_string(ka.n_xcd) +
-                       (gg::uses_cross_tile(ka, plan->grid, mode) ? " cross-tile" : " per-tile");
+                       (gg::uses_cross_tile(ka, plan->grid, mode) ? " cross-tile" : " per-tile") +
+                       (ka.splits > 1 ? " split-k=" + std::to_string(ka.splits) : "");
     } else {
         plan->detail = std::string("mi355x ") + what + ": no launch (" +
                        (has_output ? "empty contraction, zero fill" : "empty output") + ")";
@@ -391,10 +467,15 @@ int gg_prepare_fp8(int dtype, int group_num, int64_t n, int64_t k, const int64_t
         a.k_tiles         = static_cast<int>(gg::cdiv(k, 128)); // 128 fp8 values per K step
         a.x_scale         = x_scale;
         a.w_scale         = w_scale;
+        if (setup_split_k(plan, prop) != GG_OK) {
+            free_plan(plan);
+            return GG_ERR_HIP;
+        }
         plan->detail = std::string("mi355x fp8 ") + (dtype == GG_DTYPE_FP8_E4M3 ? "e4m3" : "e5m2") +
                        " persistent 256x256x128 bf16-out grid=" + std::to_string(plan->grid) +
                        " tiles=" + std::to_string(plan->total_tiles) + " xcd=" + std::to_string(a.n_xcd) +
-                       (gg::uses_cross_tile(a, plan->grid, plan->mode) ? " cross-tile" : " per-tile");
+                       (gg::uses_cross_tile(a, plan->grid, plan->mode) ? " cross-tile" : " per-tile") +
+                       (a.splits > 1 ? " split-k=" + std::to_string(a.splits) : "");
     } else {
         plan->detail = std::string("mi355x fp8: no launch (") +
                        (has_output ? "K = 0, zero fill" : "empty output") + ")";
@@ -506,19 +587,21 @@ int gg_run(const gg_plan *plan, void *stream) {
         }
         return GG_OK;
     }
-    const hipError_t e =
-        gg::launch_grouped_gemm(plan->args, plan->dtype == GG_DTYPE_FP16, plan->grid, s, plan->mode);
+    hipError_t e = gg::launch_grouped_gemm(plan->args, plan->dtype == GG_DTYPE_FP16, plan->grid, s, plan->mode);
     if (e != hipSuccess)
         return hip_fail(e, "grouped GEMM launch");
+    if (plan->args.splits > 1) {
+        e = gg::launch_split_reduce(plan->args, plan->dtype == GG_DTYPE_FP16, s, plan->mode);
+        if (e != hipSuccess)
+            return hip_fail(e, "split-K reduction launch");
+    }
     return GG_OK;
 }
 
 void gg_release(gg_plan *plan) {
     if (plan == nullptr)
         return;
-    if (plan->d_groups != nullptr)
-        (void)hipFree(plan->d_groups);
-    delete plan;
+    free_plan(plan);
 }
 
 const char *gg_plan_detail(const gg_plan *plan) { return plan ? plan->detail.c_str() : ""; }

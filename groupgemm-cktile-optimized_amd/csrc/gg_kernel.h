@@ -34,6 +34,8 @@ struct KernelArgs {
     const float      *w_scale;     // fp8: device scale of each group's w (group_num values)
     const int        *d_total;     // device tile count (device-resident group sizes), or null:
                                    // then total_tiles holds it
+    int               splits;      // split-K: K ranges per tile (1 = none; per-tile variant only)
+    float            *ws;          // split-K: fp32 partial sums, splits * total_tiles * 256 KB
 };
 
 // Header of a device-built group table (follows the group_num entries).
@@ -54,6 +56,11 @@ bool uses_cross_tile(const KernelArgs &args, int grid, int mode = 0);
 // Returns the launch status.
 hipError_t launch_grouped_gemm(const KernelArgs &args, bool fp16, int grid, hipStream_t stream,
                                int mode = 0);
+
+// Split-K second pass: out tile = sum over the splits of the partial sums in args.ws (in split
+// order), times the fp8 scale for modes 3 / 4, converted to 16 bits and stored within the tile's
+// valid rows and columns. Forward and dgrad layouts (out row stride N).
+hipError_t launch_split_reduce(const KernelArgs &args, bool fp16, hipStream_t stream, int mode = 0);
 
 // Build the group table on the device from device-resident group sizes: lens[group_num]
 // (int64 rows) and offs[group_num + 1] (int64 first rows) or null for back-to-back groups.

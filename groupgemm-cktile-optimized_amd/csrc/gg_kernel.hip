@@ -419,6 +419,10 @@ template <bool F16> __device__ __forceinline__ u32x2 pack4(const f32x4 &v) {
 constexpr bool kCrossAllowed  = GG_CROSS_TILE;
 constexpr int  kCrossMinSteps = 4; // the three prefetching steps follow the first
 constexpr int  kStoreCpol     = GG_STORE_CPOL;
+#ifndef GG_PARTIAL_NT
+#define GG_PARTIAL_NT 0
+#endif
+constexpr bool kPartialNt = GG_PARTIAL_NT; // split-K partial sums stored non-temporal (2-5 % slower)
 
 // First step of a cross tile: store s (0-3, see store_line) of the previous tile's row block
 // mi+1 is issued after MFMA 2 + 4s of row mi (row block 0 before the step).
@@ -452,6 +456,10 @@ grouped_gemm_kernel(const KernelArgs args) {
     const int total_tiles = args.d_total != nullptr
                                 ? __builtin_amdgcn_readfirstlane(*args.d_total)
                                 : args.total_tiles;
+    // Work units: a tile, or with split-K (per-tile variant only) one K range of a tile; unit
+    // u = split * total_tiles + tile.
+    const int splits      = CROSS ? 1 : args.splits;
+    const int total_units = total_tiles * splits;
 
     // DMA lane offsets within a tile's K step (the tile origin is in the buffer resource).
     // K-major operand, row stride ld: DMA j covers tile rows j*32 + wave*8 .. +8; lane -> row
@@ -572,12 +580,16 @@ grouped_gemm_kernel(const KernelArgs args) {
         int       m_valid, n_valid;
         int       o0a, o0b;       // MN-major operands: first stored column of the tile
         int       T;              // K steps (wgrad: of the tile's group, at least 1)
+        int       k0;             // first K step (split-K: the split's range), 0 otherwise
+        int       klast;          // the range ends with the problem's last (maybe partial) K step
         float     scale;          // fp8: x scale * w[g] scale (1 otherwise)
     };
     const int bad_off = static_cast<int>(0x80000000u);
     int       g       = 0; // group hint of locate_tile (logical tiles only grow)
     auto      make_tile = [&](int t) -> Tile {
-        const int L = xcd_remap(t, total_tiles, gridDim.x, args.n_xcd);
+        // split-K: one unit per workgroup, no L2 sharing across rounds to arrange
+        const int split = splits > 1 ? t / total_tiles : 0;
+        const int L     = splits > 1 ? t - split * total_tiles : xcd_remap(t, total_tiles, gridDim.x, args.n_xcd);
         int       tm, tn;
         locate_tile(L, args.groups, args.group_num, args.n_tiles, args.band, &g, &tm, &tn,
                     MODE == kWgrad ? args.m_out : 0);
@@ -590,8 +602,12 @@ grouped_gemm_kernel(const KernelArgs args) {
         tl.n_valid         = min(kTileN, N - tn * kTileN);
         const int64_t col0 = static_cast<int64_t>(tn) * kTileN;
         tl.o0a = tl.o0b = 0;
-        tl.T            = T;
-        tl.scale        = 1.0f;
+        // K range of the unit: steps [k0, k1) of k_tiles, balanced over the splits
+        const int k0 = split * args.k_tiles / splits, k1 = (split + 1) * args.k_tiles / splits;
+        tl.T     = k1 - k0;
+        tl.k0    = k0;
+        tl.klast = k1 == args.k_tiles;
+        tl.scale = 1.0f;
         if constexpr (MODE == kWgrad) {
             // A^T = grad_out rows of the group, columns tm*256..; B^T = x rows, columns tn*256..
             const int64_t o0a = static_cast<int64_t>(tm) * kTileM;
@@ -604,7 +620,9 @@ grouped_gemm_kernel(const KernelArgs args) {
             tl.o0b     = static_cast<int>(col0);
             tl.c_ptr   = static_cast<uint16_t *>(args.out) +
                        (static_cast<int64_t>(g) * args.m_out + o0a) * N + col0;
-            tl.T = max(1, static_cast<int>(cdiv(ge.m, kTileK)));
+            tl.T     = max(1, static_cast<int>(cdiv(ge.m, kTileK)));
+            tl.k0    = 0;
+            tl.klast = 1;
         } else {
             tl.m_valid         = min(kTileM, ge.m - tm * kTileM);
             const int64_t row0 = ge.row0 + static_cast<int64_t>(tm) * kTileM;
@@ -635,10 +653,10 @@ grouped_gemm_kernel(const KernelArgs args) {
     const i32x4 rsrc_0 = dma_rsrc(args.x, 0); // zero length: no traffic, the DMA writes zeros
 
     int t = blockIdx.x;
-    if (t >= total_tiles)
+    if (t >= total_units)
         return;
     Tile cur = make_tile(t), nxt = cur;
-    if constexpr (MODE == kWgrad)
+    if constexpr (!CROSS)
         T = __builtin_amdgcn_readfirstlane(cur.T);
     bool cross_next = false; // the DMAs past this tile's last K step fetch `nxt`
 
@@ -670,24 +688,26 @@ grouped_gemm_kernel(const KernelArgs args) {
         if constexpr (decltype(checked)::value) {
             const bool in_cur = kidx < T;
             const int  koff   = in_cur ? kidx : kidx - T;
-            d.rs              = in_cur ? rc : (cross_next ? rn : rsrc_0);
+            // step of the operand: the unit's first step plus koff (the next tile starts at 0)
+            const int kabs = in_cur ? koff + cur.k0 : koff;
+            d.rs           = in_cur ? rc : (cross_next ? rn : rsrc_0);
             if constexpr (MN) {
                 d.so   = 0;
-                d.vadd = koff * kTileK * ld * 2;
+                d.vadd = kabs * kTileK * ld * 2;
                 d.mask = (in_cur ? oc : on) + mn_col >= ld ? bad_off : 0;
             } else {
-                d.so   = koff * kRowBytes;
+                d.so   = kabs * kRowBytes;
                 d.vadd = 0;
-                d.mask = koff == T - 1 ? ktail_bad : 0;
+                d.mask = (koff == T - 1 && cur.klast) ? ktail_bad : 0;
             }
         } else {
             d.rs = rc;
             if constexpr (MN) {
                 d.so   = 0;
-                d.vadd = kidx * kTileK * ld * 2;
+                d.vadd = (kidx + cur.k0) * kTileK * ld * 2;
                 d.mask = oc + mn_col >= ld ? bad_off : 0;
             } else {
-                d.so   = kidx * kRowBytes;
+                d.so   = (kidx + cur.k0) * kRowBytes;
                 d.vadd = 0;
                 d.mask = 0;
             }
@@ -826,6 +846,24 @@ grouped_gemm_kernel(const KernelArgs args) {
         });
         wait_vm_lds_barrier<63>(); // every wave is done reading the staged C
     };
+    // ---- split-K unit: its fp32 accumulators to the workspace slab of unit u (256 KB), in
+    // register order: wave w, block (mi, ni), lane l at float 65536 u + 16384 w + 256 (8 mi + ni)
+    // + 4 l (whole 1 KB per store instruction). split_reduce_kernel adds the slabs of a tile.
+    auto store_partial = [&](int u) {
+        wait_vm_lds_barrier<0>(); // trailing DMAs landed, every wave is done reading LDS
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" ::: "memory"); // MFMA -> VALU read distance
+        float *dst = args.ws + static_cast<int64_t>(u) * 65536 + wave * 16384 + lane * 4;
+        sfor<0, 8>([&](auto mi) {
+            sfor<0, 8>([&](auto ni) {
+                asm volatile("" : "+a"(acc[mi][ni]));
+                f32x4 *d = reinterpret_cast<f32x4 *>(dst + (mi * 8 + ni) * 256);
+                if constexpr (kPartialNt)
+                    __builtin_nontemporal_store(acc[mi][ni], d);
+                else
+                    *d = acc[mi][ni];
+            });
+        });
+    };
 
     // ---- one K step ---------------------------------------------------------------------------
     // SA = kt % 2 (A logical stage, w register set), SB = kt % 3 (B logical stage).
@@ -946,7 +984,7 @@ grouped_gemm_kernel(const KernelArgs args) {
             step.template operator()<0, 0, false, false, false>(kt + 5);
         }
         const int  t_next = t + gridDim.x;
-        const bool more   = t_next < total_tiles;
+        const bool more   = t_next < total_units;
         cross_next        = CROSS && more;
         if (cross_next)
             nxt = make_tile(t_next);
@@ -980,19 +1018,63 @@ grouped_gemm_kernel(const KernelArgs args) {
             }
         }
         if constexpr (!CROSS) {
-            // Store this tile through LDS; the next one starts cold at the top of the loop (the
-            // stores were issued before its DMAs and complete first).
-            epilogue_lds(cur);
+            // Store this tile through LDS (split-K: its partial sums to the workspace); the next
+            // one starts cold at the top of the loop (the stores were issued before its DMAs and
+            // complete first).
+            if (splits > 1)
+                store_partial(t);
+            else
+                epilogue_lds(cur);
             if (!more)
                 return;
             t   = t_next;
             cur = make_tile(t);
-            if constexpr (MODE == kWgrad)
-                T = __builtin_amdgcn_readfirstlane(cur.T);
+            T   = __builtin_amdgcn_readfirstlane(cur.T);
         }
     }
     if constexpr (CROSS)
         epilogue_lds(cur);
+}
+
+// ---------------------------------------------------------------------------------------
+// Split-K reduction: block b takes 256 16-byte positions (b % 64) of logical tile b / 64.
+// Position p of a slab is wave p / 4096, accumulator block (mi, ni) = ((p / 64) % 64) / 8, % 8,
+// lane p % 64, which hold C row 128 (wave / 2) + 16 mi + lane % 16, columns
+// 128 (wave % 2) + 16 ni + 4 (lane / 16) .. +3 of the tile.
+// ---------------------------------------------------------------------------------------
+template <bool F16, bool F8>
+__global__ void __launch_bounds__(256) split_reduce_kernel(const KernelArgs args) {
+    const int tile = blockIdx.x >> 6;
+    int       g    = 0, tm, tn;
+    locate_tile(tile, args.groups, args.group_num, args.n_tiles, args.band, &g, &tm, &tn);
+    const GroupEntry ge   = args.groups[g];
+    const int        p    = (blockIdx.x & 63) * 256 + static_cast<int>(threadIdx.x);
+    const int        wv   = p >> 12, blk = (p >> 6) & 63, l = p & 63;
+    const int        row  = (wv >> 1) * 128 + (blk >> 3) * 16 + (l & 15);
+    const int        col  = (wv & 1) * 128 + (blk & 7) * 16 + (l >> 4) * 4;
+    const int        N    = args.n;
+    const int64_t    slab = static_cast<int64_t>(args.total_tiles) * 65536; // floats per split
+    const float     *src  = args.ws + static_cast<int64_t>(tile) * 65536 + p * 4;
+    // up to 8 loads in flight, then added in split order
+    f32x4 sum = {0.f, 0.f, 0.f, 0.f};
+    for (int i0 = 0; i0 < args.splits; i0 += 8) {
+        f32x4 v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (i0 + j < args.splits)
+                v[j] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(src + (i0 + j) * slab));
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (i0 + j < args.splits)
+                sum = (i0 + j == 0) ? v[j] : sum + v[j];
+    }
+    if constexpr (F8)
+        sum *= args.x_scale[0] * args.w_scale[g];
+    if (row < min(kTileM, ge.m - tm * kTileM) && col < N - tn * kTileN) {
+        uint16_t *o = static_cast<uint16_t *>(args.out) +
+                      (ge.row0 + static_cast<int64_t>(tm) * kTileM + row) * N + static_cast<int64_t>(tn) * kTileN + col;
+        *reinterpret_cast<u32x2 *>(o) = pack4<F16>(sum);
+    }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1095,7 +1177,7 @@ bool uses_cross_tile(const KernelArgs &args, int grid, int mode) {
     // Workgroups with a single tile gain nothing from the cross-tile pipeline.
     // (a device-built table's tile count is unknown on the host: take the cross-tile variant,
     // which also handles workgroups with a single tile)
-    return kCrossAllowed && args.k_tiles >= kCrossMinSteps &&
+    return kCrossAllowed && args.splits <= 1 && args.k_tiles >= kCrossMinSteps &&
            (args.d_total != nullptr || args.total_tiles > grid);
 }
 
@@ -1132,6 +1214,17 @@ hipError_t launch_grouped_gemm(const KernelArgs &args, bool fp16, int grid, hipS
         launch_dtype<true>(args, cross, mode, g, b, stream);
     else
         launch_dtype<false>(args, cross, mode, g, b, stream);
+    return hipGetLastError();
+}
+
+hipError_t launch_split_reduce(const KernelArgs &args, bool fp16, hipStream_t stream, int mode) {
+    const dim3 g(args.total_tiles * 64), b(256);
+    if (mode_f8(mode))
+        hipLaunchKernelGGL((split_reduce_kernel<false, true>), g, b, 0, stream, args);
+    else if (fp16)
+        hipLaunchKernelGGL((split_reduce_kernel<true, false>), g, b, 0, stream, args);
+    else
+        hipLaunchKernelGGL((split_reduce_kernel<false, false>), g, b, 0, stream, args);
     return hipGetLastError();
 }
 

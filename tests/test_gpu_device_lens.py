@@ -6,6 +6,8 @@ group_offs_ptr). Bar: the same bits as a plan built from the same sizes on the h
 within rtol = atol = 1e-2 of fp32 (bench/bench_main.cpp:264-268), rows outside every group left
 untouched, and sizes that do not fit reported, never written.
 """
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -33,13 +35,23 @@ def _inputs(pkg, dt, rows, b, n, k, seed_x=1, seed_w=2):
 
 
 def _host_plan_out(pkg, dt, x, w, group_m):
-    """Output of the host-size plan (gg_prepare) on the same inputs, NaN where unwritten."""
+    """Output of the host-size plan (gg_prepare) on the same inputs, NaN where unwritten. Split-K
+    off, as in a device-size plan (whose tile count is unknown on the host), so that every
+    output has the same fp32 summation order in both."""
     b, n, k = w.shape
     out = torch.full((x.shape[0], n), float("nan"), dtype=x.dtype, device=DEV)
     be = pkg.make_mi355x_backend()
     prob = pkg.GroupedGemmProblem(pkg.DType(dt), b, n, k, list(group_m), x.data_ptr(), w.data_ptr(),
                                   out.data_ptr())
-    assert be.prepare(prob, _stream()) == ""
+    old = os.environ.get("GG_SPLIT_K")
+    os.environ["GG_SPLIT_K"] = "1"
+    try:
+        assert be.prepare(prob, _stream()) == ""
+    finally:
+        if old is None:
+            del os.environ["GG_SPLIT_K"]
+        else:
+            os.environ["GG_SPLIT_K"] = old
     be.run(_stream())
     torch.cuda.synchronize(DEV)
     be.release()
