@@ -466,15 +466,18 @@ grouped_gemm_kernel(const KernelArgs args) {
     // lane/8, logical chunk (lane%8) ^ (lane/8).
     // MN-major operand, row stride ld, stored rows = contraction index: DMA j covers
     // contraction rows 4 (2j + wave/2) .. +4 and tile columns 128 (wave%2) .. +128. In LDS the
-    // step is 128-byte blocks of 4 rows x 16 columns, block (row/4, column/16) at byte
-    // 128 (16 (row/4) + column/16), so the DMA's 1 KB lands at 1024 (4j + wave) as for a
-    // K-major operand; lane -> block column 8 (wave%2) + lane/8, row (lane%8)/2, 8 columns
-    // at 8 (lane%2). A lane's column does not depend on j.
+    // step is 128-byte blocks of 4 rows x 16 columns: block (rb, cb) = (row/4, column/16) sits
+    // at byte 128 (16 rb + (cb ^ ((rb / 2) & 1))), so the DMA's 1 KB lands at 1024 (4j + wave)
+    // as for a K-major operand; lane -> block column (8 (wave%2) + lane/8) ^ (j & 1), row
+    // (lane%8)/2, 8 columns at 8 (lane%2). The column-block swap in every other pair of row
+    // blocks puts the blocks that lanes 0-15 and 16-31 of one transposed read take (row blocks
+    // rb and rb + 2) in different halves of the 256-byte bank window.
     const int ld_row   = lane >> 3;
     const int ld_chunk = (lane & 7) ^ ld_row;
-    const int mn_col   = ((wave & 1) * 8 + (lane >> 3)) * 16 + (lane & 1) * 8;
+    const int mn_c     = (wave & 1) * 8 + (lane >> 3);
+    auto      mn_col   = [&](int jpar) { return (mn_c ^ jpar) * 16 + (lane & 1) * 8; };
     auto      dma_off  = [&](bool mn, int j, int ld) {
-        return mn ? ((4 * (2 * j + (wave >> 1)) + ((lane & 7) >> 1)) * ld + mn_col) * 2
+        return mn ? ((4 * (2 * j + (wave >> 1)) + ((lane & 7) >> 1)) * ld + mn_col(j & 1)) * 2
                   : (j * 32 + wave * 8 + ld_row) * ld * ES + ld_chunk * 16;
     };
     // voff[0]: A's offsets; voff[1]: B's (the forward op shares A's: both row strides are K).
@@ -493,13 +496,18 @@ grouped_gemm_kernel(const KernelArgs args) {
     // kh*4 + lane/16 (one base per k-half). MN-major: ds_read_b64_tr_b16 gives lane i of each
     // 16-lane group column i of 4 consecutive rows when source lane s of the group points at
     // row s/4, column 4 (s%4): lane l reads block (row 8 (l/16) + 4 half + 32 kh, column
-    // 16 blk) at byte 8 (l%16) of it, i.e. base + 16384 kh + 2048 half + 128 blk.
+    // 16 blk) at byte 8 (l%16) of it, i.e. base + 16384 kh + 2048 half + 128 (blk ^ (l/16 & 1));
+    // base [blk & 1] holds the lane's part of the swap.
+    // ds_read_b128 serves a wave in passes that pair 8-lane groups whose lane/16 differ in bit 0;
+    // the fp8 fragment reads chunks 2q and 2q+1 (q = lane/16) in the order kh ^ (q & 1), so that
+    // the chunks of such a pair differ in bit 0 as well and take different banks. The lane's K
+    // order is then permuted the same way in x and w, which leaves the dot product unchanged.
     const int fr_row = lane & 15, fr_q = lane >> 4;
     int frag_a[2], frag_b[2];
     sfor<0, 2>([&](auto kh) {
-        // fp8: the 32 bytes of a lane are chunks 2q and 2q+1 (op kh = which one)
-        const int off = fr_row * kRowBytes + (((F8 ? 2 * fr_q + kh : kh * 4 + fr_q) ^ (fr_row & 7)) * 16);
-        const int mn  = (lane >> 4) * 4096 + (lane & 15) * 8;
+        const int off = fr_row * kRowBytes +
+                        (((F8 ? 2 * fr_q + (kh ^ (fr_q & 1)) : kh * 4 + fr_q) ^ (fr_row & 7)) * 16);
+        const int mn  = (lane >> 4) * 4096 + (lane & 15) * 8 + (kh ? -128 : 128) * (fr_q & 1);
         frag_a[kh]    = A_MN ? wm * 1024 + mn : wm * 128 * kRowBytes + off;
         frag_b[kh]    = B_MN ? wn * 1024 + mn : wn * 128 * kRowBytes + off;
     });
@@ -563,7 +571,7 @@ grouped_gemm_kernel(const KernelArgs args) {
             f[R] = lds_read(rd[R] + blk * 16 * kRowBytes);
         } else {
             constexpr int kh = R >> 1, half = R & 1;
-            const u32x2   v  = lds_read_tr(rd[0] + kh * 16384 + half * 2048 + blk * 128);
+            const u32x2   v  = lds_read_tr(rd[blk & 1] + kh * 16384 + half * 2048 + blk * 128);
             f[kh][2 * half]     = static_cast<int>(v[0]);
             f[kh][2 * half + 1] = static_cast<int>(v[1]);
         }
@@ -670,7 +678,7 @@ grouped_gemm_kernel(const KernelArgs args) {
     // partial last step's chunks past K get the out-of-range offset.
     struct DmaSrc {
         i32x4 rs;
-        int   so, vadd, mask;
+        int   so, vadd, mask, mask1; // MN-major: mask for even / odd DMA j (column-block swap)
     };
     auto dma_src = [&](auto b_op, int kidx, auto checked) -> DmaSrc {
         constexpr bool B  = decltype(b_op)::value;
@@ -694,7 +702,8 @@ grouped_gemm_kernel(const KernelArgs args) {
             if constexpr (MN) {
                 d.so   = 0;
                 d.vadd = kabs * kTileK * ld * 2;
-                d.mask = (in_cur ? oc : on) + mn_col >= ld ? bad_off : 0;
+                d.mask  = (in_cur ? oc : on) + mn_col(0) >= ld ? bad_off : 0;
+                d.mask1 = (in_cur ? oc : on) + mn_col(1) >= ld ? bad_off : 0;
             } else {
                 d.so   = kabs * kRowBytes;
                 d.vadd = 0;
@@ -705,7 +714,8 @@ grouped_gemm_kernel(const KernelArgs args) {
             if constexpr (MN) {
                 d.so   = 0;
                 d.vadd = (kidx + cur.k0) * kTileK * ld * 2;
-                d.mask = oc + mn_col >= ld ? bad_off : 0;
+                d.mask  = oc + mn_col(0) >= ld ? bad_off : 0;
+                d.mask1 = oc + mn_col(1) >= ld ? bad_off : 0;
             } else {
                 d.so   = (kidx + cur.k0) * kRowBytes;
                 d.vadd = 0;
@@ -720,7 +730,7 @@ grouped_gemm_kernel(const KernelArgs args) {
         constexpr bool MN = B ? B_MN : A_MN;
         const int      vo = voff[(B && !kSameOff) ? 1 : 0][j];
         if constexpr (MN)
-            return (vo + d.vadd) | d.mask;
+            return (vo + d.vadd) | (j & 1 ? d.mask1 : d.mask);
         else if constexpr (decltype(checked)::value)
             return vo | d.mask;
         else
