@@ -56,6 +56,14 @@ C_API = {
     "gg_prepare_wgrad": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_int64,
                                         ctypes.POINTER(ctypes.c_int64), ctypes.c_void_p, ctypes.c_void_p,
                                         ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)]),
+    "gg_prepare_dgrad_fp8": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int64,
+                                            ctypes.c_int64, ctypes.POINTER(ctypes.c_int64), ctypes.c_void_p,
+                                            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                            ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)]),
+    "gg_prepare_wgrad_fp8": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int64,
+                                            ctypes.c_int64, ctypes.POINTER(ctypes.c_int64), ctypes.c_void_p,
+                                            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                            ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -229,17 +237,27 @@ class BackwardPlan:
     kind "dgrad": out [sum(M), k] = grad_out [sum(M), n] @ w[g] [n, k] per group.
     kind "wgrad": out [B, n, k] = grad_out[g]^T [n, M_g] @ x[g] [M_g, k], zero for empty groups.
     Buffers are device addresses; prepare raises GGError (status 1 = not supported).
+    fp8 (gg_prepare_dgrad_fp8 / gg_prepare_wgrad_fp8): dtype is grad_out's fp8 type, other_dtype
+    the other operand's (default: the same), grad_scale [1] and other_scale [B] device float32
+    addresses; out is bf16, scaled by grad_scale[0] * other_scale[g].
     """
 
     def __init__(self, kind: str, dtype: DType, n: int, k: int, group_m: Sequence[int], grad_out: int,
-                 other: int, out: int, stream: int = 0) -> None:
+                 other: int, out: int, stream: int = 0, other_dtype: Optional[DType] = None,
+                 grad_scale: int = 0, other_scale: int = 0) -> None:
         if kind not in ("dgrad", "wgrad"):
             raise ValueError("kind must be 'dgrad' or 'wgrad'")
         self._lib = load_library()
         self._plan = ctypes.c_void_p()
         gm = (ctypes.c_int64 * max(1, len(group_m)))(*group_m)
-        fn = self._lib.gg_prepare_dgrad if kind == "dgrad" else self._lib.gg_prepare_wgrad
-        _check(fn(int(dtype), len(group_m), n, k, gm, grad_out, other, out, stream, ctypes.byref(self._plan)))
+        if int(dtype) in (int(DType.FP8_E4M3), int(DType.FP8_E5M2)):
+            od = dtype if other_dtype is None else other_dtype
+            fn = self._lib.gg_prepare_dgrad_fp8 if kind == "dgrad" else self._lib.gg_prepare_wgrad_fp8
+            _check(fn(int(dtype), int(od), len(group_m), n, k, gm, grad_out, other, grad_scale, other_scale, out,
+                      stream, ctypes.byref(self._plan)))
+        else:
+            fn = self._lib.gg_prepare_dgrad if kind == "dgrad" else self._lib.gg_prepare_wgrad
+            _check(fn(int(dtype), len(group_m), n, k, gm, grad_out, other, out, stream, ctypes.byref(self._plan)))
         self.kind = kind
         self.flop = 2.0 * float(sum(group_m)) * float(n) * float(k)
 
@@ -368,6 +386,57 @@ def _backward(kind: str, grad_out, other, group_m: Sequence[int], out, stream: O
     finally:
         plan.release()
     return out
+
+
+def _backward_fp8(kind: str, grad_out, other, group_m: Sequence[int], grad_scale, other_scale, out, stream):
+    import torch
+
+    kinds = {torch.float8_e4m3fn: DType.FP8_E4M3, torch.float8_e5m2: DType.FP8_E5M2}
+    if grad_out.dtype not in kinds or other.dtype not in kinds:
+        raise TypeError("operands must be float8_e4m3fn or float8_e5m2")
+    if not (grad_out.is_cuda and other.is_cuda and grad_out.is_contiguous() and other.is_contiguous()):
+        raise ValueError("operands must be contiguous device tensors")
+    if not (grad_scale.dtype == other_scale.dtype == torch.float32 and grad_scale.is_cuda and other_scale.is_cuda):
+        raise TypeError("scales must be float32 device tensors")
+    n = grad_out.shape[1]
+    if grad_out.shape[0] != sum(group_m) or other_scale.numel() != len(group_m):
+        raise ValueError("grad_out must have sum(group_m) rows and other_scale one value per group")
+    if kind == "dgrad":
+        if other.shape[0] != len(group_m) or other.shape[1] != n:
+            raise ValueError("w must be [B, N, K] with N = grad_out's columns")
+        k = other.shape[2]
+        shape = (grad_out.shape[0], k)
+    else:
+        if other.shape[0] != grad_out.shape[0]:
+            raise ValueError("x must have the rows of grad_out")
+        k = other.shape[1]
+        shape = (len(group_m), n, k)
+    if out is None:
+        out = torch.empty(shape, dtype=torch.bfloat16, device=grad_out.device)
+    s = torch.cuda.current_stream(grad_out.device).cuda_stream if stream is None else stream
+    plan = BackwardPlan(kind, kinds[grad_out.dtype], n, k, list(group_m), grad_out.data_ptr(), other.data_ptr(),
+                        out.data_ptr(), s, other_dtype=kinds[other.dtype], grad_scale=grad_scale.data_ptr(),
+                        other_scale=other_scale.data_ptr())
+    try:
+        plan.run(s)
+        torch.cuda.current_stream(grad_out.device).synchronize()
+    finally:
+        plan.release()
+    return out
+
+
+def grouped_gemm_dgrad_fp8(grad_out, w, group_m: Sequence[int], grad_scale, w_scale, out=None,
+                           stream: Optional[int] = None):
+    """bf16 grad_x = (grad_out [sum(M), N] @ w[g] [N, K]) * grad_scale * w_scale[g] for float8
+    tensors (gradient e4m3 or e5m2, w e4m3 or matching) and float32 device scales."""
+    return _backward_fp8("dgrad", grad_out, w, group_m, grad_scale, w_scale, out, stream)
+
+
+def grouped_gemm_wgrad_fp8(grad_out, x, group_m: Sequence[int], grad_scale, x_scale, out=None,
+                           stream: Optional[int] = None):
+    """bf16 grad_w [B, N, K] = (grad_out[g]^T @ x[g]) * grad_scale * x_scale[g] for float8 tensors,
+    zero for empty groups."""
+    return _backward_fp8("wgrad", grad_out, x, group_m, grad_scale, x_scale, out, stream)
 
 
 def grouped_gemm_dgrad(grad_out, w, group_m: Sequence[int], out=None, stream: Optional[int] = None):

@@ -272,15 +272,32 @@ int gg_prepare(int dtype, int group_num, int64_t n, int64_t k, const int64_t *gr
 // contraction K. dgrad: A = grad_out (K-major, row stride n), B^T = w[g] stored n x k,
 // N = k, K = n. wgrad: A^T = grad_out rows of the group (row stride n), B^T = x rows (row stride
 // k), out = grad_w[g] n x k, N = k, K = the group's rows.
-static int prepare_backward(int mode, int dtype, int group_num, int64_t n, int64_t k,
-                            const int64_t *group_m, const void *a, const void *b, void *out,
-                            void *stream, gg_plan **plan_out) {
+// dtype_a / dtype_b: formats of grad_out and of the other operand. 16-bit: both the same, no
+// scales. fp8: e4m3 x e4m3, e5m2 x e5m2 or e5m2 gradient x e4m3, bf16 out scaled by a_scale[0] *
+// b_scale[g].
+static int prepare_backward(int layout, int dtype_a, int dtype_b, int group_num, int64_t n, int64_t k,
+                            const int64_t *group_m, const void *a, const void *b, const float *a_scale,
+                            const float *b_scale, void *out, void *stream, gg_plan **plan_out) {
     g_last_error.clear();
     if (plan_out == nullptr)
         return fail(GG_ERR_INVALID, "plan_out is null");
     *plan_out = nullptr;
     if (group_num > 0 && group_m == nullptr)
         return fail(GG_ERR_INVALID, "group_m is null");
+    const bool f8     = dtype_a == GG_DTYPE_FP8_E4M3 || dtype_a == GG_DTYPE_FP8_E5M2;
+    int        format = gg::kIn16;
+    if (f8) {
+        if (dtype_a == GG_DTYPE_FP8_E4M3 && dtype_b == GG_DTYPE_FP8_E4M3)
+            format = gg::kInE4M3;
+        else if (dtype_a == GG_DTYPE_FP8_E5M2 && dtype_b == GG_DTYPE_FP8_E5M2)
+            format = gg::kInE5M2;
+        else if (dtype_a == GG_DTYPE_FP8_E5M2 && dtype_b == GG_DTYPE_FP8_E4M3)
+            format = gg::kInE5M2xE4M3;
+        else
+            return fail(GG_ERR_INVALID, "fp8 formats must be e4m3 x e4m3, e5m2 x e5m2 or e5m2 gradient x e4m3");
+    } else if ((dtype_a != GG_DTYPE_BF16 && dtype_a != GG_DTYPE_FP16) || dtype_b != dtype_a) {
+        return fail(GG_ERR_INVALID, "dtype must be GG_DTYPE_BF16 or GG_DTYPE_FP16");
+    }
     int64_t total_m = 0, max_m = 0;
     for (int g = 0; g < group_num; ++g) {
         if (group_m[g] < 0)
@@ -288,41 +305,46 @@ static int prepare_backward(int mode, int dtype, int group_num, int64_t n, int64
         total_m += group_m[g];
         max_m = std::max(max_m, group_m[g]);
     }
+    const bool dgrad = layout == gg::kDgrad;
     // Output rows: grad_x has total_m, grad_w has group_num * n.
-    const int64_t out_rows   = mode == 1 ? total_m : int64_t(group_num) * n;
+    const int64_t out_rows   = dgrad ? total_m : int64_t(group_num) * n;
     const bool    has_output = out_rows > 0 && k > 0;
     // Both operands are read when the contraction (n for dgrad, the rows for wgrad) is non-zero.
-    const bool reads = mode == 1 ? (total_m > 0 && n > 0) : (total_m > 0);
-    if (dtype != GG_DTYPE_BF16 && dtype != GG_DTYPE_FP16)
-        return fail(GG_ERR_INVALID, "dtype must be GG_DTYPE_BF16 or GG_DTYPE_FP16");
+    const bool reads = dgrad ? (total_m > 0 && n > 0) : (total_m > 0);
     if (group_num < 0 || n < 0 || k < 0)
         return fail(GG_ERR_INVALID, "group_num, n and k must be >= 0");
     if (has_output && (out == nullptr || (reads && (a == nullptr || b == nullptr))))
         return fail(GG_ERR_INVALID, "grad_out, the second operand and the output must be device pointers");
-    if (n % 8 != 0)
-        return fail(GG_ERR_UNSUPPORTED, "N must be a multiple of 8 (16-byte rows)");
-    if (k % 8 != 0)
-        return fail(GG_ERR_UNSUPPORTED, "K must be a multiple of 8 (16-byte rows)");
+    if (f8 && has_output && reads && (a_scale == nullptr || b_scale == nullptr))
+        return fail(GG_ERR_INVALID, "fp8 scales must be device pointers");
+    // 16-byte rows; fp8 transposed operands move 16-column blocks
+    const int64_t align = f8 ? 16 : 8;
+    if (n % align != 0)
+        return fail(GG_ERR_UNSUPPORTED, std::string("N must be a multiple of ") + std::to_string(align));
+    if (k % align != 0)
+        return fail(GG_ERR_UNSUPPORTED, std::string("K must be a multiple of ") + std::to_string(align));
     if (has_output && (!aligned16(out) || (reads && (!aligned16(a) || !aligned16(b)))))
         return fail(GG_ERR_UNSUPPORTED, "buffers must be 16-byte aligned");
     if (k > (int64_t(1) << 21) || n > (int64_t(1) << 21))
         return fail(GG_ERR_UNSUPPORTED, "N and K must be at most 2097152");
     // 32-bit byte offsets inside one group's transposed operand, including the rows a partial
-    // last K step addresses past the end (up to 64 more).
-    const int64_t lim = int64_t(1) << 31;
-    if (mode == 1 && (n + gg::kTileK) * k * 2 >= lim)
+    // last K step addresses past the end (up to one step more).
+    const int64_t lim   = int64_t(1) << 31;
+    const int64_t es    = f8 ? 1 : 2;
+    const int64_t steps = f8 ? 128 : gg::kTileK; // contraction rows per K step
+    if (dgrad && (n + steps) * k * es >= lim)
         return fail(GG_ERR_UNSUPPORTED, "one group's w must be smaller than 2 GiB");
-    if (mode == 2 && ((max_m + gg::kTileK) * n * 2 >= lim || (max_m + gg::kTileK) * k * 2 >= lim))
+    if (!dgrad && ((max_m + steps) * n * es >= lim || (max_m + steps) * k * es >= lim))
         return fail(GG_ERR_UNSUPPORTED, "one group's rows of grad_out and x must be smaller than 2 GiB");
 
     auto *plan = new (std::nothrow) gg_plan;
     if (plan == nullptr)
         return fail(GG_ERR_INVALID, "out of host memory");
-    plan->mode      = mode;
-    plan->dtype     = dtype;
+    plan->mode      = gg::make_mode(layout, format);
+    plan->dtype     = f8 ? GG_DTYPE_BF16 : dtype_a; // output
     plan->group_num = group_num;
     plan->n         = k;                      // output columns
-    plan->k         = mode == 1 ? n : 0;      // contraction (wgrad: per group)
+    plan->k         = dgrad ? n : 0;          // contraction (wgrad: per group)
     plan->total_m   = out_rows;               // rows zeroed when there is nothing to read
     plan->x         = a;
     plan->w         = b;
@@ -330,16 +352,20 @@ static int prepare_backward(int mode, int dtype, int group_num, int64_t n, int64
 
     const int64_t n_tiles = gg::cdiv(k, gg::kTileN);
     std::vector<gg::GroupEntry> table(static_cast<size_t>(group_num));
-    const int64_t tiles = gg::build_group_table(group_m, group_num, n_tiles, table.data(), mode == 2 ? n : 0);
+    const int64_t tiles = gg::build_group_table(group_m, group_num, n_tiles, table.data(), dgrad ? 0 : n);
     if (tiles < 0) {
         delete plan;
         return fail(GG_ERR_UNSUPPORTED, "too many rows or tiles for 32-bit tile indices");
     }
     // dgrad with n == 0: grad_x = 0 (gg_run zero-fills). wgrad with no rows: the tiles run and
     // store zeros (each group's K steps read nothing).
-    plan->total_tiles = has_output && (mode == 2 || n > 0) ? static_cast<int>(tiles) : 0;
+    plan->total_tiles = has_output && (!dgrad || n > 0) ? static_cast<int>(tiles) : 0;
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    const char *what = mode == 1 ? "dgrad" : "wgrad";
+    const std::string what = std::string(dgrad ? "dgrad" : "wgrad") +
+                             (format == gg::kIn16         ? ""
+                              : format == gg::kInE4M3     ? " fp8 e4m3"
+                              : format == gg::kInE5M2     ? " fp8 e5m2"
+                                                          : " fp8 e5m2 x e4m3");
     if (plan->total_tiles > 0) {
         hipDeviceProp_t prop;
         if (device_props(&prop) != GG_OK) {
@@ -365,21 +391,23 @@ static int prepare_backward(int mode, int dtype, int group_num, int64_t n, int64
         ka.d_total         = nullptr;
         ka.lda             = static_cast<int>(n);
         ka.ldb             = static_cast<int>(k);
-        ka.m_out           = mode == 2 ? static_cast<int>(n) : 0;
-        ka.k_tiles         = mode == 1 ? static_cast<int>(gg::cdiv(n, gg::kTileK)) : 1;
+        ka.m_out           = dgrad ? 0 : static_cast<int>(n);
+        ka.k_tiles         = dgrad ? static_cast<int>(gg::cdiv(n, steps)) : 1;
+        ka.x_scale         = f8 ? a_scale : nullptr;
+        ka.w_scale         = f8 ? b_scale : nullptr;
         // wgrad's K steps differ per group: no split
-        if (mode == 1 && setup_split_k(plan, prop) != GG_OK) {
+        if (dgrad && setup_split_k(plan, prop) != GG_OK) {
             free_plan(plan);
             return GG_ERR_HIP;
         }
-        plan->detail       = std::string("mi355x ") + what + " persistent 256x256x64 " +
-                       std::string(dtype == GG_DTYPE_BF16 ? "bf16" : "fp16") +
+        plan->detail = "mi355x " + what + " persistent 256x256x" + std::to_string(f8 ? 128 : 64) + " " +
+                       (f8 ? "bf16-out" : dtype_a == GG_DTYPE_BF16 ? "bf16" : "fp16") +
                        " grid=" + std::to_string(plan->grid) + " tiles=" + std::to_string(plan->total_tiles) +
                        " xcd=" + std::to_string(ka.n_xcd) +
-                       (gg::uses_cross_tile(ka, plan->grid, mode) ? " cross-tile" : " per-tile") +
+                       (gg::uses_cross_tile(ka, plan->grid, plan->mode) ? " cross-tile" : " per-tile") +
                        (ka.splits > 1 ? " split-k=" + std::to_string(ka.splits) : "");
     } else {
-        plan->detail = std::string("mi355x ") + what + ": no launch (" +
+        plan->detail = "mi355x " + what + ": no launch (" +
                        (has_output ? "empty contraction, zero fill" : "empty output") + ")";
         if (!has_output)
             plan->total_m = 0;
@@ -423,7 +451,7 @@ int gg_prepare_fp8(int dtype, int group_num, int64_t n, int64_t k, const int64_t
     auto *plan = new (std::nothrow) gg_plan;
     if (plan == nullptr)
         return fail(GG_ERR_INVALID, "out of host memory");
-    plan->mode      = dtype == GG_DTYPE_FP8_E4M3 ? 3 : 4;
+    plan->mode      = gg::make_mode(gg::kFwd, dtype == GG_DTYPE_FP8_E4M3 ? gg::kInE4M3 : gg::kInE5M2);
     plan->dtype     = GG_DTYPE_BF16; // output
     plan->group_num = group_num;
     plan->n         = n;
@@ -486,12 +514,36 @@ int gg_prepare_fp8(int dtype, int group_num, int64_t n, int64_t k, const int64_t
 
 int gg_prepare_dgrad(int dtype, int group_num, int64_t n, int64_t k, const int64_t *group_m,
                      const void *grad_out, const void *w, void *grad_x, void *stream, gg_plan **plan_out) {
-    return prepare_backward(1, dtype, group_num, n, k, group_m, grad_out, w, grad_x, stream, plan_out);
+    if (dtype != GG_DTYPE_BF16 && dtype != GG_DTYPE_FP16)
+        return fail(GG_ERR_INVALID, "dtype must be GG_DTYPE_BF16 or GG_DTYPE_FP16");
+    return prepare_backward(gg::kDgrad, dtype, dtype, group_num, n, k, group_m, grad_out, w, nullptr, nullptr,
+                            grad_x, stream, plan_out);
 }
 
 int gg_prepare_wgrad(int dtype, int group_num, int64_t n, int64_t k, const int64_t *group_m,
                      const void *grad_out, const void *x, void *grad_w, void *stream, gg_plan **plan_out) {
-    return prepare_backward(2, dtype, group_num, n, k, group_m, grad_out, x, grad_w, stream, plan_out);
+    if (dtype != GG_DTYPE_BF16 && dtype != GG_DTYPE_FP16)
+        return fail(GG_ERR_INVALID, "dtype must be GG_DTYPE_BF16 or GG_DTYPE_FP16");
+    return prepare_backward(gg::kWgrad, dtype, dtype, group_num, n, k, group_m, grad_out, x, nullptr, nullptr,
+                            grad_w, stream, plan_out);
+}
+
+int gg_prepare_dgrad_fp8(int grad_dtype, int w_dtype, int group_num, int64_t n, int64_t k,
+                         const int64_t *group_m, const void *grad_out, const void *w, const float *grad_scale,
+                         const float *w_scale, void *grad_x, void *stream, gg_plan **plan_out) {
+    if (grad_dtype != GG_DTYPE_FP8_E4M3 && grad_dtype != GG_DTYPE_FP8_E5M2)
+        return fail(GG_ERR_INVALID, "grad_dtype must be GG_DTYPE_FP8_E4M3 or GG_DTYPE_FP8_E5M2");
+    return prepare_backward(gg::kDgrad, grad_dtype, w_dtype, group_num, n, k, group_m, grad_out, w, grad_scale,
+                            w_scale, grad_x, stream, plan_out);
+}
+
+int gg_prepare_wgrad_fp8(int grad_dtype, int x_dtype, int group_num, int64_t n, int64_t k,
+                         const int64_t *group_m, const void *grad_out, const void *x, const float *grad_scale,
+                         const float *x_scale, void *grad_w, void *stream, gg_plan **plan_out) {
+    if (grad_dtype != GG_DTYPE_FP8_E4M3 && grad_dtype != GG_DTYPE_FP8_E5M2)
+        return fail(GG_ERR_INVALID, "grad_dtype must be GG_DTYPE_FP8_E4M3 or GG_DTYPE_FP8_E5M2");
+    return prepare_backward(gg::kWgrad, grad_dtype, x_dtype, group_num, n, k, group_m, grad_out, x, grad_scale,
+                            x_scale, grad_w, stream, plan_out);
 }
 
 int gg_prepare_device_lens(int dtype, int group_num, int64_t total_m, int64_t n, int64_t k,

@@ -9,12 +9,23 @@
 
 namespace gg {
 
+// Kernel modes: an operand layout plus an input format, mode = layout + 4 * format.
+enum Layout : int { kFwd = 0, kDgrad = 1, kWgrad = 2 };
+enum InFormat : int {
+    kIn16        = 0, // bf16 or fp16 inputs and output
+    kInE4M3      = 1, // fp8 e4m3 A and B, bf16 output
+    kInE5M2      = 2, // fp8 e5m2 A and B, bf16 output
+    kInE5M2xE4M3 = 3  // fp8 e5m2 A (the gradient), e4m3 B, bf16 output
+};
+constexpr int make_mode(int layout, int format) { return layout + 4 * format; }
+
 // Kernel arguments, passed by value in the kernarg segment. Everything a workgroup needs
 // to find its tiles: the device group table plus the problem-wide sizes.
 // Kernel terms: out (rows x N) = A (rows x K) B^T (N x K) per group, K the contraction.
 //   forward: A = x [sum(M), K], B = w [B, N, K], out [sum(M), N]
 //   dgrad:   A = grad_out [sum(M), K], B^T = w[g] [K, N] (stored K x N), out = grad_x [sum(M), N]
 //   wgrad:   A^T = grad_out [M_g, m_out], B^T = x [M_g, N], out = grad_w [B, m_out, N], K = M_g
+// fp8 formats: 1-byte inputs, bf16 out scaled by a_scale[0] * b_scale[g] (x_scale / w_scale).
 struct KernelArgs {
     const void       *x;      // A operand storage (x, or grad_out for dgrad / wgrad)
     const void       *w;      // B operand storage (w, or x for wgrad)
@@ -30,8 +41,8 @@ struct KernelArgs {
     int               band;        // M-tiles per band of the in-group tile order
     int               lda, ldb;    // row strides (elements) of the A and B storage
     int               m_out;       // wgrad: output rows per group (0 otherwise)
-    const float      *x_scale;     // fp8: device scale of x (1 value)
-    const float      *w_scale;     // fp8: device scale of each group's w (group_num values)
+    const float      *x_scale;     // fp8: device scale of the A operand (1 value)
+    const float      *w_scale;     // fp8: device scale of each group's B operand (group_num values)
     const int        *d_total;     // device tile count (device-resident group sizes), or null:
                                    // then total_tiles holds it
     int               splits;      // split-K: K ranges per tile (1 = none; per-tile variant only)
@@ -51,15 +62,15 @@ struct TableHeader {
 bool uses_cross_tile(const KernelArgs &args, int grid, int mode = 0);
 
 // Enqueue the persistent grouped GEMM: `grid` workgroups of 256 threads on `stream`.
-// fp16 selects the f16 MFMA, otherwise bf16; mode 0 forward, 1 dgrad, 2 wgrad, 3 / 4 forward
-// with fp8 e4m3 / e5m2 inputs (bf16 out, fp16 must be false).
+// fp16 selects the f16 MFMA, otherwise bf16 (16-bit formats); mode = make_mode(layout, format)
+// (fp8 formats write bf16, fp16 must be false).
 // Returns the launch status.
 hipError_t launch_grouped_gemm(const KernelArgs &args, bool fp16, int grid, hipStream_t stream,
                                int mode = 0);
 
 // Split-K second pass: out tile = sum over the splits of the partial sums in args.ws (in split
-// order), times the fp8 scale for modes 3 / 4, converted to 16 bits and stored within the tile's
-// valid rows and columns. Forward and dgrad layouts (out row stride N).
+// order), times the fp8 scales for fp8 formats, converted to 16 bits and stored within the
+// tile's valid rows and columns. Forward and dgrad layouts (out row stride N).
 hipError_t launch_split_reduce(const KernelArgs &args, bool fp16, hipStream_t stream, int mode = 0);
 
 // Build the group table on the device from device-resident group sizes: lens[group_num]

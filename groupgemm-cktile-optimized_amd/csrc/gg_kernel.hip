@@ -51,6 +51,7 @@
 namespace gg {
 namespace {
 
+typedef int      i32x2 __attribute__((ext_vector_type(2)));
 typedef int      i32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
@@ -120,18 +121,22 @@ constexpr int b_stage(int s) { return (kAStages + s) * kOpBytes; }
 // Operand layouts. K-major: the contraction index runs along each stored row (x and w of the
 // forward op, grad_out of dgrad); a 16-row fragment k-half is one ds_read_b128. MN-major: the
 // contraction index is the stored row index (w of dgrad, grad_out and x of wgrad); a fragment
-// k-half is two ds_read_b64_tr_b16, each giving 4 consecutive contraction values per lane.
+// k-half is two ds_read_b64_tr_b16, each giving 4 consecutive contraction values per lane
+// (fp8: a fragment is four ds_read_b64_tr_b8 of 8 values).
+// A kernel mode is a layout plus an input format: mode = layout + 4 * format (gg_kernel.h).
+//   layout kFwd:   out[g] = x[g] @ w[g]^T                     A = x (K-major),  B = w (K-major)
+//   layout kDgrad: grad_x[g] = grad_out[g] @ w[g]             A = grad_out (K), B = w (MN)
+//   layout kWgrad: grad_w[g] = grad_out[g]^T @ x[g], K = M_g  A = grad_out (MN), B = x (MN)
+//   format kIn16 (bf16 / fp16), kInE4M3, kInE5M2 (both operands), kInE5M2xE4M3 (A e5m2, B
+//   e4m3); fp8 formats write bf16 out = (A B^T) * a_scale * b_scale[g].
 // ---------------------------------------------------------------------------------------
-enum Mode : int {
-    kFwd   = 0, // out[g] = x[g] @ w[g]^T                       A = x (K-major),  B = w (K-major)
-    kDgrad = 1, // grad_x[g] = grad_out[g] @ w[g]               A = grad_out (K), B = w (MN)
-    kWgrad = 2, // grad_w[g] = grad_out[g]^T @ x[g], K = M_g    A = grad_out (MN), B = x (MN)
-    kFwdE4M3 = 3, // forward with fp8 e4m3 x and w, bf16 out = (x[g] @ w[g]^T) * sx * sw[g]
-    kFwdE5M2 = 4  // the same with fp8 e5m2
-};
-constexpr bool mode_f8(int m) { return m == kFwdE4M3 || m == kFwdE5M2; }
-constexpr bool mode_a_mn(int m) { return m == kWgrad; }
-constexpr bool mode_b_mn(int m) { return m == kDgrad || m == kWgrad; }
+constexpr int  mode_layout(int m) { return m & 3; }
+constexpr int  mode_fmt(int m) { return m >> 2; }
+constexpr bool mode_f8(int m) { return mode_fmt(m) != kIn16; }
+constexpr bool mode_a_e5(int m) { return mode_fmt(m) == kInE5M2 || mode_fmt(m) == kInE5M2xE4M3; }
+constexpr bool mode_b_e5(int m) { return mode_fmt(m) == kInE5M2; }
+constexpr bool mode_a_mn(int m) { return mode_layout(m) == kWgrad; }
+constexpr bool mode_b_mn(int m) { return mode_layout(m) == kDgrad || mode_layout(m) == kWgrad; }
 // LDS reads of one 16-row fragment over both k-halves.
 constexpr int reads_per_frag(bool mn) { return mn ? 4 : 2; }
 
@@ -239,19 +244,38 @@ template <int NA, int NB> struct Plan {
 static_assert(Plan<2, 2>::check() && Plan<2, 4>::check() && Plan<4, 4>::check(), "slot plans");
 
 // fp8 K step: 128 fp8 values per 128-byte row; v_mfma_f32_16x16x128_f8f6f4 takes 32 bytes of a
-// row per lane (two ds_read_b128, read op r = half), so a row mi of the step is 8 MFMAs of twice
-// the length. Reads after odd MFMAs, DMAs after even ones: A(kt+1) DMAs 1-7 in rows 0-2 (after
-// MFMAs 0 and 4) and row 3 (after MFMA 2), B(kt+3) in rows 3-6 (after 0 and 4), the barrier
-// after MFMA 5 of row 7, then row 0 of the next step's x (5, 7) and the early A DMA 0 (6).
-struct Plan8 {
-    static constexpr int slots = 8, early = 1, bar = 5;
-    static constexpr int read_a_next(int mi, int idx) { return (mi < 7 && (idx == 1 || idx == 3)) ? idx / 2 : -1; }
-    static constexpr int read_b_next(int mi, int idx) {
-        if (mi < 7)
-            return (idx == 5 || idx == 7) ? (idx - 5) / 2 : -1;
-        return (idx == 1 || idx == 3) ? idx / 2 : -1;
+// row per lane, so a row mi of the step is 8 MFMAs of twice the length, and a fragment is two
+// ds_read_b128 (K-major) or four ds_read_b64_tr_b8 (MN-major): NA / NB reads.
+// DMAs after MFMAs 0 and 4: A(kt+1) DMAs 1-7 in rows 0-2 and row 3 (after MFMA 2), B(kt+3) in
+// rows 3-6; the early A DMA 0 after MFMA 6 of row 7. The x reads of row mi+1 follow the odd
+// MFMAs of row mi, the w reads of step kt+1 the MFMAs left (rows 0-6) or the first MFMAs of
+// row 7, before the barrier (after MFMA 5, or 4 when row 0 of x takes four reads), and row 0 of
+// the next step's x follows the barrier. A 32-cycle fp8 MFMA leaves room for a DMA or a store
+// beside a read in one gap.
+template <int NA, int NB> struct Plan8 {
+    static_assert((NA == 2 || NA == 4) && (NB == 2 || NB == 4), "reads per fragment");
+    static constexpr int slots = 8, early = 1, bar = NA == 4 ? 4 : 5;
+    static constexpr int read_a_next(int mi, int idx) {
+        return (mi < 7 && idx % 2 == 1 && idx < 2 * NA) ? idx / 2 : -1;
     }
-    static constexpr int read_a_row0(int mi, int idx) { return (mi == 7 && (idx == 5 || idx == 7)) ? (idx - 5) / 2 : -1; }
+    static constexpr int read_b_next(int mi, int idx) {
+        if (mi == 7)
+            return NB == 2 ? ((idx == 1 || idx == 3) ? idx / 2 : -1) : (idx < 4 ? idx : -1);
+        if (NA == 2 && NB == 2)
+            return (idx == 5 || idx == 7) ? (idx - 5) / 2 : -1;
+        if (NA == 2)
+            return idx == 2 ? 0 : idx == 5 ? 1 : idx == 6 ? 2 : idx == 7 ? 3 : -1;
+        if (NB == 2)
+            return (idx == 2 || idx == 6) ? idx / 4 : -1;
+        return idx % 2 == 0 ? idx / 2 : -1;
+    }
+    static constexpr int read_a_row0(int mi, int idx) {
+        if (mi != 7)
+            return -1;
+        if (NA == 2)
+            return (idx == 5 || idx == 7) ? (idx - 5) / 2 : -1;
+        return idx >= 4 ? idx - 4 : -1;
+    }
     static constexpr int load_a(int mi, int idx) {
         if (mi < 3 && (idx == 0 || idx == 4))
             return 1 + 2 * mi + idx / 4;
@@ -262,7 +286,7 @@ struct Plan8 {
     }
     static constexpr int load_a_early(int mi, int idx) { return (mi == 7 && idx == 6) ? 0 : -1; }
     // Cross-tile first step: store s of the previous tile's row block mi+1 after MFMA 2, 3, 6, 7
-    // of row mi (a 32-cycle fp8 MFMA leaves room for a store next to a read).
+    // of row mi.
     static constexpr int epi(int mi, int idx) {
         return mi < 7 ? (idx == 2 ? 0 : idx == 3 ? 1 : idx == 6 ? 2 : idx == 7 ? 3 : -1) : -1;
     }
@@ -283,22 +307,28 @@ struct Plan8 {
         return n;
     }
     static constexpr bool check() {
-        int na = 0, nb = 0, ne = 0, rb = 0;
+        int na = 0, nb = 0, ne = 0, ra = 0, rb = 0, r0 = 0;
         for (int p = 0; p < 8 * slots; ++p) {
             const int mi = p / slots, idx = p % slots;
-            const int ops = (load_a(mi, idx) >= 0) + (load_b(mi, idx) >= 0) + (load_a_early(mi, idx) >= 0) +
-                            (read_a_next(mi, idx) >= 0) + (read_b_next(mi, idx) >= 0) + (read_a_row0(mi, idx) >= 0);
-            if (ops > 1)
+            const int dmas  = (load_a(mi, idx) >= 0) + (load_b(mi, idx) >= 0) + (load_a_early(mi, idx) >= 0);
+            const int reads = (read_a_next(mi, idx) >= 0) + (read_b_next(mi, idx) >= 0) + (read_a_row0(mi, idx) >= 0);
+            if (dmas > 1 || reads > 1)
+                return false;
+            // w reads of row 7 before the barrier (reads at its slot follow it), row 0 of x after it
+            if (mi == 7 && ((read_b_next(mi, idx) >= 0 && idx >= bar) || (read_a_row0(mi, idx) >= 0 && idx < bar)))
                 return false;
             na += load_a(mi, idx) >= 0;
             nb += load_b(mi, idx) >= 0;
             ne += load_a_early(mi, idx) >= 0;
+            ra += read_a_next(mi, idx) >= 0;
             rb += read_b_next(mi, idx) >= 0;
+            r0 += read_a_row0(mi, idx) >= 0;
         }
-        return na == kLoads - early && nb == kLoads && ne == early && rb == 16;
+        return na == kLoads - early && nb == kLoads && ne == early && ra == 7 * NA && rb == 8 * NB && r0 == NA;
     }
 };
-static_assert(Plan8::check(), "fp8 slot plan");
+static_assert(Plan8<2, 2>::check() && Plan8<2, 4>::check() && Plan8<4, 4>::check(), "fp8 slot plans");
+static_assert(Plan8<2, 2>::vm_at_barrier() == 7, "fp8 forward plan unchanged");
 static_assert(Plan<2, 2>::bar == GG_BAR_IDX, "forward plan keeps the tuned barrier slot");
 
 // ---------------------------------------------------------------------------------------
@@ -339,15 +369,31 @@ __device__ __forceinline__ i32x4 dma_rsrc(const void *p, uint32_t bytes) {
 template <int OFF> __device__ __forceinline__ void set_m0(uint32_t lds_base) {
     asm volatile("s_add_u32 m0, %0, %1" : : "s"(lds_base), "n"(OFF) : "memory", "scc");
 }
+// A VMEM instruction that reads an SGPR written by a VALU instruction (v_readlane_b32 of a
+// spilled SGPR, v_readfirstlane_b32, v_cmp) needs 5 wait states in between. The compiler's
+// hazard recognizer does not look inside inline asm, and under SGPR pressure it reloads a DMA's
+// soffset with v_readlane_b32 right before it (seen in the fp8 dgrad kernel's first cross-tile
+// step: the DMA then used the stale soffset and loaded the wrong K step). The DMAs of the cold
+// paths (prologue, a tile's first step, where the spilled values are reloaded) start with 5
+// wait states (NOPS = 4); those of the K loop carry none, which costs 4-5 % of throughput, and
+// the build checks the generated code for the hazard instead (csrc/check_vmem_sgpr_hazard.py).
+template <int NOPS>
 __device__ __forceinline__ void dma16_m0(int voff, const i32x4 &rsrc, int soff) {
-    asm volatile("buffer_load_dwordx4 %0, %1, %2 offen " GG_DMA_CPOL " lds"
-                 :
-                 : "v"(voff), "s"(rsrc), "s"(soff)
-                 : "memory");
+    if constexpr (NOPS > 0)
+        asm volatile("s_nop %3\n\t"
+                     "buffer_load_dwordx4 %0, %1, %2 offen " GG_DMA_CPOL " lds"
+                     :
+                     : "v"(voff), "s"(rsrc), "s"(soff), "n"(NOPS)
+                     : "memory");
+    else
+        asm volatile("buffer_load_dwordx4 %0, %1, %2 offen " GG_DMA_CPOL " lds"
+                     :
+                     : "v"(voff), "s"(rsrc), "s"(soff)
+                     : "memory");
 }
 __device__ __forceinline__ void dma16(uint32_t lds_dst, int voff, const i32x4 &rsrc, int soff) {
     asm volatile("s_mov_b32 m0, %0\n\t"
-                 "s_nop 0\n\t"
+                 "s_nop 4\n\t"
                  "buffer_load_dwordx4 %1, %2, %3 offen " GG_DMA_CPOL " lds"
                  :
                  : "s"(lds_dst), "v"(voff), "s"(rsrc), "s"(soff)
@@ -374,19 +420,27 @@ __device__ __forceinline__ void mfma_first(f32x4 &c, const i32x4 &a, const i32x4
         asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=a"(c) : "v"(a), "v"(b));
 }
 
-// fp8 x fp8 -> fp32, 16 x 16 x 128 (gfx950): A and B are 32 bytes of a row per lane.
+// fp8 x fp8 -> fp32, 16 x 16 x 128 (gfx950): both sources are 32 bytes of a row per lane.
+// The kernel passes w (B) as src0 and x (A) as src1: cbsz gives src0's format, blgp src1's
+// (0 e4m3, 1 e5m2).
 typedef int i32x8 __attribute__((ext_vector_type(8)));
-template <bool E5M2> __device__ __forceinline__ void mfma8(f32x4 &c, const i32x8 &a, const i32x8 &b) {
-    if constexpr (E5M2)
-        asm volatile("v_mfma_f32_16x16x128_f8f6f4 %0, %1, %2, %0 cbsz:1 blgp:1" : "+a"(c) : "v"(a), "v"(b));
-    else
-        asm volatile("v_mfma_f32_16x16x128_f8f6f4 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
-}
-template <bool E5M2> __device__ __forceinline__ void mfma8_first(f32x4 &c, const i32x8 &a, const i32x8 &b) {
-    if constexpr (E5M2)
-        asm volatile("v_mfma_f32_16x16x128_f8f6f4 %0, %1, %2, 0 cbsz:1 blgp:1" : "=a"(c) : "v"(a), "v"(b));
-    else
-        asm volatile("v_mfma_f32_16x16x128_f8f6f4 %0, %1, %2, 0" : "=a"(c) : "v"(a), "v"(b));
+template <bool BE5, bool AE5, bool FIRST>
+__device__ __forceinline__ void mfma8(f32x4 &c, const i32x8 &b, const i32x8 &a) {
+#define GG_MFMA8(MODS)                                                                                    \
+    if constexpr (FIRST)                                                                                  \
+        asm volatile("v_mfma_f32_16x16x128_f8f6f4 %0, %1, %2, 0" MODS : "=a"(c) : "v"(b), "v"(a));       \
+    else                                                                                                  \
+        asm volatile("v_mfma_f32_16x16x128_f8f6f4 %0, %1, %2, %0" MODS : "+a"(c) : "v"(b), "v"(a));
+    if constexpr (BE5 && AE5) {
+        GG_MFMA8(" cbsz:1 blgp:1")
+    } else if constexpr (BE5) {
+        GG_MFMA8(" cbsz:1")
+    } else if constexpr (AE5) {
+        GG_MFMA8(" blgp:1")
+    } else {
+        GG_MFMA8("")
+    }
+#undef GG_MFMA8
 }
 
 // Four fp32 accumulators -> four 16-bit outputs (RNE), as two packed dwords.
@@ -430,18 +484,20 @@ constexpr int plan_epi(int mi, int idx) {
     return (mi < 7 && idx % 4 == 2) ? (idx - 2) / 4 : -1;
 }
 
-// MODE: forward, dgrad or wgrad (operand layouts and tile mapping, see Mode and KernelArgs).
+// MODE: layout (forward, dgrad, wgrad: operand layouts and tile mapping) and input format.
 // CROSS: cross-tile pipeline (needs k_tiles >= kCrossMinSteps); otherwise every tile starts
 // with a prologue and ends with the LDS-staged epilogue.
 template <bool F16, bool CROSS, int MODE>
 __global__ void __launch_bounds__(kThreads, 1) __attribute__((amdgpu_waves_per_eu(1, 1)))
 grouped_gemm_kernel(const KernelArgs args) {
-    constexpr bool A_MN = mode_a_mn(MODE), B_MN = mode_b_mn(MODE);
-    constexpr bool F8   = mode_f8(MODE);
-    constexpr int  ES   = F8 ? 1 : 2;        // input bytes per element
-    constexpr int  KS   = kRowBytes / ES;    // contraction values per K step
-    using P = std::conditional_t<F8, Plan8, Plan<reads_per_frag(A_MN), reads_per_frag(B_MN)>>;
-    static_assert(!(CROSS && MODE == kWgrad), "wgrad has a K-step count per group");
+    constexpr bool A_MN   = mode_a_mn(MODE), B_MN = mode_b_mn(MODE);
+    constexpr bool F8     = mode_f8(MODE);
+    constexpr int  LAYOUT = mode_layout(MODE);
+    constexpr int  ES     = F8 ? 1 : 2;        // input bytes per element
+    constexpr int  KS     = kRowBytes / ES;    // contraction values per K step
+    using P = std::conditional_t<F8, Plan8<reads_per_frag(A_MN), reads_per_frag(B_MN)>,
+                                 Plan<reads_per_frag(A_MN), reads_per_frag(B_MN)>>;
+    static_assert(!(CROSS && LAYOUT == kWgrad), "wgrad has a K-step count per group");
     static_assert(!(F8 && F16), "fp8 writes bf16");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kLdsBytes];
     typedef __attribute__((address_space(3))) uint8_t lds_u8;
@@ -472,16 +528,28 @@ grouped_gemm_kernel(const KernelArgs args) {
     // (lane%8)/2, 8 columns at 8 (lane%2). The column-block swap in every other pair of row
     // blocks puts the blocks that lanes 0-15 and 16-31 of one transposed read take (row blocks
     // rb and rb + 2) in different halves of the 256-byte bank window.
+    // fp8 MN-major: blocks of 8 rows x 16 columns (one 16-byte row per lane); LDS row block p
+    // holds stored row block p ^ (2 ((p / 4) & 1)) with column blocks swapped when (p / 4) is odd:
+    // DMA j (rows of LDS block 2j + wave/2) reads stored row block 2 (j ^ s) + wave/2, column
+    // block (8 (wave%2) + lane/8) ^ s, s = (j / 2) & 1, row lane%8 of the block. The row block
+    // swap gives each lane the K order of a K-major fp8 fragment (halves swapped for odd lane/16,
+    // see below); the column swap separates the blocks of lanes 0-15 and 16-31 in the banks.
     const int ld_row   = lane >> 3;
     const int ld_chunk = (lane & 7) ^ ld_row;
     const int mn_c     = (wave & 1) * 8 + (lane >> 3);
-    auto      mn_col   = [&](int jpar) { return (mn_c ^ jpar) * 16 + (lane & 1) * 8; };
-    auto      dma_off  = [&](bool mn, int j, int ld) {
-        return mn ? ((4 * (2 * j + (wave >> 1)) + ((lane & 7) >> 1)) * ld + mn_col(j & 1)) * 2
-                  : (j * 32 + wave * 8 + ld_row) * ld * ES + ld_chunk * 16;
+    // column of the lane in a transposed DMA (elements), with column-block swap sw
+    auto mn_col = [&](int sw) { return (mn_c ^ sw) * 16 + (F8 ? 0 : (lane & 1) * 8); };
+    // the column-block swap of transposed DMA j
+    auto mn_swz = [](int j) { return F8 ? (j >> 1) & 1 : j & 1; };
+    auto dma_off = [&](bool mn, int j, int ld) {
+        if (!mn)
+            return (j * 32 + wave * 8 + ld_row) * ld * ES + ld_chunk * 16;
+        if (F8)
+            return (8 * (2 * (j ^ mn_swz(j)) + (wave >> 1)) + (lane & 7)) * ld + mn_col(mn_swz(j));
+        return ((4 * (2 * j + (wave >> 1)) + ((lane & 7) >> 1)) * ld + mn_col(mn_swz(j))) * 2;
     };
     // voff[0]: A's offsets; voff[1]: B's (the forward op shares A's: both row strides are K).
-    constexpr bool kSameOff = MODE == kFwd;
+    constexpr bool kSameOff = LAYOUT == kFwd;
     int            voff[kSameOff ? 1 : 2][kLoads];
     sfor<0, kLoads>([&](auto j) {
         voff[0][j] = dma_off(A_MN, j, args.lda);
@@ -502,12 +570,16 @@ grouped_gemm_kernel(const KernelArgs args) {
     // the fp8 fragment reads chunks 2q and 2q+1 (q = lane/16) in the order kh ^ (q & 1), so that
     // the chunks of such a pair differ in bit 0 as well and take different banks. The lane's K
     // order is then permuted the same way in x and w, which leaves the dot product unchanged.
+    // fp8 MN-major: ds_read_b64_tr_b8 gives lane i of each 16-lane group column i of 8 rows when
+    // source lane s points at row s/2, column 8 (s%2): read t (0-3) of lane l takes LDS row block
+    // 4 (l/16) + t, i.e. base + 8192 (l/16) + 2048 t + 128 (blk ^ (l/16 & 1)), which holds the
+    // lane's K values in the K-major fragment's order.
     const int fr_row = lane & 15, fr_q = lane >> 4;
     int frag_a[2], frag_b[2];
     sfor<0, 2>([&](auto kh) {
         const int off = fr_row * kRowBytes +
                         (((F8 ? 2 * fr_q + (kh ^ (fr_q & 1)) : kh * 4 + fr_q) ^ (fr_row & 7)) * 16);
-        const int mn  = (lane >> 4) * 4096 + (lane & 15) * 8 + (kh ? -128 : 128) * (fr_q & 1);
+        const int mn  = (lane >> 4) * (F8 ? 8192 : 4096) + (lane & 15) * 8 + (kh ? -128 : 128) * (fr_q & 1);
         frag_a[kh]    = A_MN ? wm * 1024 + mn : wm * 128 * kRowBytes + off;
         frag_b[kh]    = B_MN ? wn * 1024 + mn : wn * 128 * kRowBytes + off;
     });
@@ -561,8 +633,12 @@ grouped_gemm_kernel(const KernelArgs args) {
     auto lds_read = [&](int off) -> i32x4 { return *reinterpret_cast<const i32x4 *>(smem + off); };
     typedef short i16x4 __attribute__((ext_vector_type(4)));
     typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+    typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
     auto lds_read_tr = [&](int off) -> u32x2 {
-        return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(smem + off)));
+        if constexpr (F8)
+            return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2 *)(smem + off)));
+        else
+            return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(smem + off)));
     };
     // LDS read op r (Plan numbering) of the fragment of 16-row block blk into f (per k-half),
     // from the logical stage whose read bases are rd.
@@ -571,7 +647,7 @@ grouped_gemm_kernel(const KernelArgs args) {
             f[R] = lds_read(rd[R] + blk * 16 * kRowBytes);
         } else {
             constexpr int kh = R >> 1, half = R & 1;
-            const u32x2   v  = lds_read_tr(rd[blk & 1] + kh * 16384 + half * 2048 + blk * 128);
+            const u32x2   v  = lds_read_tr(rd[blk & 1] + kh * (F8 ? 4096 : 16384) + half * 2048 + blk * 128);
             f[kh][2 * half]     = static_cast<int>(v[0]);
             f[kh][2 * half + 1] = static_cast<int>(v[1]);
         }
@@ -600,12 +676,10 @@ grouped_gemm_kernel(const KernelArgs args) {
         const int L     = splits > 1 ? t - split * total_tiles : xcd_remap(t, total_tiles, gridDim.x, args.n_xcd);
         int       tm, tn;
         locate_tile(L, args.groups, args.group_num, args.n_tiles, args.band, &g, &tm, &tn,
-                    MODE == kWgrad ? args.m_out : 0);
+                    LAYOUT == kWgrad ? args.m_out : 0);
         const GroupEntry ge = args.groups[g];
-        const uint16_t  *xa = static_cast<const uint16_t *>(args.x);
-        const uint16_t  *wb = static_cast<const uint16_t *>(args.w);
-        const uint8_t   *x8 = static_cast<const uint8_t *>(args.x);
-        const uint8_t   *w8 = static_cast<const uint8_t *>(args.w);
+        const uint8_t   *xa = static_cast<const uint8_t *>(args.x); // A storage (bytes)
+        const uint8_t   *wb = static_cast<const uint8_t *>(args.w); // B storage (bytes)
         Tile             tl;
         tl.n_valid         = min(kTileN, N - tn * kTileN);
         const int64_t col0 = static_cast<int64_t>(tn) * kTileN;
@@ -616,41 +690,38 @@ grouped_gemm_kernel(const KernelArgs args) {
         tl.k0    = k0;
         tl.klast = k1 == args.k_tiles;
         tl.scale = 1.0f;
-        if constexpr (MODE == kWgrad) {
+        if constexpr (LAYOUT == kWgrad) {
             // A^T = grad_out rows of the group, columns tm*256..; B^T = x rows, columns tn*256..
             const int64_t o0a = static_cast<int64_t>(tm) * kTileM;
-            const int64_t ma  = static_cast<int64_t>(ge.m) * args.lda - o0a;
+            const int64_t ma  = static_cast<int64_t>(ge.m) * args.lda - o0a; // elements
             const int64_t mb  = static_cast<int64_t>(ge.m) * args.ldb - col0;
             tl.m_valid = min(kTileM, args.m_out - tm * kTileM);
-            tl.rsrc_a  = dma_rsrc(xa + ge.row0 * args.lda + o0a, static_cast<uint32_t>(ma > 0 ? ma * 2 : 0));
-            tl.rsrc_b  = dma_rsrc(wb + ge.row0 * args.ldb + col0, static_cast<uint32_t>(mb > 0 ? mb * 2 : 0));
+            tl.rsrc_a  = dma_rsrc(xa + (ge.row0 * args.lda + o0a) * ES, static_cast<uint32_t>(ma > 0 ? ma * ES : 0));
+            tl.rsrc_b  = dma_rsrc(wb + (ge.row0 * args.ldb + col0) * ES, static_cast<uint32_t>(mb > 0 ? mb * ES : 0));
             tl.o0a     = static_cast<int>(o0a);
             tl.o0b     = static_cast<int>(col0);
             tl.c_ptr   = static_cast<uint16_t *>(args.out) +
                        (static_cast<int64_t>(g) * args.m_out + o0a) * N + col0;
-            tl.T     = max(1, static_cast<int>(cdiv(ge.m, kTileK)));
+            tl.T     = max(1, static_cast<int>(cdiv(ge.m, KS)));
             tl.k0    = 0;
             tl.klast = 1;
         } else {
             tl.m_valid         = min(kTileM, ge.m - tm * kTileM);
             const int64_t row0 = ge.row0 + static_cast<int64_t>(tm) * kTileM;
-            tl.rsrc_a = dma_rsrc(xa + row0 * args.lda, static_cast<uint32_t>(tl.m_valid) * args.lda * 2);
-            if constexpr (F8) {
-                tl.rsrc_a = dma_rsrc(x8 + row0 * args.lda, static_cast<uint32_t>(tl.m_valid) * args.lda);
-                tl.rsrc_b = dma_rsrc(w8 + (static_cast<int64_t>(g) * N + col0) * args.ldb,
-                                     static_cast<uint32_t>(tl.n_valid) * args.ldb);
-                tl.scale = args.x_scale[0] * args.w_scale[g];
-            } else if constexpr (MODE == kFwd) {
-                tl.rsrc_b = dma_rsrc(wb + (static_cast<int64_t>(g) * N + col0) * args.ldb,
-                                     static_cast<uint32_t>(tl.n_valid) * args.ldb * 2);
+            tl.rsrc_a = dma_rsrc(xa + row0 * args.lda * ES, static_cast<uint32_t>(tl.m_valid) * args.lda * ES);
+            if constexpr (LAYOUT == kFwd) {
+                tl.rsrc_b = dma_rsrc(wb + (static_cast<int64_t>(g) * N + col0) * args.ldb * ES,
+                                     static_cast<uint32_t>(tl.n_valid) * args.ldb * ES);
             } else {
                 // w[g] stored K x N: columns col0.. of all K rows (the end of w[g] bounds it)
                 const int64_t per_g = static_cast<int64_t>(K) * args.ldb;
-                tl.rsrc_b = dma_rsrc(wb + g * per_g + col0, static_cast<uint32_t>((per_g - col0) * 2));
+                tl.rsrc_b = dma_rsrc(wb + (g * per_g + col0) * ES, static_cast<uint32_t>((per_g - col0) * ES));
                 tl.o0b = static_cast<int>(col0);
             }
             tl.c_ptr = static_cast<uint16_t *>(args.out) + row0 * N + col0;
         }
+        if constexpr (F8)
+            tl.scale = args.x_scale[0] * args.w_scale[g];
         return tl;
     };
     auto c_rsrc = [&](const Tile &tl) {
@@ -730,7 +801,7 @@ grouped_gemm_kernel(const KernelArgs args) {
         constexpr bool MN = B ? B_MN : A_MN;
         const int      vo = voff[(B && !kSameOff) ? 1 : 0][j];
         if constexpr (MN)
-            return (vo + d.vadd) | (j & 1 ? d.mask1 : d.mask);
+            return (vo + d.vadd) | (mn_swz(j) ? d.mask1 : d.mask);
         else if constexpr (decltype(checked)::value)
             return vo | d.mask;
         else
@@ -743,10 +814,10 @@ grouped_gemm_kernel(const KernelArgs args) {
         dma16(dst + j * 4096, dma_voff(b_op, j, d, std::true_type{}), d.rs, d.so);
         sched_fence();
     };
-    // DMA whose M0 was written before the slot's MFMA.
-    auto dma_go = [&](auto b_op, const DmaSrc &d, auto j, auto checked) {
+    // DMA whose M0 was written before the slot's MFMA; cold: with the SGPR wait states.
+    auto dma_go = [&](auto b_op, const DmaSrc &d, auto j, auto checked, auto cold) {
         sched_fence();
-        dma16_m0(dma_voff(b_op, j, d, checked), d.rs, d.so);
+        dma16_m0<decltype(cold)::value ? 4 : 0>(dma_voff(b_op, j, d, checked), d.rs, d.so);
         sched_fence();
     };
     using A_OP = std::false_type;
@@ -919,10 +990,7 @@ grouped_gemm_kernel(const KernelArgs args) {
                 if constexpr (F8) {
                     const i32x8 bw = __builtin_shufflevector(fb[SA][ni][0], fb[SA][ni][1], 0, 1, 2, 3, 4, 5, 6, 7);
                     const i32x8 ax = __builtin_shufflevector(fa[mi & 1][0], fa[mi & 1][1], 0, 1, 2, 3, 4, 5, 6, 7);
-                    if constexpr (FIRST)
-                        mfma8_first<MODE == kFwdE5M2>(acc[mi][ni], bw, ax);
-                    else
-                        mfma8<MODE == kFwdE5M2>(acc[mi][ni], bw, ax);
+                    mfma8<mode_b_e5(MODE), mode_a_e5(MODE), FIRST>(acc[mi][ni], bw, ax);
                 } else if constexpr (FIRST && kh == 0)
                     mfma_first<F16>(acc[mi][ni], fb[SA][ni][0], fa[mi & 1][0]);
                 else
@@ -948,12 +1016,13 @@ grouped_gemm_kernel(const KernelArgs args) {
                 }
                 if constexpr (FUSE && P::epi(mi, idx) >= 0)
                     epi_store(ic<mi + 1>{}, ic<P::epi(mi, idx)>{});
+                using cold = std::integral_constant<bool, FUSE>;
                 if constexpr (dk == 1)
-                    dma_go(A_OP{}, src_a1, ic<dj>{}, chk{});
+                    dma_go(A_OP{}, src_a1, ic<dj>{}, chk{}, cold{});
                 else if constexpr (dk == 2)
-                    dma_go(B_OP{}, src_b3, ic<dj>{}, chk{});
+                    dma_go(B_OP{}, src_b3, ic<dj>{}, chk{}, cold{});
                 else if constexpr (dk == 3)
-                    dma_go(A_OP{}, src_a2, ic<dj>{}, chk{});
+                    dma_go(A_OP{}, src_a2, ic<dj>{}, chk{}, cold{});
             });
         });
     };
@@ -1182,7 +1251,7 @@ template <bool F16> __global__ void fill_randn_kernel(uint16_t *p, size_t n, uin
 } // namespace
 
 bool uses_cross_tile(const KernelArgs &args, int grid, int mode) {
-    if (mode == kWgrad)
+    if (mode_layout(mode) == kWgrad)
         return false;
     // Workgroups with a single tile gain nothing from the cross-tile pipeline.
     // (a device-built table's tile count is unknown on the host: take the cross-tile variant,
@@ -1193,7 +1262,7 @@ bool uses_cross_tile(const KernelArgs &args, int grid, int mode) {
 
 template <bool F16, int MODE>
 void launch_mode(const KernelArgs &args, bool cross, dim3 g, dim3 b, hipStream_t stream) {
-    if constexpr (MODE == kWgrad)
+    if constexpr (mode_layout(MODE) == kWgrad)
         hipLaunchKernelGGL((grouped_gemm_kernel<F16, false, MODE>), g, b, 0, stream, args);
     else if (cross)
         hipLaunchKernelGGL((grouped_gemm_kernel<F16, true, MODE>), g, b, 0, stream, args);
@@ -1201,29 +1270,57 @@ void launch_mode(const KernelArgs &args, bool cross, dim3 g, dim3 b, hipStream_t
         hipLaunchKernelGGL((grouped_gemm_kernel<F16, false, MODE>), g, b, 0, stream, args);
 }
 
-template <bool F16>
-void launch_dtype(const KernelArgs &args, bool cross, int mode, dim3 g, dim3 b, hipStream_t stream) {
-    if constexpr (!F16) {
-        if (mode == kFwdE4M3)
-            return launch_mode<false, kFwdE4M3>(args, cross, g, b, stream);
-        if (mode == kFwdE5M2)
-            return launch_mode<false, kFwdE5M2>(args, cross, g, b, stream);
+bool mode_supported(int mode, bool fp16) {
+    switch (mode) {
+    case make_mode(kFwd, kIn16):
+    case make_mode(kDgrad, kIn16):
+    case make_mode(kWgrad, kIn16):
+        return true;
+    case make_mode(kFwd, kInE4M3):
+    case make_mode(kFwd, kInE5M2):
+    case make_mode(kDgrad, kInE4M3):
+    case make_mode(kDgrad, kInE5M2):
+    case make_mode(kDgrad, kInE5M2xE4M3):
+    case make_mode(kWgrad, kInE4M3):
+    case make_mode(kWgrad, kInE5M2):
+    case make_mode(kWgrad, kInE5M2xE4M3):
+        return !fp16;
+    default:
+        return false;
     }
-    if (mode == kDgrad)
-        launch_mode<F16, kDgrad>(args, cross, g, b, stream);
-    else if (mode == kWgrad)
-        launch_mode<F16, kWgrad>(args, cross, g, b, stream);
-    else
-        launch_mode<F16, kFwd>(args, cross, g, b, stream);
 }
 
 hipError_t launch_grouped_gemm(const KernelArgs &args, bool fp16, int grid, hipStream_t stream, int mode) {
+    if (!mode_supported(mode, fp16))
+        return hipErrorInvalidValue;
     const bool cross = uses_cross_tile(args, grid, mode);
     const dim3 g(grid), b(kThreads);
-    if (fp16)
-        launch_dtype<true>(args, cross, mode, g, b, stream);
-    else
-        launch_dtype<false>(args, cross, mode, g, b, stream);
+#define GG_CASE(L, F)                                                                          \
+    case make_mode(L, F):                                                                      \
+        launch_mode<false, make_mode(L, F)>(args, cross, g, b, stream);                        \
+        break;
+    if (fp16) {
+        switch (mode) {
+        case make_mode(kFwd, kIn16): launch_mode<true, make_mode(kFwd, kIn16)>(args, cross, g, b, stream); break;
+        case make_mode(kDgrad, kIn16): launch_mode<true, make_mode(kDgrad, kIn16)>(args, cross, g, b, stream); break;
+        case make_mode(kWgrad, kIn16): launch_mode<true, make_mode(kWgrad, kIn16)>(args, cross, g, b, stream); break;
+        }
+    } else {
+        switch (mode) {
+            GG_CASE(kFwd, kIn16)
+            GG_CASE(kDgrad, kIn16)
+            GG_CASE(kWgrad, kIn16)
+            GG_CASE(kFwd, kInE4M3)
+            GG_CASE(kFwd, kInE5M2)
+            GG_CASE(kDgrad, kInE4M3)
+            GG_CASE(kDgrad, kInE5M2)
+            GG_CASE(kDgrad, kInE5M2xE4M3)
+            GG_CASE(kWgrad, kInE4M3)
+            GG_CASE(kWgrad, kInE5M2)
+            GG_CASE(kWgrad, kInE5M2xE4M3)
+        }
+    }
+#undef GG_CASE
     return hipGetLastError();
 }
 

@@ -28,7 +28,7 @@ extern "C" {
 #endif
 
 /* Element type of x, w and out. BF16 and FP16: same values as tunemax::DType
- * (common/backend.hpp:27). The fp8 types are inputs of gg_prepare_fp8 only (out is bf16). */
+ * (common/backend.hpp:27). The fp8 types are inputs of the fp8 entry points only (out is bf16). */
 typedef enum gg_dtype {
     GG_DTYPE_BF16     = 0,
     GG_DTYPE_FP16     = 1,
@@ -106,6 +106,24 @@ int gg_prepare_wgrad(int dtype, int group_num, int64_t n, int64_t k, const int64
 int gg_prepare_fp8(int dtype, int group_num, int64_t n, int64_t k, const int64_t *group_m,
                    const void *x, const void *w, const float *x_scale, const float *w_scale, void *out,
                    void *stream, gg_plan **plan_out);
+
+/*
+ * fp8 backward, the shapes of gg_prepare_dgrad / gg_prepare_wgrad with fp8 inputs and a bf16
+ * output scaled by grad_scale[0] * w_scale[g] (dgrad) or grad_scale[0] * x_scale[g] (wgrad):
+ * device scales, one for grad_out, one per group for the other operand (repeat a tensor-wise
+ * scale). Formats (grad_dtype x w_dtype / x_dtype): e4m3 x e4m3, e5m2 x e5m2, or the hybrid
+ * recipe's e5m2 gradient x e4m3. Replaces primus_turbo::ck_grouped_gemm_fp8 with a transposed
+ * operand and ck_grouped_gemm_fp8_variable_k
+ * (third_party/primus_turbo/include/primus_turbo/grouped_gemm.h:123-130, with the aq_ptr /
+ * bq_ptr scales of :72-74). Same plan life cycle as gg_prepare; N/A unless n and k are multiples
+ * of 16, plus the 2 GiB rules of gg_prepare_dgrad / gg_prepare_wgrad.
+ */
+int gg_prepare_dgrad_fp8(int grad_dtype, int w_dtype, int group_num, int64_t n, int64_t k,
+                         const int64_t *group_m, const void *grad_out, const void *w, const float *grad_scale,
+                         const float *w_scale, void *grad_x, void *stream, gg_plan **plan_out);
+int gg_prepare_wgrad_fp8(int grad_dtype, int x_dtype, int group_num, int64_t n, int64_t k,
+                         const int64_t *group_m, const void *grad_out, const void *x, const float *grad_scale,
+                         const float *x_scale, void *grad_w, void *stream, gg_plan **plan_out);
 
 /* Free the plan and its device table. Replaces CkTileBackend::release
  * (ck_kernel/ck_grouped_gemm.cpp:142-146). NULL is accepted. */

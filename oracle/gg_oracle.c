@@ -210,6 +210,70 @@ void gg_oracle_grouped_gemm_fp8(int fmt, int group_num, int64_t n, int64_t k, co
     }
 }
 
+static void fp8_lut(int fmt, float *lut) {
+    for (int i = 0; i < 256; ++i)
+        lut[i] = gg_oracle_fp8_to_f32(fmt, (uint8_t)i);
+}
+
+/* Follows gg_oracle_grouped_dgrad below with fp8 decode and the two scales. */
+void gg_oracle_grouped_dgrad_fp8(int a_fmt, int b_fmt, int group_num, int64_t n, int64_t k,
+                                 const int64_t *group_m, const uint8_t *grad_out, const uint8_t *w,
+                                 float a_scale, const float *b_scale, float *out) {
+    float la[256], lb[256];
+    fp8_lut(a_fmt, la);
+    fp8_lut(b_fmt, lb);
+    int64_t row0 = 0;
+    for (int g = 0; g < group_num; ++g) {
+        const int64_t  m  = group_m[g];
+        const uint8_t *wg = w + (int64_t)g * n * k;
+        const float    sc = a_scale * b_scale[g];
+#pragma omp parallel for schedule(static)
+        for (int64_t r = row0; r < row0 + m; ++r) {
+            float *o = out + r * k;
+            for (int64_t c = 0; c < k; ++c)
+                o[c] = 0.f;
+            for (int64_t j = 0; j < n; ++j) {
+                const float    a  = la[grad_out[r * n + j]];
+                const uint8_t *wr = wg + j * k;
+                for (int64_t c = 0; c < k; ++c)
+                    o[c] += a * lb[wr[c]];
+            }
+            for (int64_t c = 0; c < k; ++c)
+                o[c] *= sc;
+        }
+        row0 += m;
+    }
+}
+
+/* Follows gg_oracle_grouped_wgrad below with fp8 decode and the two scales. */
+void gg_oracle_grouped_wgrad_fp8(int a_fmt, int b_fmt, int group_num, int64_t n, int64_t k,
+                                 const int64_t *group_m, const uint8_t *grad_out, const uint8_t *x,
+                                 float a_scale, const float *b_scale, float *out) {
+    float la[256], lb[256];
+    fp8_lut(a_fmt, la);
+    fp8_lut(b_fmt, lb);
+    int64_t row0 = 0;
+    for (int g = 0; g < group_num; ++g) {
+        const int64_t m  = group_m[g];
+        const float   sc = a_scale * b_scale[g];
+#pragma omp parallel for schedule(static)
+        for (int64_t i = 0; i < n; ++i) {
+            float *o = out + ((int64_t)g * n + i) * k;
+            for (int64_t c = 0; c < k; ++c)
+                o[c] = 0.f;
+            for (int64_t r = row0; r < row0 + m; ++r) {
+                const float    a  = la[grad_out[r * n + i]];
+                const uint8_t *xr = x + r * k;
+                for (int64_t c = 0; c < k; ++c)
+                    o[c] += a * lb[xr[c]];
+            }
+            for (int64_t c = 0; c < k; ++c)
+                o[c] *= sc;
+        }
+        row0 += m;
+    }
+}
+
 static inline float dec(int dtype, uint16_t h) {
     return dtype == 0 ? gg_oracle_bf16_to_f32(h) : gg_oracle_f16_to_f32(h);
 }

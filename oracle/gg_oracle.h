@@ -21,6 +21,10 @@
  *                           Primus-Turbo (third_party/primus_turbo/include/primus_turbo/
  *                           grouped_gemm.h:72-74, 120-123: aq_ptr / bq_ptr); fp8 formats are the
  *                           OCP e4m3 (bias 7, no infinities, 0x7f/0xff NaN) and e5m2 (bias 15)
+ *   gg_oracle_grouped_dgrad_fp8 / gg_oracle_grouped_wgrad_fp8
+ *                           its fp8 backward (grouped_gemm.h:123-130: ck_grouped_gemm_fp8 with a
+ *                           transposed operand, ck_grouped_gemm_fp8_variable_k), per-operand
+ *                           formats (the gradient may be e5m2 while w or x is e4m3)
  *   gg_oracle_make_samples  bench/bench_main.cpp:210-227 (4 corners + 256 random per group,
  *                           one std::mt19937_64(1234) engine for all groups)
  *   gg_oracle_check         bench/bench_main.cpp:235-271 (|got-ref| <= atol + rtol*|ref|, NaN is a
@@ -80,6 +84,19 @@ float gg_oracle_fp8_to_f32(int fmt, uint8_t b);
 void gg_oracle_grouped_gemm_fp8(int fmt, int group_num, int64_t n, int64_t k, const int64_t *group_m,
                                 const uint8_t *x, const uint8_t *w, float x_scale, const float *w_scale,
                                 float *out);
+
+/* fp8 input gradient: out[row, c] (fp32) = (sum_j grad_out[row, j] * w[g, j, c]) * a_scale *
+ * b_scale[g]; grad_out [sum(group_m), n] in format a_fmt, w [group_num, n, k] in b_fmt. */
+void gg_oracle_grouped_dgrad_fp8(int a_fmt, int b_fmt, int group_num, int64_t n, int64_t k,
+                                 const int64_t *group_m, const uint8_t *grad_out, const uint8_t *w,
+                                 float a_scale, const float *b_scale, float *out);
+
+/* fp8 weight gradient: out[g, i, c] (fp32) = (sum over the rows r of group g of grad_out[r, i] *
+ * x[r, c]) * a_scale * b_scale[g], zero for an empty group; grad_out [sum(group_m), n] in a_fmt,
+ * x [sum(group_m), k] in b_fmt, out [group_num, n, k]. */
+void gg_oracle_grouped_wgrad_fp8(int a_fmt, int b_fmt, int group_num, int64_t n, int64_t k,
+                                 const int64_t *group_m, const uint8_t *grad_out, const uint8_t *x,
+                                 float a_scale, const float *b_scale, float *out);
 
 /* Same dot products for rows [row_begin, row_end) of one group only (out: [rows, n]).
  * The bounded CPU baseline sample. */

@@ -38,6 +38,14 @@ def lib() -> ctypes.CDLL:
             "gg_oracle_grouped_gemm_fp8": (None, [ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_int64,
                                                   ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                                   ctypes.c_float, ctypes.c_void_p, ctypes.c_void_p]),
+            "gg_oracle_grouped_dgrad_fp8": (None, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int64,
+                                                   ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
+                                                   ctypes.c_void_p, ctypes.c_float, ctypes.c_void_p,
+                                                   ctypes.c_void_p]),
+            "gg_oracle_grouped_wgrad_fp8": (None, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int64,
+                                                   ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
+                                                   ctypes.c_void_p, ctypes.c_float, ctypes.c_void_p,
+                                                   ctypes.c_void_p]),
             "gg_oracle_grouped_dgrad": (None, [ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_int64,
                                                ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                                ctypes.c_void_p]),
@@ -114,6 +122,36 @@ def grouped_gemm_fp8(fmt: int, x: np.ndarray, w: np.ndarray, group_m, x_scale: f
     out = np.zeros((int(gm.sum()), n), dtype=np.float32)
     lib().gg_oracle_grouped_gemm_fp8(fmt, b, n, k, gm.ctypes.data, x.ctypes.data, w.ctypes.data, float(x_scale),
                                      ws.ctypes.data, out.ctypes.data)
+    return out
+
+
+def grouped_dgrad_fp8(a_fmt: int, b_fmt: int, grad_out: np.ndarray, w: np.ndarray, group_m, a_scale: float,
+                      b_scale) -> np.ndarray:
+    """fp32 grad_x [sum(M), K] = (grad_out [sum(M), N] @ w[g] [N, K]) * a_scale * b_scale[g] per
+    group from fp8 bytes (formats 0: e4m3, 1: e5m2)."""
+    grad_out = np.ascontiguousarray(grad_out, dtype=np.uint8)
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    b, n, k = w.shape
+    gm = np.ascontiguousarray(group_m, dtype=np.int64)
+    bs = np.ascontiguousarray(b_scale, dtype=np.float32)
+    out = np.zeros((int(gm.sum()), k), dtype=np.float32)
+    lib().gg_oracle_grouped_dgrad_fp8(a_fmt, b_fmt, b, n, k, gm.ctypes.data, grad_out.ctypes.data, w.ctypes.data,
+                                      float(a_scale), bs.ctypes.data, out.ctypes.data)
+    return out
+
+
+def grouped_wgrad_fp8(a_fmt: int, b_fmt: int, grad_out: np.ndarray, x: np.ndarray, group_m, a_scale: float,
+                      b_scale) -> np.ndarray:
+    """fp32 grad_w [B, N, K] = (grad_out[g]^T @ x[g]) * a_scale * b_scale[g] per group from fp8
+    bytes; zero for an empty group."""
+    grad_out = np.ascontiguousarray(grad_out, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.uint8)
+    gm = np.ascontiguousarray(group_m, dtype=np.int64)
+    bs = np.ascontiguousarray(b_scale, dtype=np.float32)
+    n, k = grad_out.shape[1], x.shape[1]
+    out = np.zeros((len(gm), n, k), dtype=np.float32)
+    lib().gg_oracle_grouped_wgrad_fp8(a_fmt, b_fmt, len(gm), n, k, gm.ctypes.data, grad_out.ctypes.data,
+                                      x.ctypes.data, float(a_scale), bs.ctypes.data, out.ctypes.data)
     return out
 
 

@@ -237,6 +237,58 @@ def test_grouped_gemm_fp8_vs_numpy_float64(oracle, fmt):
         row += m
 
 
+@pytest.mark.parametrize("a_fmt,b_fmt", [(0, 0), (1, 1), (1, 0)])
+def test_backward_fp8_vs_numpy_float64(oracle, a_fmt, b_fmt):
+    """fp8 dgrad and wgrad (per-operand formats, tensor-wise gradient scale, per-group scale of
+    the other operand) vs numpy float64 on the decoded inputs; an empty group's wgrad is 0."""
+    rng = np.random.default_rng(11 + 2 * a_fmt + b_fmt)
+    tdt = {0: torch.float8_e4m3fn, 1: torch.float8_e5m2}
+    q = lambda shape, fmt: torch.from_numpy(rng.standard_normal(shape).astype(np.float32)).to(tdt[fmt]) \
+        .view(torch.uint8).numpy()
+    group_m, n, k = [7, 0, 33, 12], 48, 40
+    go = q((sum(group_m), n), a_fmt)
+    w = q((len(group_m), n, k), b_fmt)
+    x = q((sum(group_m), k), b_fmt)
+    bs = np.array([0.5, 4.0, 0.25, 2.0], dtype=np.float32)
+    gx = oracle.grouped_dgrad_fp8(a_fmt, b_fmt, go, w, group_m, 1.5, bs)
+    gw = oracle.grouped_wgrad_fp8(a_fmt, b_fmt, go, x, group_m, 1.5, bs)
+    gof = oracle.fp8_decode(a_fmt, go).astype(np.float64)
+    wf, xf = oracle.fp8_decode(b_fmt, w).astype(np.float64), oracle.fp8_decode(b_fmt, x).astype(np.float64)
+    row = 0
+    for g, m in enumerate(group_m):
+        np.testing.assert_allclose(gx[row:row + m], gof[row:row + m] @ wf[g] * 1.5 * bs[g], rtol=1e-4,
+                                   atol=1e-4 * np.sqrt(n))
+        want = gof[row:row + m].T @ xf[row:row + m] * 1.5 * bs[g] if m else np.zeros((n, k))
+        np.testing.assert_allclose(gw[g], want, rtol=1e-4, atol=1e-4 * np.sqrt(max(m, 1)))
+        row += m
+
+
+def test_backward_fp8_product_rule_and_mixed_formats(oracle):
+    """Small integers in e4m3 and e5m2 (both exact): the fp8 dgrad / wgrad equal int64 matmuls,
+    the 16-bit oracle's results on the same values, and satisfy the product rule with the fp8
+    forward. A swapped operand or format fails these."""
+    rng = np.random.default_rng(7)
+    group_m, n, k = [9, 0, 14, 3], 32, 48
+    gi = rng.integers(-3, 4, (sum(group_m), n))
+    xi = rng.integers(-3, 4, (sum(group_m), k))
+    wi = rng.integers(-3, 4, (len(group_m), n, k))
+    f8 = lambda a, fmt: torch.from_numpy(a.astype(np.float32)).to(
+        torch.float8_e5m2 if fmt else torch.float8_e4m3fn).view(torch.uint8).numpy()
+    ones = np.ones(len(group_m), dtype=np.float32)
+    gx = oracle.grouped_dgrad_fp8(1, 0, f8(gi, 1), f8(wi, 0), group_m, 1.0, ones).astype(np.int64)
+    gw = oracle.grouped_wgrad_fp8(1, 0, f8(gi, 1), f8(xi, 0), group_m, 1.0, ones).astype(np.int64)
+    out = oracle.grouped_gemm_fp8(0, f8(xi, 0), f8(wi, 0), group_m, 1.0, ones).astype(np.int64)
+    enc = lambda a: oracle_encode_np(0, a.astype(np.float32))
+    assert np.array_equal(gx, oracle.grouped_dgrad(0, enc(gi), enc(wi), group_m).astype(np.int64))
+    assert np.array_equal(gw, oracle.grouped_wgrad(0, enc(gi), enc(xi), group_m).astype(np.int64))
+    row = 0
+    for g, m in enumerate(group_m):
+        assert np.array_equal(gx[row:row + m], gi[row:row + m] @ wi[g])
+        assert np.array_equal(gw[g], gi[row:row + m].T @ xi[row:row + m])
+        row += m
+    assert (gi * out).sum() == (gw * wi).sum() == (gx * xi).sum()
+
+
 def test_group_rows_and_sampled_agree_with_full(oracle):
     dt, group_m, n, k = 0, [40, 9, 33], 56, 200
     x, w = _rand_problem(dt, group_m, n, k, seed=5)
