@@ -6,8 +6,9 @@ groups, x and w ~ N(0,1) from the seeded generator (x seed 1, w seed 2), inputs 
 HBM before timing (the reference's protocol, bench/bench_main.cpp:436-501).
 
 --op runs another pass of the same workload instead of the forward GEMM (default: forward, the
-headline): dgrad (grad_x = grad_out @ w[g]), wgrad (grad_w[g] = grad_out[g]^T @ x[g]), or the
-fp8 forward (e4m3 / e5m2 inputs, unit tensor-wise scales, bf16 out). Same FLOPs, 2 sum(M) N K.
+headline): dgrad (grad_x = grad_out @ w[g]), wgrad (grad_w[g] = grad_out[g]^T @ x[g]), the
+fp8 forward (e4m3 / e5m2 inputs, unit tensor-wise scales, bf16 out), or the fp8 dgrad / wgrad
+(e5m2 gradient, e4m3 w / x, unit scales, bf16 out). Same FLOPs, 2 sum(M) N K.
 
 Prints ONE JSON line on stdout. Besides the driver's fields it carries:
   roofline     the kernel against the dense bf16 MFMA peak (2.5 PFLOP/s): achieved = FLOPs
@@ -44,7 +45,7 @@ WORKLOADS = {
 HEADLINE = "moe_gate_up_b8_m4096_n4096_k7168_bf16"
 MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16/fp16
 FP8_PEAK_TFLOPS = 5000.0  # MI355X dense fp8
-OPS = ("fwd", "dgrad", "wgrad", "fp8_e4m3", "fp8_e5m2")
+OPS = ("fwd", "dgrad", "wgrad", "fp8_e4m3", "fp8_e5m2", "dgrad_fp8", "wgrad_fp8")
 
 
 def log(*a):
@@ -122,6 +123,17 @@ def other_pass(pkg, op, dtype, b, m, n, k, sh, dev):
         plan = pkg.BackwardPlan("wgrad", pkg.DType(dtype), n, k, group_m, gy.data_ptr(), x.data_ptr(),
                                 out.data_ptr(), sh)
         keep = (gy, x, out)
+    elif op in ("dgrad_fp8", "wgrad_fp8"):  # e5m2 gradient, e4m3 other operand, unit scales
+        gy = randn((rows, n), 3).to(torch.float8_e5m2)
+        other = randn((b, n, k), 2) if op == "dgrad_fp8" else randn((rows, k), 1)
+        other = other.to(torch.float8_e4m3fn)
+        gs = torch.ones(1, dtype=torch.float32, device=dev)
+        os_ = torch.ones(b, dtype=torch.float32, device=dev)
+        out = torch.zeros((rows, k) if op == "dgrad_fp8" else (b, n, k), dtype=torch.bfloat16, device=dev)
+        plan = pkg.BackwardPlan(op[:5], pkg.DType.FP8_E5M2, n, k, group_m, gy.data_ptr(), other.data_ptr(),
+                                out.data_ptr(), sh, other_dtype=pkg.DType.FP8_E4M3, grad_scale=gs.data_ptr(),
+                                other_scale=os_.data_ptr())
+        keep = (gy, other, gs, os_, out)
     else:  # fp8 forward: N(0,1) inputs rounded to the fp8 format, unit scales, bf16 out
         fdt = torch.float8_e4m3fn if op == "fp8_e4m3" else torch.float8_e5m2
         x = randn((rows, k), 1).to(fdt)
@@ -221,7 +233,7 @@ def main():
         log(f"[bench] cpu baseline: {cpu['value']} TFLOPS on {cpu['cores']} threads")
     be.release()
 
-    fp8 = args.op.startswith("fp8")
+    fp8 = "fp8" in args.op
     peak = FP8_PEAK_TFLOPS if fp8 else MFMA_PEAK_TFLOPS
     metric = "grouped-GEMM TFLOPS (bf16) + % of MFMA peak, 1 MI355X, per config"
     if args.op != "fwd":
@@ -237,7 +249,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": args.op[4:] if fp8 else "bf16" if dtype == 0 else "fp16",
+        "dtype": ("e5m2 x e4m3" if args.op.endswith("_fp8") else args.op[4:]) if fp8
+                 else "bf16" if dtype == 0 else "fp16",
         "data": "synthetic (seeded N(0,1), balanced groups)",
         "config": {"workload": args.workload, "op": args.op, "groups": b, "m_per_group": m, "n": n,
                    "k": k, "layout": "RCR", "parallelism": "single GPU"},
