@@ -82,6 +82,8 @@ std::unique_ptr<Backend> make_hipblaslt_grouped_backend();
 // One hipblasLtMatmul per group with a heuristic query each, over 4 streams (the
 // Primus-Turbo loop the reference compares against).
 std::unique_ptr<Backend> make_hipblaslt_loop_backend();
+// The same loop on the caller's stream only (no concurrent hipBLASLt kernels).
+std::unique_ptr<Backend> make_hipblaslt_seq_backend();
 
 // Name -> factory, for drivers (the reference hard-codes an if-chain,
 // bench/bench_main.cpp:398-407).
@@ -90,6 +92,7 @@ inline const std::map<std::string, std::function<std::unique_ptr<Backend>()>> &b
         {"mi355x", make_mi355x_backend},
         {"hipblaslt_grouped", make_hipblaslt_grouped_backend},
         {"hipblaslt_loop", make_hipblaslt_loop_backend},
+        {"hipblaslt_seq", make_hipblaslt_seq_backend},
     };
     return r;
 }

@@ -12,6 +12,9 @@
 //   handle per stream, and Primus-Turbo reports multi-stream stalls on MI355X without both
 //   (hipblaslt_grouped_gemm.cu:21-27, 40-55). Unlike Primus-Turbo, the side streams keep the
 //   default priority.
+// hipblaslt_seq: the same per-group loop (host lengths, heuristic per call, all timed) on the
+//   caller's stream alone. No two hipBLASLt kernels run at once, so it cannot stall the way
+//   the 4-stream loop did (below); it gives up the overlap of small groups.
 // hipblaslt_grouped: hipblaslt_ext::GroupedGemm, one launch for all groups, device-side
 //   arguments, heuristic top-1, prepared untimed; N/A when the library has no kernel for the
 //   type (the reference's backends/hipblaslt_grouped_backend.cpp:45-98).
@@ -41,11 +44,10 @@ hipDataType hip_type(DType t) { return t == DType::BF16 ? HIP_R_16BF : HIP_R_16F
 // ---------------------------------------------------------------------------------------
 class HipblasltLoopBackend final : public Backend {
 public:
-    static constexpr int     kStreams         = 4; // slots used per run
     static constexpr int     kSlots           = 8; // slots created (handle + stream + event)
     static constexpr int64_t kWorkspacePerStr = int64_t(64) << 20;
 
-    HipblasltLoopBackend() {
+    explicit HipblasltLoopBackend(int streams) : kStreams(streams) {
         for (int i = 0; i < kSlots; ++i)
             blas_check(hipblasLtCreate(&handle_[i]), "create");
         TUNEMAX_HIP_CHECK(hipMalloc(&workspace_, kStreams * kWorkspacePerStr));
@@ -65,7 +67,7 @@ public:
             (void)hipblasLtDestroy(handle_[i]);
     }
 
-    std::string name() const override { return "hipblaslt_loop"; }
+    std::string name() const override { return kStreams == 1 ? "hipblaslt_seq" : "hipblaslt_loop"; }
 
     std::string prepare(const GroupedGemmProblem &p, hipStream_t) override {
         if (p.group_lens_pinned == nullptr)
@@ -73,7 +75,7 @@ public:
         // This 4-stream loop never finished its first call on groups of 1024 x 4096 x 7168
         // (shapes/full.csv TestID 3) on MI355X, with one shared handle and again with one
         // handle per stream; it is not run there.
-        for (int g = 0; g < p.group_num; ++g)
+        for (int g = 0; g < p.group_num && kStreams > 1; ++g)
             if (p.group_m[g] == 1024 && p.n == 4096 && p.k == 7168)
                 return "skipped: the multi-stream hipBLASLt loop hung on 1024 x 4096 x 7168 groups on MI355X";
         p_ = p;
@@ -85,7 +87,8 @@ public:
         const size_t      es = dtype_bytes(p_.dtype);
         side_[0]             = stream;
         // fork: side streams start after everything already queued on the caller's stream
-        TUNEMAX_HIP_CHECK(hipEventRecord(ev_[0], stream));
+        if (kStreams > 1)
+            TUNEMAX_HIP_CHECK(hipEventRecord(ev_[0], stream));
         for (int i = 1; i < kStreams; ++i)
             TUNEMAX_HIP_CHECK(hipStreamWaitEvent(side_[i], ev_[0], 0));
         const float alpha = 1.0f, beta = 0.0f;
@@ -111,7 +114,10 @@ public:
         }
     }
 
-    std::string detail() const override { return "1 hipblasLtMatmul per group (heuristic each call), 4 streams"; }
+    std::string detail() const override {
+        return "1 hipblasLtMatmul per group (heuristic each call), " + std::to_string(kStreams) +
+               (kStreams == 1 ? " stream" : " streams");
+    }
 
 private:
     // D [m, n] col-major = op_T(A: k x m col-major) * B (k x n col-major), one group.
@@ -148,6 +154,7 @@ private:
         (void)hipblasLtMatmulDescDestroy(desc);
     }
 
+    const int          kStreams; // slots used per run: 4 (hipblaslt_loop) or 1 (hipblaslt_seq)
     hipblasLtHandle_t  handle_[kSlots]{};
     void              *workspace_ = nullptr;
     hipStream_t        side_[kSlots]{};
@@ -250,7 +257,8 @@ private:
 
 } // namespace
 
-std::unique_ptr<Backend> make_hipblaslt_loop_backend() { return std::make_unique<HipblasltLoopBackend>(); }
+std::unique_ptr<Backend> make_hipblaslt_loop_backend() { return std::make_unique<HipblasltLoopBackend>(4); }
+std::unique_ptr<Backend> make_hipblaslt_seq_backend() { return std::make_unique<HipblasltLoopBackend>(1); }
 std::unique_ptr<Backend> make_hipblaslt_grouped_backend() { return std::make_unique<HipblasltGroupedBackend>(); }
 
 } // namespace tunemax
