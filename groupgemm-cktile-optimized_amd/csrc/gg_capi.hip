@@ -110,6 +110,7 @@ void fill_args(gg_plan *plan, int n_xcd) {
     a.lda       = static_cast<int>(plan->k);
     a.ldb       = static_cast<int>(plan->k);
     a.m_out     = 0;
+    a.min_steps = 0;
     a.x_scale   = nullptr;
     a.w_scale   = nullptr;
     a.splits    = 1;
@@ -393,6 +394,12 @@ static int prepare_backward(int layout, int dtype_a, int dtype_b, int group_num,
         ka.ldb             = static_cast<int>(k);
         ka.m_out           = dgrad ? 0 : static_cast<int>(n);
         ka.k_tiles         = dgrad ? static_cast<int>(gg::cdiv(n, steps)) : 1;
+        if (!dgrad) { // fewest K steps of a group: the cross-tile variant needs every group's
+            int64_t mn = max_m;
+            for (int g = 0; g < group_num; ++g)
+                mn = std::min(mn, group_m[g]);
+            ka.min_steps = static_cast<int>(gg::cdiv(mn, steps));
+        }
         ka.x_scale         = f8 ? a_scale : nullptr;
         ka.w_scale         = f8 ? b_scale : nullptr;
         // wgrad's K steps differ per group: no split

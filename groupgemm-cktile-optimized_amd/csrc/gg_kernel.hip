@@ -497,7 +497,6 @@ grouped_gemm_kernel(const KernelArgs args) {
     constexpr int  KS     = kRowBytes / ES;    // contraction values per K step
     using P = std::conditional_t<F8, Plan8<reads_per_frag(A_MN), reads_per_frag(B_MN)>,
                                  Plan<reads_per_frag(A_MN), reads_per_frag(B_MN)>>;
-    static_assert(!(CROSS && LAYOUT == kWgrad), "wgrad has a K-step count per group");
     static_assert(!(F8 && F16), "fp8 writes bf16");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kLdsBytes];
     typedef __attribute__((address_space(3))) uint8_t lds_u8;
@@ -595,7 +594,6 @@ grouped_gemm_kernel(const KernelArgs args) {
     // tile) lives in physical stage (L + rot) mod n. A tile that follows with prefetched data
     // rotates by its predecessor's K-step count.
     int      rot_a = 0, rot_b = 0;
-    const int t_mod3 = T % 3;
     int      a_rd[2][2], b_rd[3][2]; // LDS read base per logical stage and k-half
     uint32_t a_dst[2], b_dst[3];     // this wave's DMA destination per logical stage
     auto set_stages = [&]() {
@@ -735,7 +733,7 @@ grouped_gemm_kernel(const KernelArgs args) {
     if (t >= total_units)
         return;
     Tile cur = make_tile(t), nxt = cur;
-    if constexpr (!CROSS)
+    if constexpr (!CROSS || LAYOUT == kWgrad)
         T = __builtin_amdgcn_readfirstlane(cur.T);
     bool cross_next = false; // the DMAs past this tile's last K step fetch `nxt`
 
@@ -1088,11 +1086,13 @@ grouped_gemm_kernel(const KernelArgs args) {
                 cur      = nxt;
                 t        = t_next;
                 rot_a    = (rot_a + T) & 1;
-                rot_b    = rot_b + t_mod3;
+                rot_b    = rot_b + T % 3;
                 rot_b    = rot_b >= 3 ? rot_b - 3 : rot_b;
                 set_stages();
                 if (T & 1) // the first step reads w set 0
                     sfor<0, 8>([&](auto ni) { sfor<0, 2>([&](auto h) { fb[0][ni][h] = fb[1][ni][h]; }); });
+                if constexpr (LAYOUT == kWgrad) // the next group's K-step count
+                    T = __builtin_amdgcn_readfirstlane(cur.T);
                 continue;
             }
         }
@@ -1251,20 +1251,19 @@ template <bool F16> __global__ void fill_randn_kernel(uint16_t *p, size_t n, uin
 } // namespace
 
 bool uses_cross_tile(const KernelArgs &args, int grid, int mode) {
-    if (mode_layout(mode) == kWgrad)
-        return false;
     // Workgroups with a single tile gain nothing from the cross-tile pipeline.
     // (a device-built table's tile count is unknown on the host: take the cross-tile variant,
     // which also handles workgroups with a single tile)
-    return kCrossAllowed && args.splits <= 1 && args.k_tiles >= kCrossMinSteps &&
+    // wgrad: every group's K-step count (the cross-tile pipeline prefetches three steps of the
+    // next tile inside the current one)
+    const int steps = mode_layout(mode) == kWgrad ? args.min_steps : args.k_tiles;
+    return kCrossAllowed && args.splits <= 1 && steps >= kCrossMinSteps &&
            (args.d_total != nullptr || args.total_tiles > grid);
 }
 
 template <bool F16, int MODE>
 void launch_mode(const KernelArgs &args, bool cross, dim3 g, dim3 b, hipStream_t stream) {
-    if constexpr (mode_layout(MODE) == kWgrad)
-        hipLaunchKernelGGL((grouped_gemm_kernel<F16, false, MODE>), g, b, 0, stream, args);
-    else if (cross)
+    if (cross)
         hipLaunchKernelGGL((grouped_gemm_kernel<F16, true, MODE>), g, b, 0, stream, args);
     else
         hipLaunchKernelGGL((grouped_gemm_kernel<F16, false, MODE>), g, b, 0, stream, args);

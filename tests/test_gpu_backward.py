@@ -132,6 +132,41 @@ def test_backward_large_vs_torch_fp32(pkg, case):
         row += m
 
 
+@pytest.mark.parametrize("dt", [0, 1])
+def test_wgrad_cross_tile_varying_groups(pkg, dt):
+    """More tiles than workgroups with every group at least 4 K steps long: the cross-tile
+    variant, whose K-step count changes at every group boundary (rows 300, 1000, 257, 700: partial
+    last steps of different lengths)."""
+    gm, n, k = [300, 1000, 257, 700], 2048, 2304
+    print(f"[backward] wgrad cross: dtype={dt} group_m={gm} N={n} K={k}", flush=True)
+    go = _rand(pkg, dt, (sum(gm), n), 5)
+    x = _rand(pkg, dt, (sum(gm), k), 6)
+    out, detail = _run(pkg, "wgrad", dt, gm, n, k, go, x)
+    assert "cross-tile" in detail, detail
+    row = 0
+    for g, m in enumerate(gm):
+        ref = go[row:row + m].float().t().contiguous() @ x[row:row + m].float()
+        got = out[g].float()
+        assert not torch.isnan(got).any(), f"group {g}: unwritten outputs ({detail})"
+        nbad = int(((got - ref).abs() > ATOL + RTOL * ref.abs()).sum())
+        assert nbad == 0, f"group {g}: {nbad} outputs off ({detail})"
+        row += m
+
+
+def test_wgrad_short_group_keeps_per_tile(pkg):
+    """A group shorter than 4 K steps (or empty) keeps wgrad on the per-tile variant."""
+    gm, n, k = [300, 100, 700], 2048, 2304
+    go = _rand(pkg, 0, (sum(gm), n), 7)
+    x = _rand(pkg, 0, (sum(gm), k), 8)
+    out, detail = _run(pkg, "wgrad", 0, gm, n, k, go, x)
+    assert "per-tile" in detail, detail
+    row = 0
+    for g, m in enumerate(gm):
+        ref = go[row:row + m].float().t().contiguous() @ x[row:row + m].float()
+        assert ((out[g].float() - ref).abs() <= ATOL + RTOL * ref.abs()).all(), f"group {g}"
+        row += m
+
+
 def test_torch_wrappers(pkg):
     gm, n, k = [100, 0, 412], 264, 520
     go = _rand(pkg, 1, (sum(gm), n), 1)

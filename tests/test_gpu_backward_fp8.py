@@ -144,6 +144,28 @@ def test_backward_fp8_large_vs_torch_fp32(pkg, kind, fmts, b, m, n, k):
         assert nbad == 0, f"group {g}: {nbad} outputs off ({detail})"
 
 
+@pytest.mark.parametrize("fmts", FMTS)
+def test_wgrad_fp8_cross_tile_varying_groups(pkg, fmts):
+    """fp8 wgrad on the cross-tile variant: more tiles than workgroups, every group at least
+    4 K steps of 128 rows, group lengths (and so K-step counts and scales) changing between
+    tiles."""
+    gm, n, k = [600, 1000, 513, 1400], 2048, 2304
+    print(f"[fp8 backward] wgrad cross: formats={fmts} group_m={gm} N={n} K={k}", flush=True)
+    go = _fp8((sum(gm), n), fmts[0], 12).to(DEV)
+    x = _fp8((sum(gm), k), fmts[1], 13).to(DEV)
+    xs = [0.5, 1.5, 2.0, 0.25]
+    out, detail = _run(pkg, "wgrad", fmts, gm, n, k, go, x, 2.0, xs)
+    assert "cross-tile" in detail, detail
+    row = 0
+    for g, m in enumerate(gm):
+        ref = (go[row:row + m].float().t().contiguous() @ x[row:row + m].float()) * (2.0 * xs[g])
+        got = out[g].float()
+        assert not torch.isnan(got).any(), f"group {g}: unwritten outputs ({detail})"
+        nbad = int(((got - ref).abs() > ATOL + RTOL * ref.abs()).sum())
+        assert nbad == 0, f"group {g}: {nbad} outputs off ({detail})"
+        row += m
+
+
 def test_dgrad_fp8_split_k(pkg, oracle, monkeypatch):
     """Few output tiles and a long contraction: split-K with the fp8 scales applied once."""
     monkeypatch.setenv("GG_SPLIT_K", "3")
