@@ -56,6 +56,11 @@ C_API = {
     "gg_prepare_wgrad": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_int64,
                                         ctypes.POINTER(ctypes.c_int64), ctypes.c_void_p, ctypes.c_void_p,
                                         ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)]),
+    "gg_prepare_device_lens_op": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                                 ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p,
+                                                 ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                                 ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                                 ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)]),
     "gg_prepare_dgrad_fp8": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int64,
                                             ctypes.c_int64, ctypes.POINTER(ctypes.c_int64), ctypes.c_void_p,
                                             ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
@@ -279,6 +284,77 @@ class BackwardPlan:
             pass
 
 
+OP_FORWARD, OP_DGRAD, OP_WGRAD = 0, 1, 2  # gg_op
+
+
+class DeviceLensPlan:
+    """A plan over device-resident group sizes for any pass (gg_prepare_device_lens_op): op
+    OP_FORWARD / OP_DGRAD / OP_WGRAD, a_dtype / b_dtype the input types (fp8 with device float32
+    scales a_scale [1], b_scale [group_num]). Every run re-reads group_lens (and group_offs, or 0
+    for back-to-back groups) on the stream; status() reports sizes that did not fit."""
+
+    def __init__(self, op: int, a_dtype: DType, b_dtype: DType, group_num: int, total_m: int, n: int, k: int,
+                 group_lens: int, group_offs: int, a: int, b: int, out: int, stream: int = 0,
+                 a_scale: int = 0, b_scale: int = 0) -> None:
+        self._lib = load_library()
+        self._plan = ctypes.c_void_p()
+        _check(self._lib.gg_prepare_device_lens_op(op, int(a_dtype), int(b_dtype), group_num, total_m, n, k,
+                                                   group_lens, group_offs or None, a, b, a_scale or None,
+                                                   b_scale or None, out, stream, ctypes.byref(self._plan)))
+
+    def run(self, stream: int = 0) -> None:
+        _check(self._lib.gg_run(self._plan, stream))
+
+    def status(self, stream: int = 0):
+        """(status, tile count, message) of the last run's device-side size check; synchronizes."""
+        tiles = ctypes.c_int(0)
+        st = self._lib.gg_plan_device_status(self._plan, stream, ctypes.byref(tiles))
+        return st, tiles.value, last_error() if st != GG_OK else ""
+
+    def detail(self) -> str:
+        return self._lib.gg_plan_detail(self._plan).decode() if self._plan else ""
+
+    def release(self) -> None:
+        if self._plan:
+            self._lib.gg_release(self._plan)
+            self._plan = ctypes.c_void_p()
+
+    def __del__(self) -> None:
+        try:
+            self.release()
+        except Exception:
+            pass
+
+
+def _device_sizes(group_m, group_offs, b):
+    """Validates device group sizes (and offsets); True if group_m is a device tensor."""
+    import torch
+
+    if not isinstance(group_m, torch.Tensor):
+        if group_offs is not None:
+            raise ValueError("group_offs goes with device group sizes")
+        return False
+    if not (group_m.is_cuda and group_m.dtype == torch.int64 and group_m.numel() == b and group_m.is_contiguous()):
+        raise ValueError("device group sizes must be a contiguous int64 cuda tensor of B entries")
+    if group_offs is not None and not (group_offs.is_cuda and group_offs.dtype == torch.int64
+                                       and group_offs.numel() == b + 1 and group_offs.is_contiguous()):
+        raise ValueError("group_offs must be a contiguous int64 cuda tensor of B + 1 entries")
+    return True
+
+
+def _run_device_plan(plan: DeviceLensPlan, s: int, dev) -> None:
+    import torch
+
+    try:
+        plan.run(s)
+        st, _, msg = plan.status(s)
+        if st != GG_OK:
+            raise GGError(st, msg)
+        torch.cuda.current_stream(dev).synchronize()
+    finally:
+        plan.release()
+
+
 class Fp8Plan:
     """An fp8 forward plan (gg_prepare_fp8): out (bf16) = (x[g] @ w[g]^T) * x_scale[0] *
     w_scale[g], tensor-wise scales in device memory (float32). Run any number of times."""
@@ -355,30 +431,42 @@ def fill_randn(dtype: DType, ptr: int, count: int, seed: int, stream: int = 0) -
     _check(load_library().gg_fill_randn(int(dtype), ptr, count, seed, stream))
 
 
-def _backward(kind: str, grad_out, other, group_m: Sequence[int], out, stream: Optional[int]):
+def _backward_shapes(kind, grad_out, other, group_m, device_sizes):
+    n = grad_out.shape[1]
+    b = group_m.numel() if device_sizes else len(group_m)
+    if not device_sizes and grad_out.shape[0] != sum(group_m):
+        raise ValueError("grad_out must have sum(group_m) rows")
+    if kind == "dgrad":
+        if other.shape[0] != b or other.shape[1] != n:
+            raise ValueError("w must be [B, N, K] with N = grad_out's columns")
+        k = other.shape[2]
+        return n, k, (grad_out.shape[0], k)
+    if other.shape[0] != grad_out.shape[0]:
+        raise ValueError("x must have the rows of grad_out")
+    k = other.shape[1]
+    return n, k, (b, n, k)
+
+
+def _backward(kind: str, grad_out, other, group_m, out, stream: Optional[int], group_offs=None):
     import torch
 
     if grad_out.dtype != other.dtype or grad_out.dtype not in (torch.bfloat16, torch.float16):
         raise TypeError("operands must both be bfloat16 or both float16")
     if not (grad_out.is_cuda and other.is_cuda and grad_out.is_contiguous() and other.is_contiguous()):
         raise ValueError("operands must be contiguous device tensors")
-    n = grad_out.shape[1]
-    if grad_out.shape[0] != sum(group_m):
-        raise ValueError("grad_out must have sum(group_m) rows")
-    if kind == "dgrad":
-        if other.shape[0] != len(group_m) or other.shape[1] != n:
-            raise ValueError("w must be [B, N, K] with N = grad_out's columns")
-        k = other.shape[2]
-        shape = (grad_out.shape[0], k)
-    else:
-        if other.shape[0] != grad_out.shape[0]:
-            raise ValueError("x must have the rows of grad_out")
-        k = other.shape[1]
-        shape = (len(group_m), n, k)
+    b = group_m.numel() if isinstance(group_m, torch.Tensor) else len(group_m)
+    device_sizes = _device_sizes(group_m, group_offs, b)
+    n, k, shape = _backward_shapes(kind, grad_out, other, group_m, device_sizes)
     if out is None:
         out = torch.empty(shape, dtype=grad_out.dtype, device=grad_out.device)
     s = torch.cuda.current_stream(grad_out.device).cuda_stream if stream is None else stream
     dt = DType.BF16 if grad_out.dtype == torch.bfloat16 else DType.FP16
+    if device_sizes:
+        plan = DeviceLensPlan(OP_DGRAD if kind == "dgrad" else OP_WGRAD, dt, dt, b, grad_out.shape[0], n, k,
+                              group_m.data_ptr(), group_offs.data_ptr() if group_offs is not None else 0,
+                              grad_out.data_ptr(), other.data_ptr(), out.data_ptr(), s)
+        _run_device_plan(plan, s, grad_out.device)
+        return out
     plan = BackwardPlan(kind, dt, n, k, list(group_m), grad_out.data_ptr(), other.data_ptr(), out.data_ptr(), s)
     try:
         plan.run(s)
@@ -388,7 +476,7 @@ def _backward(kind: str, grad_out, other, group_m: Sequence[int], out, stream: O
     return out
 
 
-def _backward_fp8(kind: str, grad_out, other, group_m: Sequence[int], grad_scale, other_scale, out, stream):
+def _backward_fp8(kind: str, grad_out, other, group_m, grad_scale, other_scale, out, stream, group_offs=None):
     import torch
 
     kinds = {torch.float8_e4m3fn: DType.FP8_E4M3, torch.float8_e5m2: DType.FP8_E5M2}
@@ -398,22 +486,21 @@ def _backward_fp8(kind: str, grad_out, other, group_m: Sequence[int], grad_scale
         raise ValueError("operands must be contiguous device tensors")
     if not (grad_scale.dtype == other_scale.dtype == torch.float32 and grad_scale.is_cuda and other_scale.is_cuda):
         raise TypeError("scales must be float32 device tensors")
-    n = grad_out.shape[1]
-    if grad_out.shape[0] != sum(group_m) or other_scale.numel() != len(group_m):
-        raise ValueError("grad_out must have sum(group_m) rows and other_scale one value per group")
-    if kind == "dgrad":
-        if other.shape[0] != len(group_m) or other.shape[1] != n:
-            raise ValueError("w must be [B, N, K] with N = grad_out's columns")
-        k = other.shape[2]
-        shape = (grad_out.shape[0], k)
-    else:
-        if other.shape[0] != grad_out.shape[0]:
-            raise ValueError("x must have the rows of grad_out")
-        k = other.shape[1]
-        shape = (len(group_m), n, k)
+    b = group_m.numel() if isinstance(group_m, torch.Tensor) else len(group_m)
+    device_sizes = _device_sizes(group_m, group_offs, b)
+    if other_scale.numel() != b:
+        raise ValueError("other_scale must hold one value per group")
+    n, k, shape = _backward_shapes(kind, grad_out, other, group_m, device_sizes)
     if out is None:
         out = torch.empty(shape, dtype=torch.bfloat16, device=grad_out.device)
     s = torch.cuda.current_stream(grad_out.device).cuda_stream if stream is None else stream
+    if device_sizes:
+        plan = DeviceLensPlan(OP_DGRAD if kind == "dgrad" else OP_WGRAD, kinds[grad_out.dtype], kinds[other.dtype],
+                              b, grad_out.shape[0], n, k, group_m.data_ptr(),
+                              group_offs.data_ptr() if group_offs is not None else 0, grad_out.data_ptr(),
+                              other.data_ptr(), out.data_ptr(), s, grad_scale.data_ptr(), other_scale.data_ptr())
+        _run_device_plan(plan, s, grad_out.device)
+        return out
     plan = BackwardPlan(kind, kinds[grad_out.dtype], n, k, list(group_m), grad_out.data_ptr(), other.data_ptr(),
                         out.data_ptr(), s, other_dtype=kinds[other.dtype], grad_scale=grad_scale.data_ptr(),
                         other_scale=other_scale.data_ptr())
@@ -425,28 +512,31 @@ def _backward_fp8(kind: str, grad_out, other, group_m: Sequence[int], grad_scale
     return out
 
 
-def grouped_gemm_dgrad_fp8(grad_out, w, group_m: Sequence[int], grad_scale, w_scale, out=None,
-                           stream: Optional[int] = None):
+def grouped_gemm_dgrad_fp8(grad_out, w, group_m, grad_scale, w_scale, out=None, stream: Optional[int] = None,
+                           group_offs=None):
     """bf16 grad_x = (grad_out [sum(M), N] @ w[g] [N, K]) * grad_scale * w_scale[g] for float8
-    tensors (gradient e4m3 or e5m2, w e4m3 or matching) and float32 device scales."""
-    return _backward_fp8("dgrad", grad_out, w, group_m, grad_scale, w_scale, out, stream)
+    tensors (gradient e4m3 or e5m2, w e4m3 or matching) and float32 device scales. group_m: host
+    sequence, or device int64 tensor (with optional device offsets), as for grouped_gemm."""
+    return _backward_fp8("dgrad", grad_out, w, group_m, grad_scale, w_scale, out, stream, group_offs)
 
 
-def grouped_gemm_wgrad_fp8(grad_out, x, group_m: Sequence[int], grad_scale, x_scale, out=None,
-                           stream: Optional[int] = None):
+def grouped_gemm_wgrad_fp8(grad_out, x, group_m, grad_scale, x_scale, out=None, stream: Optional[int] = None,
+                           group_offs=None):
     """bf16 grad_w [B, N, K] = (grad_out[g]^T @ x[g]) * grad_scale * x_scale[g] for float8 tensors,
-    zero for empty groups."""
-    return _backward_fp8("wgrad", grad_out, x, group_m, grad_scale, x_scale, out, stream)
+    zero for empty groups. group_m: host sequence or device int64 tensor."""
+    return _backward_fp8("wgrad", grad_out, x, group_m, grad_scale, x_scale, out, stream, group_offs)
 
 
-def grouped_gemm_dgrad(grad_out, w, group_m: Sequence[int], out=None, stream: Optional[int] = None):
-    """grad_x [sum(M), K] = grad_out [sum(M), N] @ w[g] [N, K] per group (torch tensors)."""
-    return _backward("dgrad", grad_out, w, group_m, out, stream)
+def grouped_gemm_dgrad(grad_out, w, group_m, out=None, stream: Optional[int] = None, group_offs=None):
+    """grad_x [sum(M), K] = grad_out [sum(M), N] @ w[g] [N, K] per group (torch tensors). group_m:
+    host sequence, or device int64 tensor (with optional device offsets), as for grouped_gemm."""
+    return _backward("dgrad", grad_out, w, group_m, out, stream, group_offs)
 
 
-def grouped_gemm_wgrad(grad_out, x, group_m: Sequence[int], out=None, stream: Optional[int] = None):
-    """grad_w [B, N, K] = grad_out[g]^T @ x[g] per group, zero for empty groups (torch tensors)."""
-    return _backward("wgrad", grad_out, x, group_m, out, stream)
+def grouped_gemm_wgrad(grad_out, x, group_m, out=None, stream: Optional[int] = None, group_offs=None):
+    """grad_w [B, N, K] = grad_out[g]^T @ x[g] per group, zero for empty groups (torch tensors).
+    group_m: host sequence or device int64 tensor."""
+    return _backward("wgrad", grad_out, x, group_m, out, stream, group_offs)
 
 
 def compute_group_offs(group_lens, stream: Optional[int] = None):

@@ -38,6 +38,7 @@ struct gg_plan {
     const int64_t      *d_offs      = nullptr;
     gg::TableHeader    *d_header    = nullptr; // follows the table in the d_groups allocation
     float              *d_ws        = nullptr; // split-K partial sums (args.ws)
+    int64_t             in_rows     = 0;       // device-size plans: rows of the inputs
 };
 
 namespace {
@@ -556,37 +557,108 @@ int gg_prepare_wgrad_fp8(int grad_dtype, int x_dtype, int group_num, int64_t n, 
 int gg_prepare_device_lens(int dtype, int group_num, int64_t total_m, int64_t n, int64_t k,
                            const int64_t *group_lens, const int64_t *group_offs, const void *x,
                            const void *w, void *out, void *stream, gg_plan **plan_out) {
+    if (dtype != GG_DTYPE_BF16 && dtype != GG_DTYPE_FP16) {
+        g_last_error.clear();
+        if (plan_out != nullptr)
+            *plan_out = nullptr;
+        return fail(GG_ERR_INVALID, "dtype must be GG_DTYPE_BF16 or GG_DTYPE_FP16");
+    }
+    return gg_prepare_device_lens_op(GG_OP_FORWARD, dtype, dtype, group_num, total_m, n, k, group_lens,
+                                     group_offs, x, w, nullptr, nullptr, out, stream, plan_out);
+}
+
+int gg_prepare_device_lens_op(int op, int a_dtype, int b_dtype, int group_num, int64_t total_m, int64_t n,
+                              int64_t k, const int64_t *group_lens, const int64_t *group_offs, const void *a,
+                              const void *b, const float *a_scale, const float *b_scale, void *out,
+                              void *stream, gg_plan **plan_out) {
     g_last_error.clear();
     if (plan_out == nullptr)
         return fail(GG_ERR_INVALID, "plan_out is null");
     *plan_out = nullptr;
-    if (total_m < 0)
-        return fail(GG_ERR_INVALID, "total_m must be >= 0");
+    if (op != GG_OP_FORWARD && op != GG_OP_DGRAD && op != GG_OP_WGRAD)
+        return fail(GG_ERR_INVALID, "op must be GG_OP_FORWARD, GG_OP_DGRAD or GG_OP_WGRAD");
+    if (total_m < 0 || group_num < 0 || n < 0 || k < 0)
+        return fail(GG_ERR_INVALID, "group_num, total_m, n and k must be >= 0");
     if (group_num > 0 && group_lens == nullptr)
         return fail(GG_ERR_INVALID, "group_lens is null");
-    const bool has_output = total_m > 0 && n > 0;
-    const int  st         = check_problem(dtype, group_num, n, k, has_output, x, w, out);
-    if (st != GG_OK)
-        return st;
+    // Input formats: two equal 16-bit types, or fp8 (forward: both e4m3 or both e5m2; backward
+    // also an e5m2 gradient with e4m3 w / x).
+    const bool f8     = a_dtype == GG_DTYPE_FP8_E4M3 || a_dtype == GG_DTYPE_FP8_E5M2;
+    int        format = gg::kIn16;
+    if (f8) {
+        if (a_dtype == GG_DTYPE_FP8_E4M3 && b_dtype == GG_DTYPE_FP8_E4M3)
+            format = gg::kInE4M3;
+        else if (a_dtype == GG_DTYPE_FP8_E5M2 && b_dtype == GG_DTYPE_FP8_E5M2)
+            format = gg::kInE5M2;
+        else if (op != GG_OP_FORWARD && a_dtype == GG_DTYPE_FP8_E5M2 && b_dtype == GG_DTYPE_FP8_E4M3)
+            format = gg::kInE5M2xE4M3;
+        else
+            return fail(GG_ERR_INVALID, "unsupported pair of fp8 formats");
+    } else if ((a_dtype != GG_DTYPE_BF16 && a_dtype != GG_DTYPE_FP16) || b_dtype != a_dtype) {
+        return fail(GG_ERR_INVALID, "dtypes must be equal bf16 / fp16 types, or fp8 formats");
+    }
+    const int     layout   = op == GG_OP_FORWARD ? gg::kFwd : op == GG_OP_DGRAD ? gg::kDgrad : gg::kWgrad;
+    // kernel terms (KernelArgs): output columns N_out, contraction K_c, output rows
+    const int64_t n_out    = op == GG_OP_FORWARD ? n : k;
+    const int64_t k_c      = op == GG_OP_FORWARD ? k : op == GG_OP_DGRAD ? n : 0; // wgrad: per group
+    const int64_t out_rows = op == GG_OP_WGRAD ? int64_t(group_num) * n : total_m;
+    const bool    has_output = out_rows > 0 && n_out > 0;
+    const bool    reads      = op == GG_OP_WGRAD ? total_m > 0 : (total_m > 0 && k_c > 0);
+    if (has_output && (out == nullptr || (reads && (a == nullptr || b == nullptr))))
+        return fail(GG_ERR_INVALID, "the inputs and the output must be device pointers");
+    if (f8 && has_output && reads && (a_scale == nullptr || b_scale == nullptr))
+        return fail(GG_ERR_INVALID, "fp8 scales must be device pointers");
+    // 16-byte rows; transposed fp8 operands move 16-column blocks
+    const int64_t align_n = (f8 && op != GG_OP_FORWARD) ? 16 : 8;
+    const int64_t align_k = f8 ? 16 : 8;
+    if (n % align_n != 0)
+        return fail(GG_ERR_UNSUPPORTED, "N must be a multiple of " + std::to_string(align_n));
+    if (k % align_k != 0)
+        return fail(GG_ERR_UNSUPPORTED, "K must be a multiple of " + std::to_string(align_k));
+    if (has_output && (!aligned16(out) || (reads && (!aligned16(a) || !aligned16(b)))))
+        return fail(GG_ERR_UNSUPPORTED, "buffers must be 16-byte aligned");
+    if (k > (int64_t(1) << 21) || n > (int64_t(1) << 21))
+        return fail(GG_ERR_UNSUPPORTED, "N and K must be at most 2097152");
+    const int64_t lim   = int64_t(1) << 31;
+    const int64_t es    = f8 ? 1 : 2;
+    const int64_t steps = f8 ? 128 : gg::kTileK;
+    if (op == GG_OP_DGRAD && (n + steps) * k * es >= lim)
+        return fail(GG_ERR_UNSUPPORTED, "one group's w must be smaller than 2 GiB");
+    // wgrad: a group may hold every row
+    if (op == GG_OP_WGRAD && ((total_m + steps) * n * es >= lim || (total_m + steps) * k * es >= lim))
+        return fail(GG_ERR_UNSUPPORTED, "grad_out and x rows must be smaller than 2 GiB");
 
     auto *plan = new (std::nothrow) gg_plan;
     if (plan == nullptr)
         return fail(GG_ERR_INVALID, "out of host memory");
-    plan->dtype       = dtype;
+    plan->mode        = gg::make_mode(layout, format);
+    plan->dtype       = f8 ? GG_DTYPE_BF16 : a_dtype; // output
     plan->group_num   = group_num;
-    plan->n           = n;
-    plan->k           = k;
-    plan->total_m     = total_m;
-    plan->x           = x;
-    plan->w           = w;
+    plan->n           = n_out;
+    plan->k           = k_c;
+    plan->total_m     = out_rows;
+    plan->in_rows     = total_m;
+    plan->x           = a;
+    plan->w           = b;
     plan->out         = out;
     plan->device_lens = true;
     plan->d_lens      = group_lens;
     plan->d_offs      = group_offs;
-    if (!has_output || k == 0 || group_num == 0) {
-        plan->detail = "mi355x: no launch (" +
-                       std::string(!has_output || group_num == 0 ? "empty output" : "K = 0, zero fill") +
+    const std::string what = std::string(op == GG_OP_FORWARD ? "" : op == GG_OP_DGRAD ? "dgrad " : "wgrad ") +
+                             (format == gg::kIn16     ? std::string(a_dtype == GG_DTYPE_BF16 ? "bf16" : "fp16")
+                              : format == gg::kInE4M3 ? std::string("fp8 e4m3")
+                              : format == gg::kInE5M2 ? std::string("fp8 e5m2")
+                                                      : std::string("fp8 e5m2 x e4m3"));
+    const bool no_launch = !has_output || group_num == 0 || (op != GG_OP_WGRAD && k_c == 0);
+    if (no_launch) {
+        // forward / dgrad with an empty contraction: gg_run zero-fills the output
+        plan->detail = "mi355x " + what + ": no launch (" +
+                       (has_output && group_num > 0
+                            ? (op == GG_OP_FORWARD ? "K = 0, zero fill" : "empty contraction, zero fill")
+                            : "empty output") +
                        ")";
+        if (!has_output || group_num == 0)
+            plan->total_m = 0;
         *plan_out = plan;
         return GG_OK;
     }
@@ -604,19 +676,45 @@ int gg_prepare_device_lens(int dtype, int group_num, int64_t total_m, int64_t n,
     }
     plan->d_header = reinterpret_cast<gg::TableHeader *>(reinterpret_cast<char *>(plan->d_groups) +
                                                          table_bytes);
-    // Tile count is unknown here: one workgroup per CU, or fewer if even the largest routing
-    // (every group's rows tiled separately) has fewer tiles.
-    const int64_t n_tiles   = gg::cdiv(n, gg::kTileN);
-    const int64_t max_tiles = (gg::cdiv(total_m, gg::kTileM) + group_num) * n_tiles;
-    plan->grid              = static_cast<int>(std::min<int64_t>(prop.multiProcessorCount, max_tiles));
-    fill_args(plan, xcd_count(prop));
-    plan->args.total_tiles = 0;
-    plan->args.d_total     = &plan->d_header->total_tiles;
-    plan->detail = "mi355x persistent 256x256x64 " +
-                   std::string(dtype == GG_DTYPE_BF16 ? "bf16" : "fp16") +
-                   " grid=" + std::to_string(plan->grid) + " tiles=device xcd=" +
-                   std::to_string(plan->args.n_xcd) +
-                   (gg::uses_cross_tile(plan->args, plan->grid) ? " cross-tile" : " per-tile") +
+    const int64_t n_tiles = gg::cdiv(n_out, gg::kTileN);
+    fill_args(plan, 1);
+    gg::KernelArgs &ka = plan->args;
+    ka.k_tiles         = op == GG_OP_WGRAD ? 1 : static_cast<int>(gg::cdiv(k_c, steps));
+    ka.x_scale         = f8 ? a_scale : nullptr;
+    ka.w_scale         = f8 ? b_scale : nullptr;
+    if (op != GG_OP_FORWARD) {
+        ka.lda = static_cast<int>(n);
+        ka.ldb = static_cast<int>(k);
+    }
+    if (op == GG_OP_WGRAD) {
+        // Output tiles do not depend on the sizes: m_out rows per group. The K-step counts do,
+        // so the per-tile variant runs (min_steps = 0).
+        ka.m_out       = static_cast<int>(n);
+        ka.min_steps   = 0;
+        const int64_t tiles = int64_t(group_num) * gg::cdiv(n, gg::kTileM) * n_tiles;
+        if (tiles > INT32_MAX) {
+            free_plan(plan);
+            return fail(GG_ERR_UNSUPPORTED, "too many tiles for 32-bit tile indices");
+        }
+        plan->total_tiles = static_cast<int>(tiles);
+        plan->grid        = static_cast<int>(std::min<int64_t>(prop.multiProcessorCount, tiles));
+        ka.total_tiles    = plan->total_tiles;
+        ka.d_total        = nullptr;
+    } else {
+        // Tile count is unknown here: one workgroup per CU, or fewer if even the largest routing
+        // (every group's rows tiled separately) has fewer tiles.
+        const int64_t max_tiles = (gg::cdiv(total_m, gg::kTileM) + group_num) * n_tiles;
+        plan->grid     = static_cast<int>(std::min<int64_t>(prop.multiProcessorCount, max_tiles));
+        ka.total_tiles = 0;
+        ka.d_total     = &plan->d_header->total_tiles;
+    }
+    const int n_xcd = xcd_count(prop);
+    ka.n_xcd        = plan->grid % n_xcd == 0 ? n_xcd : 1;
+    plan->detail = "mi355x " + what + " persistent 256x256x" + std::to_string(f8 ? 128 : 64) + " grid=" +
+                   std::to_string(plan->grid) + " tiles=" +
+                   (op == GG_OP_WGRAD ? std::to_string(plan->total_tiles) : std::string("device")) +
+                   " xcd=" + std::to_string(ka.n_xcd) +
+                   (gg::uses_cross_tile(ka, plan->grid, plan->mode) ? " cross-tile" : " per-tile") +
                    " (device group sizes)";
     *plan_out = plan;
     return GG_OK;
@@ -628,8 +726,9 @@ int gg_run(const gg_plan *plan, void *stream) {
     const hipStream_t s = static_cast<hipStream_t>(stream);
     if (plan->device_lens && plan->d_groups != nullptr) {
         hipError_t e = gg::launch_build_group_table(plan->d_lens, plan->d_offs, plan->group_num,
-                                                    plan->total_m, plan->args.n_tiles,
-                                                    plan->d_groups, plan->d_header, s);
+                                                    plan->in_rows, plan->args.n_tiles,
+                                                    plan->d_groups, plan->d_header, s,
+                                                    plan->args.m_out);
         if (e != hipSuccess)
             return hip_fail(e, "group table launch");
         e = gg::launch_grouped_gemm(plan->args, plan->dtype == GG_DTYPE_FP16, plan->grid, s, plan->mode);

@@ -76,10 +76,11 @@ hipError_t launch_split_reduce(const KernelArgs &args, bool fp16, hipStream_t st
 
 // Build the group table on the device from device-resident group sizes: lens[group_num]
 // (int64 rows) and offs[group_num + 1] (int64 first rows) or null for back-to-back groups.
-// Groups outside [0, total_m) get no tiles and are reported in the header. One wave.
+// Groups outside [0, total_m) get no rows (forward / dgrad: no tiles) and are reported in the
+// header. out_rows > 0 (wgrad): every group owns ceil(out_rows / 256) * n_tiles tiles. One wave.
 hipError_t launch_build_group_table(const int64_t *lens, const int64_t *offs, int group_num,
                                     int64_t total_m, int n_tiles, GroupEntry *table,
-                                    TableHeader *header, hipStream_t stream);
+                                    TableHeader *header, hipStream_t stream, int out_rows = 0);
 
 // offs[0] = 0, offs[g + 1] = offs[g] + lens[g]: group offsets from device lengths. One wave.
 hipError_t launch_group_offsets(const int64_t *lens, int64_t *offs, int group_num, hipStream_t stream);

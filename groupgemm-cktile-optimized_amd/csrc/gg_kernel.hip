@@ -1171,7 +1171,7 @@ __device__ __forceinline__ int64_t wave_inclusive_sum(int64_t v, int lane) {
 
 __global__ void __launch_bounds__(64)
 build_group_table_kernel(const int64_t *lens, const int64_t *offs, int group_num, int64_t total_m,
-                         int n_tiles, GroupEntry *table, TableHeader *header) {
+                         int n_tiles, GroupEntry *table, TableHeader *header, int out_rows) {
     const int lane      = threadIdx.x;
     int64_t   row_carry = 0, tile_carry = 0;
     int       first_bad = -1;
@@ -1185,7 +1185,10 @@ build_group_table_kernel(const int64_t *lens, const int64_t *offs, int group_num
         const int64_t rows_incl = wave_inclusive_sum(m, lane);
         const int64_t row0      = offs != nullptr ? (live ? offs[g] : 0) : row_carry + rows_incl - m;
         ok = ok && row0 >= 0 && row0 <= total_m && m <= total_m - row0;
-        const int64_t tiles      = ok ? cdiv(m, kTileM) * n_tiles : 0;
+        // wgrad (out_rows > 0): every group owns the tiles of its out_rows x N output, zero
+        // for a group without rows or with sizes that do not fit
+        const int64_t tiles      = out_rows > 0 ? (live ? cdiv(out_rows, kTileM) * n_tiles : 0)
+                                                : (ok ? cdiv(m, kTileM) * n_tiles : 0);
         const int64_t tiles_incl = wave_inclusive_sum(tiles, lane);
         if (live) {
             GroupEntry e;
@@ -1336,9 +1339,9 @@ hipError_t launch_split_reduce(const KernelArgs &args, bool fp16, hipStream_t st
 
 hipError_t launch_build_group_table(const int64_t *lens, const int64_t *offs, int group_num,
                                     int64_t total_m, int n_tiles, GroupEntry *table,
-                                    TableHeader *header, hipStream_t stream) {
+                                    TableHeader *header, hipStream_t stream, int out_rows) {
     hipLaunchKernelGGL(build_group_table_kernel, dim3(1), dim3(64), 0, stream, lens, offs,
-                       group_num, total_m, n_tiles, table, header);
+                       group_num, total_m, n_tiles, table, header, out_rows);
     return hipGetLastError();
 }
 

@@ -157,6 +157,32 @@ int gg_prepare_device_lens(int dtype, int group_num, int64_t total_m, int64_t n,
                            const int64_t *group_lens, const int64_t *group_offs, const void *x,
                            const void *w, void *out, void *stream, gg_plan **plan_out);
 
+/* Passes of gg_prepare_device_lens_op. */
+typedef enum gg_op {
+    GG_OP_FORWARD = 0, /* out = x @ w[g]^T: a = x [total_m, k], b = w [group_num, n, k], out [total_m, n] */
+    GG_OP_DGRAD   = 1, /* grad_x = grad_out @ w[g]: a = grad_out [total_m, n], b = w, out [total_m, k] */
+    GG_OP_WGRAD   = 2  /* grad_w[g] = grad_out[g]^T @ x[g]: a = grad_out [total_m, n], b = x [total_m, k],
+                          out [group_num, n, k] (zero for a group without rows) */
+} gg_op;
+
+/*
+ * Device-resident group sizes for every pass and input type: gg_prepare_device_lens's contract
+ * (group_lens / group_offs in device memory, re-read by every gg_run, sizes that do not fit
+ * reported by gg_plan_device_status) for the forward, dgrad and wgrad GEMMs, with 16-bit or fp8
+ * inputs. a_dtype / b_dtype: equal GG_DTYPE_BF16 / GG_DTYPE_FP16, or fp8 (both e4m3, both e5m2,
+ * or for dgrad / wgrad an e5m2 a with an e4m3 b), then out is bf16 scaled by a_scale[0] *
+ * b_scale[g] (device floats; NULL for 16-bit types). Primus-Turbo passes group_lens_ptr /
+ * group_offs_ptr to each of its grouped GEMMs (third_party/primus_turbo/include/primus_turbo/
+ * grouped_gemm.h:35-36, 95-96, 112-130). total_m: rows of the row-indexed operands. The
+ * requirements of the matching host-size entry point apply; wgrad's 2 GiB rule counts all
+ * total_m rows, since any group may hold them all. wgrad always runs the per-tile variant here
+ * (its K-step counts are not known on the host).
+ */
+int gg_prepare_device_lens_op(int op, int a_dtype, int b_dtype, int group_num, int64_t total_m, int64_t n,
+                              int64_t k, const int64_t *group_lens, const int64_t *group_offs, const void *a,
+                              const void *b, const float *a_scale, const float *b_scale, void *out,
+                              void *stream, gg_plan **plan_out);
+
 /*
  * Device-side size check of the last gg_run of a gg_prepare_device_lens plan, read back with a
  * synchronization of `stream`: GG_OK, or GG_ERR_INVALID naming the first group whose length or

@@ -225,3 +225,150 @@ def test_compute_group_offs(pkg, b):
     torch.cuda.synchronize(DEV)
     want = torch.cat([torch.zeros(1, dtype=torch.int64), torch.cumsum(lens, 0)])
     assert torch.equal(offs.cpu(), want)
+
+
+# ---- every pass over device sizes (gg_prepare_device_lens_op) --------------------------------
+TDT8 = {0: torch.float8_e4m3fn, 1: torch.float8_e5m2}
+
+
+def _dt8(pkg, f):
+    return pkg.DType.FP8_E4M3 if f == 0 else pkg.DType.FP8_E5M2
+
+
+def _host_backward(pkg, kind, fmts, gm, n, k, go, other, gs=None, os_=None):
+    """Output of the host-size backward plan, split-K off, NaN where unwritten."""
+    shape = (go.shape[0], k) if kind == "dgrad" else (len(gm), n, k)
+    odt = torch.bfloat16 if fmts is not None else go.dtype
+    out = torch.full(shape, float("nan"), dtype=odt, device=DEV)
+    old = os.environ.get("GG_SPLIT_K")
+    os.environ["GG_SPLIT_K"] = "1"
+    try:
+        if fmts is None:
+            dt = pkg.DType.BF16 if go.dtype == torch.bfloat16 else pkg.DType.FP16
+            plan = pkg.BackwardPlan(kind, dt, n, k, gm, go.data_ptr(), other.data_ptr(), out.data_ptr(), _stream())
+        else:
+            plan = pkg.BackwardPlan(kind, _dt8(pkg, fmts[0]), n, k, gm, go.data_ptr(), other.data_ptr(),
+                                    out.data_ptr(), _stream(), other_dtype=_dt8(pkg, fmts[1]),
+                                    grad_scale=gs.data_ptr(), other_scale=os_.data_ptr())
+    finally:
+        if old is None:
+            del os.environ["GG_SPLIT_K"]
+        else:
+            os.environ["GG_SPLIT_K"] = old
+    plan.run(_stream())
+    torch.cuda.synchronize(DEV)
+    plan.release()
+    return out
+
+
+BWD_CASES = [
+    ("dgrad", None, [300, 0, 17, 513], 272, 528),
+    ("wgrad", None, [300, 0, 17, 513], 272, 528),
+    ("dgrad", None, [1000, 2000, 1100], 1024, 2048),   # more tiles than workgroups (cross-tile)
+    ("wgrad", None, [600, 1000, 513, 1400], 1024, 2304),
+    ("dgrad", (1, 0), [300, 0, 17, 513], 272, 528),
+    ("wgrad", (1, 0), [600, 0, 513, 1400], 1024, 2304),
+    ("dgrad", (0, 0), [1000, 2000, 1100], 1024, 2048),
+]
+
+
+@pytest.mark.parametrize("case", range(len(BWD_CASES)))
+def test_device_sizes_backward_match_host_sizes(pkg, case):
+    """dgrad / wgrad (16-bit and fp8) with device group sizes give the bits of the host-size
+    plan on the same inputs; wgrad of an empty group is zero."""
+    kind, fmts, gm, n, k = BWD_CASES[case]
+    print(f"[device-lens] backward {case}: {kind} formats={fmts} group_m={gm} N={n} K={k}", flush=True)
+    rows = sum(gm)
+    gen = torch.Generator().manual_seed(40 + case)
+    if fmts is None:
+        go = torch.randn((rows, n), generator=gen).to(torch.bfloat16).to(DEV)
+        other = torch.randn((len(gm), n, k) if kind == "dgrad" else (rows, k), generator=gen).to(torch.bfloat16).to(DEV)
+        gs = os_ = None
+        adt = bdt = pkg.DType.BF16
+    else:
+        go = torch.randn((rows, n), generator=gen).to(TDT8[fmts[0]]).to(DEV)
+        other = torch.randn((len(gm), n, k) if kind == "dgrad" else (rows, k), generator=gen).to(TDT8[fmts[1]]).to(DEV)
+        gs = torch.tensor([0.5], device=DEV)
+        os_ = torch.tensor([0.25 * (g + 1) for g in range(len(gm))], device=DEV)
+        adt, bdt = _dt8(pkg, fmts[0]), _dt8(pkg, fmts[1])
+    shape = (rows, k) if kind == "dgrad" else (len(gm), n, k)
+    out = torch.full(shape, float("nan"), dtype=torch.bfloat16, device=DEV)
+    lens = torch.tensor(gm, dtype=torch.int64, device=DEV)
+    plan = pkg.DeviceLensPlan(pkg.OP_DGRAD if kind == "dgrad" else pkg.OP_WGRAD, adt, bdt, len(gm), rows, n, k,
+                              lens.data_ptr(), 0, go.data_ptr(), other.data_ptr(), out.data_ptr(), _stream(),
+                              gs.data_ptr() if gs is not None else 0, os_.data_ptr() if os_ is not None else 0)
+    plan.run(_stream())
+    st, _, msg = plan.status(_stream())
+    detail = plan.detail()
+    plan.release()
+    assert st == pkg.GG_OK, msg
+    host = _host_backward(pkg, kind, fmts, gm, n, k, go, other, gs, os_)
+    assert torch.equal(out.view(torch.int16), host.view(torch.int16)), f"bits differ from host plan ({detail})"
+    if kind == "wgrad":
+        for g, m in enumerate(gm):
+            if m == 0:
+                assert torch.count_nonzero(out[g].float()) == 0
+
+
+def test_device_sizes_fp8_forward(pkg):
+    """The fp8 forward over device sizes gives the bits of the host-size fp8 plan."""
+    gm, n, k = [700, 0, 1324, 513], 776, 1040
+    gen = torch.Generator().manual_seed(50)
+    x = torch.randn((sum(gm), k), generator=gen).to(torch.float8_e4m3fn).to(DEV)
+    w = torch.randn((len(gm), n, k), generator=gen).to(torch.float8_e4m3fn).to(DEV)
+    xs = torch.tensor([1.5], device=DEV)
+    ws = torch.tensor([0.5, 1.0, 2.0, 0.25], device=DEV)
+    out = torch.full((sum(gm), n), float("nan"), dtype=torch.bfloat16, device=DEV)
+    lens = torch.tensor(gm, dtype=torch.int64, device=DEV)
+    plan = pkg.DeviceLensPlan(pkg.OP_FORWARD, pkg.DType.FP8_E4M3, pkg.DType.FP8_E4M3, len(gm), sum(gm), n, k,
+                              lens.data_ptr(), 0, x.data_ptr(), w.data_ptr(), out.data_ptr(), _stream(),
+                              xs.data_ptr(), ws.data_ptr())
+    plan.run(_stream())
+    st, _, msg = plan.status(_stream())
+    plan.release()
+    assert st == pkg.GG_OK, msg
+    host = torch.full_like(out, float("nan"))
+    old = os.environ.get("GG_SPLIT_K")
+    os.environ["GG_SPLIT_K"] = "1"
+    try:
+        hp = pkg.Fp8Plan(pkg.DType.FP8_E4M3, n, k, gm, x.data_ptr(), w.data_ptr(), xs.data_ptr(), ws.data_ptr(),
+                         host.data_ptr(), _stream())
+    finally:
+        if old is None:
+            del os.environ["GG_SPLIT_K"]
+        else:
+            os.environ["GG_SPLIT_K"] = old
+    hp.run(_stream())
+    torch.cuda.synchronize(DEV)
+    hp.release()
+    assert torch.equal(out.view(torch.int16), host.view(torch.int16))
+
+
+def test_device_sizes_backward_bad_sizes_and_wrappers(pkg):
+    """A negative length is reported and its group computes nothing (wgrad: zero output); the
+    torch wrappers take device sizes."""
+    gm, n, k = [300, 500, 200], 512, 256
+    go = _inputs(pkg, 0, sum(gm), 1, n, n)[0][:, :n].contiguous()
+    x = _inputs(pkg, 0, sum(gm), 1, k, k, seed_x=7)[0][:, :k].contiguous()
+    bad = torch.tensor([300, -5, 200], dtype=torch.int64, device=DEV)
+    out = torch.full((3, n, k), float("nan"), dtype=torch.bfloat16, device=DEV)
+    plan = pkg.DeviceLensPlan(pkg.OP_WGRAD, pkg.DType.BF16, pkg.DType.BF16, 3, sum(gm), n, k, bad.data_ptr(), 0,
+                              go.data_ptr(), x.data_ptr(), out.data_ptr(), _stream())
+    plan.run(_stream())
+    st, _, msg = plan.status(_stream())
+    plan.release()
+    assert st == pkg.GG_ERR_INVALID and "group 1" in msg, msg
+    assert torch.count_nonzero(out[1].float()) == 0
+    ref = go[:300].float().t().contiguous() @ x[:300].float()
+    assert ((out[0].float() - ref).abs() <= ATOL + RTOL * ref.abs()).all()
+    # wrappers with device sizes
+    lens = torch.tensor(gm, dtype=torch.int64, device=DEV)
+    gw = pkg.grouped_gemm_wgrad(go, x, lens)
+    ref = go[800:].float().t().contiguous() @ x[800:].float()
+    assert ((gw[2].float() - ref).abs() <= ATOL + RTOL * ref.abs()).all()
+    w = _inputs(pkg, 0, 1, 3, n, k)[1]  # [3, n, k]
+    gx = pkg.grouped_gemm_dgrad(go, w, lens)
+    ref = go[300:800].float() @ w[1].float()
+    assert ((gx[300:800].float() - ref).abs() <= ATOL + RTOL * ref.abs()).all()
+    with pytest.raises(pkg.GGError):
+        pkg.grouped_gemm_dgrad(go, w, torch.tensor([300, 500, 900], dtype=torch.int64, device=DEV))
