@@ -17,6 +17,12 @@ Prints ONE JSON line on stdout. Besides the driver's fields it carries:
                (profiles/hbm_traffic_<workload>.json) when present, else null.
   cpu_baseline the CPU oracle (OpenMP fp32, test infrastructure) timed on a bounded sample
                of the same workload on this host; a reported baseline only.
+  clock_power  gfx clock (MHz) and socket power (W) sampled through amdsmi during a separate
+               sustained window of the same launches after the timed region (--power-seconds,
+               default 1 s; the timed region itself runs without a sampling thread), its own
+               TFLOPS, and the dense peak scaled to the sampled clock. The MI355X is power-capped,
+               so the clock under a sustained GEMM sits well below 2.4 GHz; the reference records
+               the same two figures (scripts/power.py:1-9).
 Human-readable progress goes to stderr.
 """
 from __future__ import annotations
@@ -149,6 +155,43 @@ def other_pass(pkg, op, dtype, b, m, n, k, sh, dev):
     return plan, plan.flop, keep
 
 
+def peak_of(op):
+    return FP8_PEAK_TFLOPS if "fp8" in op else MFMA_PEAK_TFLOPS
+
+
+def sustained_clock_power(be, sh, stream, flops, ms, seconds, peak):
+    """Run the same launch back to back for about `seconds` while a background thread samples
+    the gfx clock and socket power (amdsmi). Returns the samples' means, this window's TFLOPS and
+    the dense peak scaled to the sampled clock (peak x MHz / 2400)."""
+    import torch
+
+    power = entry.load_submodule("power")
+    sampler = power.PowerSampler(0)
+    n = max(1, int(seconds / max(ms * 1e-3, 1e-6)))
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    with sampler:
+        t0.record(stream)
+        for _ in range(n):
+            be.run(sh)
+        t1.record(stream)
+        torch.cuda.synchronize()
+    sampler.close()
+    res = sampler.summary()
+    w_ms = t0.elapsed_time(t1)
+    res["steps"] = n
+    res["seconds"] = round(w_ms * 1e-3, 3)
+    res["tflops"] = round(flops * n / (w_ms * 1e-3) / 1e12, 2)
+    res["power_cap_w"] = sampler.power_cap_w
+    mhz = res.get("gfx_mhz")
+    if mhz:
+        at_clk = peak * mhz / 2400.0
+        res["peak_at_clock_tflops"] = round(at_clk, 1)
+        res["frac_at_clock"] = round(res["tflops"] / at_clk, 4)
+    res["source"] = "amdsmi: clock_info(GFX).clk, power_info.current_socket_power"
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -159,6 +202,9 @@ def main():
                     help="pass to time (fwd is the headline; the others print no cpu_baseline)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--power-seconds", type=float, default=1.0,
+                    help="sustained window sampled for clock and power after the timed region "
+                         "(0: skip)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="only run 3 device copies of BYTES bytes (reference kernel for the "
                          "FETCH_SIZE / WRITE_SIZE scale factors) and exit")
@@ -219,6 +265,12 @@ def main():
     tflops = flops / (ms * 1e-3) / 1e12
     log(f"[bench] {args.steps} steps, {ms:.4f} ms/step, {tflops:.1f} TFLOPS")
 
+    clock_power = None
+    if args.power_seconds > 0:
+        clock_power = sustained_clock_power(be, sh, stream, flops, ms, args.power_seconds, peak_of(args.op))
+        log(f"[bench] sustained {clock_power.get('seconds')} s: {clock_power.get('tflops')} TFLOPS at "
+            f"{clock_power.get('gfx_mhz')} MHz, {clock_power.get('socket_w')} W")
+
     traffic = None
     suffix = "" if args.op == "fwd" else f"_{args.op}"
     tpath = os.path.join(ROOT, "profiles", f"hbm_traffic_{args.workload}{suffix}.json")
@@ -234,7 +286,7 @@ def main():
     be.release()
 
     fp8 = "fp8" in args.op
-    peak = FP8_PEAK_TFLOPS if fp8 else MFMA_PEAK_TFLOPS
+    peak = peak_of(args.op)
     metric = "grouped-GEMM TFLOPS (bf16) + % of MFMA peak, 1 MI355X, per config"
     if args.op != "fwd":
         metric = f"grouped-GEMM {args.op} TFLOPS + % of MFMA peak, 1 MI355X"
@@ -259,6 +311,7 @@ def main():
                      "unit": "TFLOP/s", "frac": round(tflops / peak, 4),
                      "traffic": traffic},
         "cpu_baseline": cpu,
+        "clock_power": clock_power,
     }
     print(json.dumps(line), flush=True)
 

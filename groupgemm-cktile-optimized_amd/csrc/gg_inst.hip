@@ -1,0 +1,53 @@
+// One instance unit of the persistent grouped GEMM: the (input type, mode) pair GG_PART selects,
+// both variants (cross-tile and per-tile). The Makefile compiles this file once per part, in
+// parallel; gg_kernel.hip's dispatch calls launch_mode of every part.
+#include "gg_kernel_impl.h"
+
+#ifndef GG_PART
+#error "GG_PART selects the instance (0-13)"
+#endif
+
+namespace gg {
+
+template <bool F16, int MODE>
+void launch_mode(const KernelArgs &args, bool cross, dim3 g, dim3 b, hipStream_t stream) {
+    if (cross)
+        hipLaunchKernelGGL((grouped_gemm_kernel<F16, true, MODE>), g, b, 0, stream, args);
+    else
+        hipLaunchKernelGGL((grouped_gemm_kernel<F16, false, MODE>), g, b, 0, stream, args);
+}
+
+// part -> (fp16 MFMA, mode); the dispatch's switch in gg_kernel.hip covers the same 14 pairs
+#if GG_PART == 0
+template void launch_mode<false, make_mode(kFwd, kIn16)>(const KernelArgs &, bool, dim3, dim3, hipStream_t);
+#elif GG_PART == 1
+template void launch_mode<true, make_mode(kFwd, kIn16)>(const KernelArgs &, bool, dim3, dim3, hipStream_t);
+#elif GG_PART == 2
+template void launch_mode<false, make_mode(kDgrad, kIn16)>(const KernelArgs &, bool, dim3, dim3, hipStream_t);
+#elif GG_PART == 3
+template void launch_mode<true, make_mode(kDgrad, kIn16)>(const KernelArgs &, bool, dim3, dim3, hipStream_t);
+#elif GG_PART == 4
+template void launch_mode<false, make_mode(kWgrad, kIn16)>(const KernelArgs &, bool, dim3, dim3, hipStream_t);
+#elif GG_PART == 5
+template void launch_mode<true, make_mode(kWgrad, kIn16)>(const KernelArgs &, bool, dim3, dim3, hipStream_t);
+#elif GG_PART == 6
+template void launch_mode<false, make_mode(kFwd, kInE4M3)>(const KernelArgs &, bool, dim3, dim3, hipStream_t);
+#elif GG_PART == 7
+template void launch_mode<false, make_mode(kFwd, kInE5M2)>(const KernelArgs &, bool, dim3, dim3, hipStream_t);
+#elif GG_PART == 8
+template void launch_mode<false, make_mode(kDgrad, kInE4M3)>(const KernelArgs &, bool, dim3, dim3, hipStream_t);
+#elif GG_PART == 9
+template void launch_mode<false, make_mode(kDgrad, kInE5M2)>(const KernelArgs &, bool, dim3, dim3, hipStream_t);
+#elif GG_PART == 10
+template void launch_mode<false, make_mode(kDgrad, kInE5M2xE4M3)>(const KernelArgs &, bool, dim3, dim3, hipStream_t);
+#elif GG_PART == 11
+template void launch_mode<false, make_mode(kWgrad, kInE4M3)>(const KernelArgs &, bool, dim3, dim3, hipStream_t);
+#elif GG_PART == 12
+template void launch_mode<false, make_mode(kWgrad, kInE5M2)>(const KernelArgs &, bool, dim3, dim3, hipStream_t);
+#elif GG_PART == 13
+template void launch_mode<false, make_mode(kWgrad, kInE5M2xE4M3)>(const KernelArgs &, bool, dim3, dim3, hipStream_t);
+#else
+#error "GG_PART out of range"
+#endif
+
+} // namespace gg

@@ -62,6 +62,11 @@ struct TableHeader {
 // K steps) rather than a prologue and an LDS-staged epilogue per tile.
 bool uses_cross_tile(const KernelArgs &args, int grid, int mode = 0);
 
+// Launch of one kernel instance (cross-tile or per-tile variant), defined and explicitly
+// instantiated in the instance units (gg_inst.hip, one (F16, MODE) pair per unit).
+template <bool F16, int MODE>
+void launch_mode(const KernelArgs &args, bool cross, dim3 g, dim3 b, hipStream_t stream);
+
 // Enqueue the persistent grouped GEMM: `grid` workgroups of 256 threads on `stream`.
 // fp16 selects the f16 MFMA, otherwise bf16 (16-bit formats); mode = make_mode(layout, format)
 // (fp8 formats write bf16, fp16 must be false).

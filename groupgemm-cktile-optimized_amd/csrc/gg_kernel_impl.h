@@ -1,0 +1,1124 @@
+// Device code of the persistent grouped GEMM kernel. Included by the instance units
+// (gg_inst.hip, one (input type, mode) pair each) and by gg_kernel.hip (helper kernels and the
+// host-side dispatch).
+#pragma once
+
+// Persistent grouped GEMM for MI355X (gfx950, CDNA4): out[g] = x[g] @ w[g]^T, bf16/fp16 in,
+// fp32 accumulate, bf16/fp16 out (RNE).
+//
+// Replaces the reference's hot path: CK's persistent GroupedGemmKernel tile loop, the
+// hand-scheduled HandPipelineAsmS main loop and FastEpilogue
+// (ck_kernel/ck_grouped_gemm.cpp:97, hand_pipeline_asm_s.hpp:155-357, fast_epilogue.hpp:29-118).
+// Written directly against gfx950: no CK headers, no portability layers.
+//
+// Work decomposition
+//   * Output tile 256 x 256, K step 64. One workgroup = 4 waves, one per SIMD; wave (wm, wn)
+//     owns the 128 x 128 sub-tile rows wm*128.., cols wn*128.. as 8 x 8 MFMA tiles of 16 x 16.
+//   * v_mfma_f32_16x16x32_{bf16,f16}. The w fragment is the first source and the x fragment
+//     the second, so each 16 x 16 accumulator holds C^T: lane l has row l%16 of the block and
+//     the four consecutive columns 4*(l/16)..+3, i.e. 8 contiguous output bytes.
+//   * All 256 accumulators per lane live in AGPRs (inline-asm MFMAs with "a" operands);
+//     fragments, offsets and addresses use the 256 arch VGPRs.
+//   * grid = min(#CUs, #tiles) persistent workgroups walking the tile list of all groups
+//     (gg_schedule.h: banded in-group order + XCD remap).
+//   * Two variants: cross-tile (a workgroup's tiles run as one continuous K pipeline and a
+//     finished tile is stored from registers during the next tile's first step) and per-tile
+//     (prologue and LDS-staged epilogue around every tile, for one tile per workgroup).
+//
+// LDS (160 KB, all of it): A (x rows) 2 stages + B (w rows) 3 stages of 256 rows x 128 B.
+// Row r keeps its 16-byte chunk c at chunk position c ^ (r % 8): the eight lanes that a
+// ds_read_b128 serves together (8 consecutive rows, same chunk) hit eight different 16-byte
+// slots of a 128-byte window, which is conflict-free on gfx950.
+// Global -> LDS copies use buffer_load_dwordx4 ... lds (no VGPR staging): one instruction
+// moves 64 lanes x 16 B = 8 rows; lane l fetches logical chunk (l%8) ^ (l/8) of row l/8 so
+// that the fixed lane -> LDS mapping (M0 + 16 l) realises the swizzle.
+//
+// K-step schedule (one "iteration" kt, 8 rows of 16 MFMAs per wave, see the plan_* table):
+//   * x fragments are read one row ahead (2-row register ring); w fragments of step kt+1
+//     are pre-read during step kt into the second half of a double-buffered register set.
+//   * DMA: A(kt+1) in rows 0-2 (its first two loads were issued at the end of step kt-1),
+//     B(kt+3) in rows 3-6, the first two loads of A(kt+2) at the end of row 7.
+//   * One barrier per step, in row 7: after it A(kt+1) is complete in LDS, every wave is done
+//     with A(kt) and with B(kt+1)'s LDS copy, so their stages can be refilled.
+//   * Buffer resources are bounded by the tile's valid rows: rows past M or N read zeros and
+//     are never stored. Prefetches past the last K step use a zero-length resource (no
+//     traffic, the DMA writes zeros) so the DMA count, and every vmcnt, stays static.
+//     K % 64 != 0: the last K step's out-of-range 16-byte chunks get an out-of-range offset.
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+#include <type_traits>
+
+#include "gg_kernel.h"
+
+#pragma clang diagnostic ignored "-Winline-asm"
+
+namespace gg {
+namespace {
+
+typedef int      i32x2 __attribute__((ext_vector_type(2)));
+typedef int      i32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef float    f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16   bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kThreads  = 256;
+constexpr int kWaves    = kThreads / 64;
+constexpr int kRowBytes = kTileK * 2;           // 128: one K step of one operand row
+constexpr int kOpBytes  = kTileM * kRowBytes;   // 32 KB: one K step of one operand tile
+static_assert(kTileM == kTileN, "x and w tiles share one load layout");
+constexpr int kAStages  = 2;
+constexpr int kBStages  = 3;
+constexpr int kLdsBytes = (kAStages + kBStages) * kOpBytes; // 163840 = all of gfx950's LDS
+constexpr int kLoads    = kOpBytes / 1024 / kWaves;         // 1 KB DMAs per wave per operand step
+// Slot-plan knobs (compile-time; the defaults are the tuned plan).
+#ifndef GG_EARLY_A
+#define GG_EARLY_A 2 // DMAs of A(kt+2) issued at the end of step kt
+#endif
+#ifndef GG_A_PER_ROW
+#define GG_A_PER_ROW 2 // A(kt+1) DMAs per row: 2 (after MFMAs 0, 8) or 4 (0, 4, 8, 12)
+#endif
+#ifndef GG_B_ROW0
+#define GG_B_ROW0 3 // B(kt+3) DMAs: two per row in rows GG_B_ROW0 .. +3
+#endif
+#ifndef GG_B_SLOT0
+#define GG_B_SLOT0 0 // ... after MFMAs GG_B_SLOT0 and GG_B_SLOT0 + 8
+#endif
+#ifndef GG_BAR_IDX
+#define GG_BAR_IDX 7 // the step's barrier follows this MFMA of row 7
+#endif
+#ifndef GG_M0_AHEAD
+#define GG_M0_AHEAD 1 // write M0 for a DMA before the MFMA of its slot (1) or next to it (0)
+#endif
+#ifndef GG_ROW0_AT_BAR
+#define GG_ROW0_AT_BAR 1 // next step's row-0 x fragments right after the barrier (1) or 2 slots later (0)
+#endif
+#ifndef GG_STAGE_BASES
+#define GG_STAGE_BASES 1 // per-stage LDS base registers so every read uses the 16-bit offset field
+#endif
+#ifndef GG_DMA_CPOL_ID
+#define GG_DMA_CPOL_ID 0 // cache-policy modifiers of the operand DMAs: see GG_DMA_CPOL
+#endif
+#if GG_DMA_CPOL_ID == 0
+#define GG_DMA_CPOL ""
+#elif GG_DMA_CPOL_ID == 1
+#define GG_DMA_CPOL "nt"
+#elif GG_DMA_CPOL_ID == 2
+#define GG_DMA_CPOL "sc0"
+#elif GG_DMA_CPOL_ID == 3
+#define GG_DMA_CPOL "sc1"
+#elif GG_DMA_CPOL_ID == 4
+#define GG_DMA_CPOL "sc0 sc1"
+#elif GG_DMA_CPOL_ID == 5
+#define GG_DMA_CPOL "sc1 nt"
+#endif
+constexpr int kEarlyA   = GG_EARLY_A;
+constexpr int kCStride  = kTileN * 2 + 16;                  // staged C row stride (528 B)
+static_assert(kLoads == 8 && kEarlyA >= 0 && kEarlyA <= 4, "slot plan written for 8 DMAs per operand");
+static_assert(kTileM * kCStride <= kLdsBytes, "the staged C tile must fit in LDS");
+
+constexpr int a_stage(int s) { return s * kOpBytes; }
+constexpr int b_stage(int s) { return (kAStages + s) * kOpBytes; }
+
+// ---------------------------------------------------------------------------------------
+// Operand layouts. K-major: the contraction index runs along each stored row (x and w of the
+// forward op, grad_out of dgrad); a 16-row fragment k-half is one ds_read_b128. MN-major: the
+// contraction index is the stored row index (w of dgrad, grad_out and x of wgrad); a fragment
+// k-half is two ds_read_b64_tr_b16, each giving 4 consecutive contraction values per lane
+// (fp8: a fragment is four ds_read_b64_tr_b8 of 8 values).
+// A kernel mode is a layout plus an input format: mode = layout + 4 * format (gg_kernel.h).
+//   layout kFwd:   out[g] = x[g] @ w[g]^T                     A = x (K-major),  B = w (K-major)
+//   layout kDgrad: grad_x[g] = grad_out[g] @ w[g]             A = grad_out (K), B = w (MN)
+//   layout kWgrad: grad_w[g] = grad_out[g]^T @ x[g], K = M_g  A = grad_out (MN), B = x (MN)
+//   format kIn16 (bf16 / fp16), kInE4M3, kInE5M2 (both operands), kInE5M2xE4M3 (A e5m2, B
+//   e4m3); fp8 formats write bf16 out = (A B^T) * a_scale * b_scale[g].
+// ---------------------------------------------------------------------------------------
+constexpr int  mode_layout(int m) { return m & 3; }
+constexpr int  mode_fmt(int m) { return m >> 2; }
+constexpr bool mode_f8(int m) { return mode_fmt(m) != kIn16; }
+constexpr bool mode_a_e5(int m) { return mode_fmt(m) == kInE5M2 || mode_fmt(m) == kInE5M2xE4M3; }
+constexpr bool mode_b_e5(int m) { return mode_fmt(m) == kInE5M2; }
+constexpr bool mode_a_mn(int m) { return mode_layout(m) == kWgrad; }
+constexpr bool mode_b_mn(int m) { return mode_layout(m) == kDgrad || mode_layout(m) == kWgrad; }
+// LDS reads of one 16-row fragment over both k-halves.
+constexpr int reads_per_frag(bool mn) { return mn ? 4 : 2; }
+
+// ---------------------------------------------------------------------------------------
+// Slot plan of one K step. Row mi (0..7) issues 16 MFMAs, idx = kh * 8 + ni; each function
+// says which memory operation follows MFMA idx of row mi (-1: none). LDS reads sit after odd
+// MFMAs, DMAs after even ones, so no MFMA gap holds more than one memory operation.
+// NA / NB: LDS reads per fragment of A / B (2 K-major, 4 MN-major); a read op index r is the
+// k-half (K-major) or k-half * 2 + half (MN-major).
+// ---------------------------------------------------------------------------------------
+constexpr int kBarRow = 7; // the step's barrier follows MFMA Plan::bar of this row
+static_assert(GG_BAR_IDX >= 5 && GG_BAR_IDX <= 11 && GG_BAR_IDX % 2 == 1, "barrier slot");
+
+constexpr int plan_epi(int mi, int idx);
+template <int NA, int NB> struct Plan {
+    static constexpr int slots = 16, early = kEarlyA;
+    static constexpr int epi(int mi, int idx) { return plan_epi(mi, idx); }
+    // The w fragments of row 7 are read before the barrier, at MFMAs 1 .. 2 NB - 1.
+    static constexpr int bar = GG_BAR_IDX > 2 * NB + 1 ? GG_BAR_IDX : 2 * NB + 1;
+    static constexpr int row0_first = GG_ROW0_AT_BAR ? bar : bar + 2;
+    static_assert(row0_first + 2 * (NA - 1) <= 15, "row-0 reads fit in row 7");
+
+    // x fragments of row mi+1 into the register ring: the first NA odd slots of rows 0-6.
+    static constexpr int read_a_next(int mi, int idx) {
+        return (mi < 7 && idx % 2 == 1 && idx < 2 * NA) ? idx / 2 : -1;
+    }
+    // w fragments of step kt+1, column block ni = mi: the next NB odd slots of rows 0-6; in
+    // row 7 the first NB odd slots, so they are complete before the barrier.
+    static constexpr int read_b_next(int mi, int idx) {
+        if (idx % 2 == 0)
+            return -1;
+        if (mi < 7)
+            return (idx >= 2 * NA && idx < 2 * (NA + NB)) ? (idx - 2 * NA) / 2 : -1;
+        return idx < 2 * NB ? idx / 2 : -1;
+    }
+    // x fragments of row 0 of step kt+1, right after the barrier.
+    static constexpr int read_a_row0(int mi, int idx) {
+        return (mi == 7 && idx % 2 == 1 && idx >= row0_first && idx < row0_first + 2 * NA)
+                   ? (idx - row0_first) / 2
+                   : -1;
+    }
+    // DMA j of A(kt+1), j = kEarlyA..7: GG_A_PER_ROW per row from row 0.
+    static constexpr int load_a(int mi, int idx) {
+        constexpr int per = GG_A_PER_ROW, step = 16 / per;
+        if (idx % step != 0)
+            return -1;
+        const int j = kEarlyA + mi * per + idx / step;
+        return j < kLoads ? j : -1;
+    }
+    // DMA j of B(kt+3): two per row in rows GG_B_ROW0 .. +3.
+    static constexpr int load_b(int mi, int idx) {
+        return (mi >= GG_B_ROW0 && mi < GG_B_ROW0 + 4 && (idx == GG_B_SLOT0 || idx == GG_B_SLOT0 + 8))
+                   ? (mi - GG_B_ROW0) * 2 + (idx - GG_B_SLOT0) / 8
+                   : -1;
+    }
+    // DMA j < kEarlyA of A(kt+2): the first even slots of row 7 after the barrier (A(kt)'s
+    // stage is free once every wave passed it).
+    static constexpr int load_a_early(int mi, int idx) {
+        const int j = (idx - (bar + 1)) / 2;
+        return (mi == 7 && idx > bar && idx % 2 == 0 && j < kEarlyA) ? j : -1;
+    }
+    // The DMA that follows MFMA idx of row mi: 0 none, 1 A(kt+1), 2 B(kt+3), 3 A(kt+2).
+    static constexpr int dma_kind(int mi, int idx) {
+        return load_a(mi, idx) >= 0 ? 1 : load_b(mi, idx) >= 0 ? 2 : load_a_early(mi, idx) >= 0 ? 3 : 0;
+    }
+    static constexpr int dma_j(int mi, int idx) {
+        return load_a(mi, idx) >= 0 ? load_a(mi, idx) : load_b(mi, idx) >= 0 ? load_b(mi, idx) : load_a_early(mi, idx);
+    }
+    // DMAs that may still be in flight at the barrier: those issued after the last A(kt+1)
+    // DMA. Loads complete in order, so vmcnt(this) means all of A(kt+1) (and everything older)
+    // landed. Stores are never counted here, wherever they sit in the step: a store may
+    // complete before an older load, so counting one could let the barrier pass while an
+    // A(kt+1) DMA is in flight. With loads alone counted, pending stores only make the wait
+    // longer.
+    static constexpr int vm_at_barrier() {
+        int last_a = -1;
+        for (int p = 0; p < 8 * 16; ++p)
+            if (load_a(p / 16, p % 16) >= 0)
+                last_a = p;
+        int n = 0;
+        for (int p = last_a + 1; p < kBarRow * 16 + bar; ++p)
+            n += (load_b(p / 16, p % 16) >= 0) + (load_a_early(p / 16, p % 16) >= 0);
+        return n;
+    }
+    template <typename F> static constexpr int count(F f) {
+        int n = 0;
+        for (int p = 0; p < 8 * 16; ++p)
+            n += f(p / 16, p % 16) >= 0;
+        return n;
+    }
+    static constexpr bool check() {
+        for (int p = 0; p < 8 * 16; ++p) {
+            const int mi = p / 16, idx = p % 16;
+            const int dmas  = (load_a(mi, idx) >= 0) + (load_b(mi, idx) >= 0) + (load_a_early(mi, idx) >= 0);
+            const int reads = (read_a_next(mi, idx) >= 0) + (read_b_next(mi, idx) >= 0) +
+                              (read_a_row0(mi, idx) >= 0);
+            if (dmas > 1 || reads > 1 || (dmas && reads))
+                return false;
+        }
+        return count(load_a) == kLoads - kEarlyA && count(load_b) == kLoads &&
+               count(load_a_early) == kEarlyA && count(read_b_next) == 8 * NB &&
+               count(read_a_next) == 7 * NA && count(read_a_row0) == NA;
+    }
+};
+static_assert(Plan<2, 2>::check() && Plan<2, 4>::check() && Plan<4, 4>::check(), "slot plans");
+
+// fp8 K step: 128 fp8 values per 128-byte row; v_mfma_f32_16x16x128_f8f6f4 takes 32 bytes of a
+// row per lane, so a row mi of the step is 8 MFMAs of twice the length, and a fragment is two
+// ds_read_b128 (K-major) or four ds_read_b64_tr_b8 (MN-major): NA / NB reads.
+// DMAs after MFMAs 0 and 4: A(kt+1) DMAs 1-7 in rows 0-2 and row 3 (after MFMA 2), B(kt+3) in
+// rows 3-6; the early A DMA 0 after MFMA 6 of row 7. The x reads of row mi+1 follow the odd
+// MFMAs of row mi, the w reads of step kt+1 the MFMAs left (rows 0-6) or the first MFMAs of
+// row 7, before the barrier (after MFMA 5, or 4 when row 0 of x takes four reads), and row 0 of
+// the next step's x follows the barrier. A 32-cycle fp8 MFMA leaves room for a DMA or a store
+// beside a read in one gap.
+template <int NA, int NB> struct Plan8 {
+    static_assert((NA == 2 || NA == 4) && (NB == 2 || NB == 4), "reads per fragment");
+    static constexpr int slots = 8, early = 1, bar = NA == 4 ? 4 : 5;
+    static constexpr int read_a_next(int mi, int idx) {
+        return (mi < 7 && idx % 2 == 1 && idx < 2 * NA) ? idx / 2 : -1;
+    }
+    static constexpr int read_b_next(int mi, int idx) {
+        if (mi == 7)
+            return NB == 2 ? ((idx == 1 || idx == 3) ? idx / 2 : -1) : (idx < 4 ? idx : -1);
+        if (NA == 2 && NB == 2)
+            return (idx == 5 || idx == 7) ? (idx - 5) / 2 : -1;
+        if (NA == 2)
+            return idx == 2 ? 0 : idx == 5 ? 1 : idx == 6 ? 2 : idx == 7 ? 3 : -1;
+        if (NB == 2)
+            return (idx == 2 || idx == 6) ? idx / 4 : -1;
+        return idx % 2 == 0 ? idx / 2 : -1;
+    }
+    static constexpr int read_a_row0(int mi, int idx) {
+        if (mi != 7)
+            return -1;
+        if (NA == 2)
+            return (idx == 5 || idx == 7) ? (idx - 5) / 2 : -1;
+        return idx >= 4 ? idx - 4 : -1;
+    }
+    static constexpr int load_a(int mi, int idx) {
+        if (mi < 3 && (idx == 0 || idx == 4))
+            return 1 + 2 * mi + idx / 4;
+        return (mi == 3 && idx == 2) ? 7 : -1;
+    }
+    static constexpr int load_b(int mi, int idx) {
+        return (mi >= 3 && mi < 7 && (idx == 0 || idx == 4)) ? 2 * (mi - 3) + idx / 4 : -1;
+    }
+    static constexpr int load_a_early(int mi, int idx) { return (mi == 7 && idx == 6) ? 0 : -1; }
+    // Cross-tile first step: store s of the previous tile's row block mi+1 after MFMA 2, 3, 6, 7
+    // of row mi.
+    static constexpr int epi(int mi, int idx) {
+        return mi < 7 ? (idx == 2 ? 0 : idx == 3 ? 1 : idx == 6 ? 2 : idx == 7 ? 3 : -1) : -1;
+    }
+    static constexpr int dma_kind(int mi, int idx) {
+        return load_a(mi, idx) >= 0 ? 1 : load_b(mi, idx) >= 0 ? 2 : load_a_early(mi, idx) >= 0 ? 3 : 0;
+    }
+    static constexpr int dma_j(int mi, int idx) {
+        return load_a(mi, idx) >= 0 ? load_a(mi, idx) : load_b(mi, idx) >= 0 ? load_b(mi, idx) : load_a_early(mi, idx);
+    }
+    static constexpr int vm_at_barrier() { // loads issued after A(kt+1)'s last DMA, as in Plan
+        int last_a = -1;
+        for (int p = 0; p < 8 * slots; ++p)
+            if (load_a(p / slots, p % slots) >= 0)
+                last_a = p;
+        int n = 0;
+        for (int p = last_a + 1; p < kBarRow * slots + bar; ++p)
+            n += (load_b(p / slots, p % slots) >= 0) + (load_a_early(p / slots, p % slots) >= 0);
+        return n;
+    }
+    static constexpr bool check() {
+        int na = 0, nb = 0, ne = 0, ra = 0, rb = 0, r0 = 0;
+        for (int p = 0; p < 8 * slots; ++p) {
+            const int mi = p / slots, idx = p % slots;
+            const int dmas  = (load_a(mi, idx) >= 0) + (load_b(mi, idx) >= 0) + (load_a_early(mi, idx) >= 0);
+            const int reads = (read_a_next(mi, idx) >= 0) + (read_b_next(mi, idx) >= 0) + (read_a_row0(mi, idx) >= 0);
+            if (dmas > 1 || reads > 1)
+                return false;
+            // w reads of row 7 before the barrier (reads at its slot follow it), row 0 of x after it
+            if (mi == 7 && ((read_b_next(mi, idx) >= 0 && idx >= bar) || (read_a_row0(mi, idx) >= 0 && idx < bar)))
+                return false;
+            na += load_a(mi, idx) >= 0;
+            nb += load_b(mi, idx) >= 0;
+            ne += load_a_early(mi, idx) >= 0;
+            ra += read_a_next(mi, idx) >= 0;
+            rb += read_b_next(mi, idx) >= 0;
+            r0 += read_a_row0(mi, idx) >= 0;
+        }
+        return na == kLoads - early && nb == kLoads && ne == early && ra == 7 * NA && rb == 8 * NB && r0 == NA;
+    }
+};
+static_assert(Plan8<2, 2>::check() && Plan8<2, 4>::check() && Plan8<4, 4>::check(), "fp8 slot plans");
+static_assert(Plan8<2, 2>::vm_at_barrier() == 7, "fp8 forward plan unchanged");
+static_assert(Plan<2, 2>::bar == GG_BAR_IDX, "forward plan keeps the tuned barrier slot");
+
+// ---------------------------------------------------------------------------------------
+// Device primitives
+// ---------------------------------------------------------------------------------------
+template <int N> using ic = std::integral_constant<int, N>;
+template <int B, int E, typename F> __device__ __forceinline__ void sfor(F &&f) {
+    if constexpr (B < E) {
+        f(ic<B>{});
+        sfor<B + 1, E>(static_cast<F &&>(f));
+    }
+}
+
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// Make a value look freshly produced at this point. Values derived from it are then
+// recomputed next to their uses inside the loop instead of being hoisted out of it as loop
+// invariants (which would keep dozens of precomputed addresses live across the K loop).
+__device__ __forceinline__ void fresh_v(int &v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void fresh_s(uint32_t &v) { asm volatile("" : "+s"(v)); }
+
+// Buffer resource for the LDS DMA (SGPR quad): base, stride 0, byte bound, gfx9 raw format.
+__device__ __forceinline__ i32x4 dma_rsrc(const void *p, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(p);
+    i32x4 r;
+    r[0] = static_cast<int>(static_cast<uint32_t>(a));
+    r[1] = static_cast<int>(static_cast<uint32_t>(a >> 32) & 0xffffu);
+    r[2] = static_cast<int>(bytes);
+    r[3] = 0x00020000;
+    return r;
+}
+
+// 64 lanes x 16 B from global (resource + lane offset + K-step offset) into LDS at
+// M0 + 16 * lane. The compiler cannot see this LDS write: waits are placed by hand.
+// set_m0 must precede the load by at least one instruction (SALU M0 write -> LDS DMA).
+// s_add_u32 writes SCC: the clobber keeps the compiler from holding a branch condition in SCC
+// across it.
+template <int OFF> __device__ __forceinline__ void set_m0(uint32_t lds_base) {
+    asm volatile("s_add_u32 m0, %0, %1" : : "s"(lds_base), "n"(OFF) : "memory", "scc");
+}
+// A VMEM instruction that reads an SGPR written by a VALU instruction (v_readlane_b32 of a
+// spilled SGPR, v_readfirstlane_b32, v_cmp) needs 5 wait states in between. The compiler's
+// hazard recognizer does not look inside inline asm, and under SGPR pressure it reloads a DMA's
+// soffset with v_readlane_b32 right before it (seen in the fp8 dgrad kernel's first cross-tile
+// step: the DMA then used the stale soffset and loaded the wrong K step). The DMAs of the cold
+// paths (prologue, a tile's first step, where the spilled values are reloaded) start with 5
+// wait states (NOPS = 4); those of the K loop carry none, which costs 4-5 % of throughput, and
+// the build checks the generated code for the hazard instead (csrc/check_vmem_sgpr_hazard.py).
+template <int NOPS>
+__device__ __forceinline__ void dma16_m0(int voff, const i32x4 &rsrc, int soff) {
+    if constexpr (NOPS > 0)
+        asm volatile("s_nop %3\n\t"
+                     "buffer_load_dwordx4 %0, %1, %2 offen " GG_DMA_CPOL " lds"
+                     :
+                     : "v"(voff), "s"(rsrc), "s"(soff), "n"(NOPS)
+                     : "memory");
+    else
+        asm volatile("buffer_load_dwordx4 %0, %1, %2 offen " GG_DMA_CPOL " lds"
+                     :
+                     : "v"(voff), "s"(rsrc), "s"(soff)
+                     : "memory");
+}
+__device__ __forceinline__ void dma16(uint32_t lds_dst, int voff, const i32x4 &rsrc, int soff) {
+    asm volatile("s_mov_b32 m0, %0\n\t"
+                 "s_nop 4\n\t"
+                 "buffer_load_dwordx4 %1, %2, %3 offen " GG_DMA_CPOL " lds"
+                 :
+                 : "s"(lds_dst), "v"(voff), "s"(rsrc), "s"(soff)
+                 : "memory", "m0");
+}
+
+template <int VM> __device__ __forceinline__ void wait_vm_lds_barrier() {
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(VM) : "memory");
+}
+
+template <bool F16>
+__device__ __forceinline__ void mfma(f32x4 &c, const i32x4 &a, const i32x4 &b) {
+    if constexpr (F16)
+        asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+    else
+        asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+}
+// First K half of a tile: C = 0, so the accumulators need no clearing.
+template <bool F16>
+__device__ __forceinline__ void mfma_first(f32x4 &c, const i32x4 &a, const i32x4 &b) {
+    if constexpr (F16)
+        asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, 0" : "=a"(c) : "v"(a), "v"(b));
+    else
+        asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=a"(c) : "v"(a), "v"(b));
+}
+
+// fp8 x fp8 -> fp32, 16 x 16 x 128 (gfx950): both sources are 32 bytes of a row per lane.
+// The kernel passes w (B) as src0 and x (A) as src1: cbsz gives src0's format, blgp src1's
+// (0 e4m3, 1 e5m2).
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+template <bool BE5, bool AE5, bool FIRST>
+__device__ __forceinline__ void mfma8(f32x4 &c, const i32x8 &b, const i32x8 &a) {
+#define GG_MFMA8(MODS)                                                                                    \
+    if constexpr (FIRST)                                                                                  \
+        asm volatile("v_mfma_f32_16x16x128_f8f6f4 %0, %1, %2, 0" MODS : "=a"(c) : "v"(b), "v"(a));       \
+    else                                                                                                  \
+        asm volatile("v_mfma_f32_16x16x128_f8f6f4 %0, %1, %2, %0" MODS : "+a"(c) : "v"(b), "v"(a));
+    if constexpr (BE5 && AE5) {
+        GG_MFMA8(" cbsz:1 blgp:1")
+    } else if constexpr (BE5) {
+        GG_MFMA8(" cbsz:1")
+    } else if constexpr (AE5) {
+        GG_MFMA8(" blgp:1")
+    } else {
+        GG_MFMA8("")
+    }
+#undef GG_MFMA8
+}
+
+// Four fp32 accumulators -> four 16-bit outputs (RNE), as two packed dwords.
+template <bool F16> __device__ __forceinline__ u32x2 pack4(const f32x4 &v) {
+    u32x2 r;
+    if constexpr (F16) {
+        r[0] = __builtin_bit_cast(unsigned, f16x2{(_Float16)v[0], (_Float16)v[1]});
+        r[1] = __builtin_bit_cast(unsigned, f16x2{(_Float16)v[2], (_Float16)v[3]});
+    } else {
+        r[0] = __builtin_bit_cast(unsigned, bf16x2{(__bf16)v[0], (__bf16)v[1]});
+        r[1] = __builtin_bit_cast(unsigned, bf16x2{(__bf16)v[2], (__bf16)v[3]});
+    }
+    return r;
+}
+
+// ---------------------------------------------------------------------------------------
+// The kernel
+// ---------------------------------------------------------------------------------------
+// Cross-tile pipeline (kernel variant CROSS, for workgroups with several tiles of
+// >= kCrossMinSteps K steps): the DMAs of a tile's last three K steps already fetch the first K
+// steps of the workgroup's next tile, so a tile boundary has no prologue bubble and no drained
+// pipeline. The finished tile's accumulators are stored from registers inside the next tile's
+// first step, row block by row block, just before its first MFMAs overwrite them.
+#ifndef GG_CROSS_TILE
+#define GG_CROSS_TILE 1
+#endif
+#ifndef GG_STORE_CPOL
+#define GG_STORE_CPOL 2 // cache policy of the register-direct C stores: bit 0 sc0, bit 1 nt, bit 4 sc1
+#endif
+constexpr bool kCrossAllowed  = GG_CROSS_TILE;
+constexpr int  kCrossMinSteps = 4; // the three prefetching steps follow the first
+constexpr int  kStoreCpol     = GG_STORE_CPOL;
+#ifndef GG_PARTIAL_NT
+#define GG_PARTIAL_NT 0
+#endif
+constexpr bool kPartialNt = GG_PARTIAL_NT; // split-K partial sums stored non-temporal (2-5 % slower)
+
+// First step of a cross tile: store s (0-3, see store_line) of the previous tile's row block
+// mi+1 is issued after MFMA 2 + 4s of row mi (row block 0 before the step).
+constexpr int plan_epi(int mi, int idx) {
+    return (mi < 7 && idx % 4 == 2) ? (idx - 2) / 4 : -1;
+}
+
+// MODE: layout (forward, dgrad, wgrad: operand layouts and tile mapping) and input format.
+// CROSS: cross-tile pipeline (needs k_tiles >= kCrossMinSteps); otherwise every tile starts
+// with a prologue and ends with the LDS-staged epilogue.
+template <bool F16, bool CROSS, int MODE>
+__global__ void __launch_bounds__(kThreads, 1) __attribute__((amdgpu_waves_per_eu(1, 1)))
+grouped_gemm_kernel(const KernelArgs args) {
+    constexpr bool A_MN   = mode_a_mn(MODE), B_MN = mode_b_mn(MODE);
+    constexpr bool F8     = mode_f8(MODE);
+    constexpr int  LAYOUT = mode_layout(MODE);
+    constexpr int  ES     = F8 ? 1 : 2;        // input bytes per element
+    constexpr int  KS     = kRowBytes / ES;    // contraction values per K step
+    using P = std::conditional_t<F8, Plan8<reads_per_frag(A_MN), reads_per_frag(B_MN)>,
+                                 Plan<reads_per_frag(A_MN), reads_per_frag(B_MN)>>;
+    static_assert(!(F8 && F16), "fp8 writes bf16");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[kLdsBytes];
+    typedef __attribute__((address_space(3))) uint8_t lds_u8;
+    const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8 *)smem));
+
+    const int lane = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6) & 3;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int K = args.k, N = args.n;
+    int       T = args.k_tiles; // K steps of the current tile (per group for wgrad)
+    // Tile count: from the kernel arguments, or from a group table built on the device.
+    const int total_tiles = args.d_total != nullptr
+                                ? __builtin_amdgcn_readfirstlane(*args.d_total)
+                                : args.total_tiles;
+    // Work units: a tile, or with split-K (per-tile variant only) one K range of a tile; unit
+    // u = split * total_tiles + tile.
+    const int splits      = CROSS ? 1 : args.splits;
+    const int total_units = total_tiles * splits;
+
+    // DMA lane offsets within a tile's K step (the tile origin is in the buffer resource).
+    // K-major operand, row stride ld: DMA j covers tile rows j*32 + wave*8 .. +8; lane -> row
+    // lane/8, logical chunk (lane%8) ^ (lane/8).
+    // MN-major operand, row stride ld, stored rows = contraction index: DMA j covers
+    // contraction rows 4 (2j + wave/2) .. +4 and tile columns 128 (wave%2) .. +128. In LDS the
+    // step is 128-byte blocks of 4 rows x 16 columns: block (rb, cb) = (row/4, column/16) sits
+    // at byte 128 (16 rb + (cb ^ ((rb / 2) & 1))), so the DMA's 1 KB lands at 1024 (4j + wave)
+    // as for a K-major operand; lane -> block column (8 (wave%2) + lane/8) ^ (j & 1), row
+    // (lane%8)/2, 8 columns at 8 (lane%2). The column-block swap in every other pair of row
+    // blocks puts the blocks that lanes 0-15 and 16-31 of one transposed read take (row blocks
+    // rb and rb + 2) in different halves of the 256-byte bank window.
+    // fp8 MN-major: blocks of 8 rows x 16 columns (one 16-byte row per lane); LDS row block p
+    // holds stored row block p ^ (2 ((p / 4) & 1)) with column blocks swapped when (p / 4) is odd:
+    // DMA j (rows of LDS block 2j + wave/2) reads stored row block 2 (j ^ s) + wave/2, column
+    // block (8 (wave%2) + lane/8) ^ s, s = (j / 2) & 1, row lane%8 of the block. The row block
+    // swap gives each lane the K order of a K-major fp8 fragment (halves swapped for odd lane/16,
+    // see below); the column swap separates the blocks of lanes 0-15 and 16-31 in the banks.
+    const int ld_row   = lane >> 3;
+    const int ld_chunk = (lane & 7) ^ ld_row;
+    const int mn_c     = (wave & 1) * 8 + (lane >> 3);
+    // column of the lane in a transposed DMA (elements), with column-block swap sw
+    auto mn_col = [&](int sw) { return (mn_c ^ sw) * 16 + (F8 ? 0 : (lane & 1) * 8); };
+    // the column-block swap of transposed DMA j
+    auto mn_swz = [](int j) { return F8 ? (j >> 1) & 1 : j & 1; };
+    auto dma_off = [&](bool mn, int j, int ld) {
+        if (!mn)
+            return (j * 32 + wave * 8 + ld_row) * ld * ES + ld_chunk * 16;
+        if (F8)
+            return (8 * (2 * (j ^ mn_swz(j)) + (wave >> 1)) + (lane & 7)) * ld + mn_col(mn_swz(j));
+        return ((4 * (2 * j + (wave >> 1)) + ((lane & 7) >> 1)) * ld + mn_col(mn_swz(j))) * 2;
+    };
+    // voff[0]: A's offsets; voff[1]: B's (the forward op shares A's: both row strides are K).
+    constexpr bool kSameOff = LAYOUT == kFwd;
+    int            voff[kSameOff ? 1 : 2][kLoads];
+    sfor<0, kLoads>([&](auto j) {
+        voff[0][j] = dma_off(A_MN, j, args.lda);
+        if constexpr (!kSameOff)
+            voff[1][j] = dma_off(B_MN, j, args.ldb);
+    });
+    // Last K step when K % 64 != 0: chunks at k >= K get an offset past every bound.
+    const int k_last    = K - (T - 1) * KS; // valid K of the last step
+    int       ktail_bad = (ld_chunk * (16 / ES) >= k_last) ? static_cast<int>(0x80000000u) : 0;
+
+    // Fragment reads. K-major: lane -> row lane%16 of a 16-row block, logical chunk
+    // kh*4 + lane/16 (one base per k-half). MN-major: ds_read_b64_tr_b16 gives lane i of each
+    // 16-lane group column i of 4 consecutive rows when source lane s of the group points at
+    // row s/4, column 4 (s%4): lane l reads block (row 8 (l/16) + 4 half + 32 kh, column
+    // 16 blk) at byte 8 (l%16) of it, i.e. base + 16384 kh + 2048 half + 128 (blk ^ (l/16 & 1));
+    // base [blk & 1] holds the lane's part of the swap.
+    // ds_read_b128 serves a wave in passes that pair 8-lane groups whose lane/16 differ in bit 0;
+    // the fp8 fragment reads chunks 2q and 2q+1 (q = lane/16) in the order kh ^ (q & 1), so that
+    // the chunks of such a pair differ in bit 0 as well and take different banks. The lane's K
+    // order is then permuted the same way in x and w, which leaves the dot product unchanged.
+    // fp8 MN-major: ds_read_b64_tr_b8 gives lane i of each 16-lane group column i of 8 rows when
+    // source lane s points at row s/2, column 8 (s%2): read t (0-3) of lane l takes LDS row block
+    // 4 (l/16) + t, i.e. base + 8192 (l/16) + 2048 t + 128 (blk ^ (l/16 & 1)), which holds the
+    // lane's K values in the K-major fragment's order.
+    const int fr_row = lane & 15, fr_q = lane >> 4;
+    int frag_a[2], frag_b[2];
+    sfor<0, 2>([&](auto kh) {
+        const int off = fr_row * kRowBytes +
+                        (((F8 ? 2 * fr_q + (kh ^ (fr_q & 1)) : kh * 4 + fr_q) ^ (fr_row & 7)) * 16);
+        const int mn  = (lane >> 4) * (F8 ? 8192 : 4096) + (lane & 15) * 8 + (kh ? -128 : 128) * (fr_q & 1);
+        frag_a[kh]    = A_MN ? wm * 1024 + mn : wm * 128 * kRowBytes + off;
+        frag_b[kh]    = B_MN ? wn * 1024 + mn : wn * 128 * kRowBytes + off;
+    });
+
+    // Register epilogue: in store s = 2h + half of a 16-row block, lane l writes 16 bytes of
+    // row 8 half + l%8 at column ecol + 64 h (see pack_pair).
+    const int q    = lane >> 4;
+    const int ecol = wn * 128 + ((lane >> 3) & 1) * 32 + (q & 1) * 16 + (q >> 1) * 8;
+    int       voffc = ((wm * 128 + (lane & 7)) * N + ecol) * 2;
+    const int blk_stride = 16 * N * 2; // bytes between 16-row blocks of C
+
+    // Logical stage L of an operand (the K step's index mod 2 for A, mod 3 for B within the
+    // tile) lives in physical stage (L + rot) mod n. A tile that follows with prefetched data
+    // rotates by its predecessor's K-step count.
+    int      rot_a = 0, rot_b = 0;
+    int      a_rd[2][2], b_rd[3][2]; // LDS read base per logical stage and k-half
+    uint32_t a_dst[2], b_dst[3];     // this wave's DMA destination per logical stage
+    auto set_stages = [&]() {
+        sfor<0, 2>([&](auto L) {
+            const int p = ((L + rot_a) & 1) * kOpBytes;
+            a_dst[L]    = lds0 + wave * 1024 + a_stage(0) + p;
+            sfor<0, 2>([&](auto h) { a_rd[L][h] = frag_a[h] + a_stage(0) + p; });
+        });
+        sfor<0, 3>([&](auto L) {
+            int s = L + rot_b;
+            s     = s >= 3 ? s - 3 : s;
+            const int p = b_stage(0) + s * kOpBytes;
+            b_dst[L]    = lds0 + wave * 1024 + p;
+            sfor<0, 2>([&](auto h) { b_rd[L][h] = frag_b[h] + p; });
+        });
+    };
+    // Re-materialise loop-invariant offsets at the top of every loop body (see fresh_v).
+    auto refresh = [&]() {
+        sfor<0, kLoads>([&](auto j) {
+            fresh_v(voff[0][j]);
+            if constexpr (!kSameOff)
+                fresh_v(voff[1][j]);
+        });
+        fresh_v(ktail_bad);
+        fresh_v(voffc);
+        sfor<0, 2>([&](auto L) {
+            fresh_s(a_dst[L]);
+            sfor<0, 2>([&](auto h) { fresh_v(a_rd[L][h]); });
+        });
+        sfor<0, 3>([&](auto L) {
+            fresh_s(b_dst[L]);
+            sfor<0, 2>([&](auto h) { fresh_v(b_rd[L][h]); });
+        });
+    };
+    auto lds_read = [&](int off) -> i32x4 { return *reinterpret_cast<const i32x4 *>(smem + off); };
+    typedef short i16x4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+    typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
+    auto lds_read_tr = [&](int off) -> u32x2 {
+        if constexpr (F8)
+            return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2 *)(smem + off)));
+        else
+            return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(smem + off)));
+    };
+    // LDS read op r (Plan numbering) of the fragment of 16-row block blk into f (per k-half),
+    // from the logical stage whose read bases are rd.
+    auto read_frag = [&]<bool MN, int R>(i32x4(&f)[2], const int(&rd)[2], auto blk) {
+        if constexpr (!MN) {
+            f[R] = lds_read(rd[R] + blk * 16 * kRowBytes);
+        } else {
+            constexpr int kh = R >> 1, half = R & 1;
+            const u32x2   v  = lds_read_tr(rd[blk & 1] + kh * (F8 ? 4096 : 16384) + half * 2048 + blk * 128);
+            f[kh][2 * half]     = static_cast<int>(v[0]);
+            f[kh][2 * half + 1] = static_cast<int>(v[1]);
+        }
+    };
+
+    f32x4 acc[8][8];
+    i32x4 fa[2][2];    // x fragments: row ring x k-half
+    i32x4 fb[2][8][2]; // w fragments: step parity x column block x k-half
+
+    // One output tile: its DMA sources and where its C block goes.
+    struct Tile {
+        i32x4     rsrc_a, rsrc_b; // A / B storage of the tile, bounded to its valid rows
+        uint16_t *c_ptr;          // output block origin
+        int       m_valid, n_valid;
+        int       o0a, o0b;       // MN-major operands: first stored column of the tile
+        int       T;              // K steps (wgrad: of the tile's group, at least 1)
+        int       k0;             // first K step (split-K: the split's range), 0 otherwise
+        int       klast;          // the range ends with the problem's last (maybe partial) K step
+        float     scale;          // fp8: x scale * w[g] scale (1 otherwise)
+    };
+    const int bad_off = static_cast<int>(0x80000000u);
+    int       g       = 0; // group hint of locate_tile (logical tiles only grow)
+    auto      make_tile = [&](int t) -> Tile {
+        // split-K: one unit per workgroup, no L2 sharing across rounds to arrange
+        const int split = splits > 1 ? t / total_tiles : 0;
+        const int L     = splits > 1 ? t - split * total_tiles : xcd_remap(t, total_tiles, gridDim.x, args.n_xcd);
+        int       tm, tn;
+        locate_tile(L, args.groups, args.group_num, args.n_tiles, args.band, &g, &tm, &tn,
+                    LAYOUT == kWgrad ? args.m_out : 0);
+        const GroupEntry ge = args.groups[g];
+        const uint8_t   *xa = static_cast<const uint8_t *>(args.x); // A storage (bytes)
+        const uint8_t   *wb = static_cast<const uint8_t *>(args.w); // B storage (bytes)
+        Tile             tl;
+        tl.n_valid         = min(kTileN, N - tn * kTileN);
+        const int64_t col0 = static_cast<int64_t>(tn) * kTileN;
+        tl.o0a = tl.o0b = 0;
+        // K range of the unit: steps [k0, k1) of k_tiles, balanced over the splits
+        const int k0 = split * args.k_tiles / splits, k1 = (split + 1) * args.k_tiles / splits;
+        tl.T     = k1 - k0;
+        tl.k0    = k0;
+        tl.klast = k1 == args.k_tiles;
+        tl.scale = 1.0f;
+        if constexpr (LAYOUT == kWgrad) {
+            // A^T = grad_out rows of the group, columns tm*256..; B^T = x rows, columns tn*256..
+            const int64_t o0a = static_cast<int64_t>(tm) * kTileM;
+            const int64_t ma  = static_cast<int64_t>(ge.m) * args.lda - o0a; // elements
+            const int64_t mb  = static_cast<int64_t>(ge.m) * args.ldb - col0;
+            tl.m_valid = min(kTileM, args.m_out - tm * kTileM);
+            tl.rsrc_a  = dma_rsrc(xa + (ge.row0 * args.lda + o0a) * ES, static_cast<uint32_t>(ma > 0 ? ma * ES : 0));
+            tl.rsrc_b  = dma_rsrc(wb + (ge.row0 * args.ldb + col0) * ES, static_cast<uint32_t>(mb > 0 ? mb * ES : 0));
+            tl.o0a     = static_cast<int>(o0a);
+            tl.o0b     = static_cast<int>(col0);
+            tl.c_ptr   = static_cast<uint16_t *>(args.out) +
+                       (static_cast<int64_t>(g) * args.m_out + o0a) * N + col0;
+            tl.T     = max(1, static_cast<int>(cdiv(ge.m, KS)));
+            tl.k0    = 0;
+            tl.klast = 1;
+        } else {
+            tl.m_valid         = min(kTileM, ge.m - tm * kTileM);
+            const int64_t row0 = ge.row0 + static_cast<int64_t>(tm) * kTileM;
+            tl.rsrc_a = dma_rsrc(xa + row0 * args.lda * ES, static_cast<uint32_t>(tl.m_valid) * args.lda * ES);
+            if constexpr (LAYOUT == kFwd) {
+                tl.rsrc_b = dma_rsrc(wb + (static_cast<int64_t>(g) * N + col0) * args.ldb * ES,
+                                     static_cast<uint32_t>(tl.n_valid) * args.ldb * ES);
+            } else {
+                // w[g] stored K x N: columns col0.. of all K rows (the end of w[g] bounds it)
+                const int64_t per_g = static_cast<int64_t>(K) * args.ldb;
+                tl.rsrc_b = dma_rsrc(wb + (g * per_g + col0) * ES, static_cast<uint32_t>((per_g - col0) * ES));
+                tl.o0b = static_cast<int>(col0);
+            }
+            tl.c_ptr = static_cast<uint16_t *>(args.out) + row0 * N + col0;
+        }
+        if constexpr (F8)
+            tl.scale = args.x_scale[0] * args.w_scale[g];
+        return tl;
+    };
+    auto c_rsrc = [&](const Tile &tl) {
+        // rows past m_valid fall outside the resource
+        return __builtin_amdgcn_make_buffer_rsrc(tl.c_ptr, static_cast<short>(0),
+                                                 static_cast<int>(tl.m_valid * N * 2), 0x00020000);
+    };
+    const i32x4 rsrc_0 = dma_rsrc(args.x, 0); // zero length: no traffic, the DMA writes zeros
+
+    int t = blockIdx.x;
+    if (t >= total_units)
+        return;
+    Tile cur = make_tile(t), nxt = cur;
+    if constexpr (!CROSS || LAYOUT == kWgrad)
+        T = __builtin_amdgcn_readfirstlane(cur.T);
+    bool cross_next = false; // the DMAs past this tile's last K step fetch `nxt`
+
+    // Where the DMAs of K step kidx of an operand (false: x, true: w) read from: resource,
+    // K offset and the per-lane mask of a partial last step. Unchecked: kidx is a full step of
+    // the current tile. Checked: kidx may be the tile's partial last step or lie past it (the
+    // next tile's first steps, or nothing). Evaluated once per step and operand stream.
+    // MN-major operands: a K step is 64 stored rows, added to the lane offset (not soffset)
+    // so that rows past the contraction length fall outside the resource; lane columns past
+    // the row get an out-of-range offset (mask). K-major: the K step is soffset, and the
+    // partial last step's chunks past K get the out-of-range offset.
+    struct DmaSrc {
+        i32x4 rs;
+        int   so, vadd, mask, mask1; // MN-major: mask for even / odd DMA j (column-block swap)
+    };
+    auto dma_src = [&](auto b_op, int kidx, auto checked) -> DmaSrc {
+        constexpr bool B  = decltype(b_op)::value;
+        constexpr bool MN = B ? B_MN : A_MN;
+        const int      ld = B ? args.ldb : args.lda;
+        i32x4          rc = cur.rsrc_a, rn = nxt.rsrc_a;
+        int            oc = cur.o0a, on = nxt.o0a;
+        if constexpr (B) {
+            rc = cur.rsrc_b;
+            rn = nxt.rsrc_b;
+            oc = cur.o0b;
+            on = nxt.o0b;
+        }
+        DmaSrc d;
+        if constexpr (decltype(checked)::value) {
+            const bool in_cur = kidx < T;
+            const int  koff   = in_cur ? kidx : kidx - T;
+            // step of the operand: the unit's first step plus koff (the next tile starts at 0)
+            const int kabs = in_cur ? koff + cur.k0 : koff;
+            d.rs           = in_cur ? rc : (cross_next ? rn : rsrc_0);
+            if constexpr (MN) {
+                d.so   = 0;
+                d.vadd = kabs * kTileK * ld * 2;
+                d.mask  = (in_cur ? oc : on) + mn_col(0) >= ld ? bad_off : 0;
+                d.mask1 = (in_cur ? oc : on) + mn_col(1) >= ld ? bad_off : 0;
+            } else {
+                d.so   = kabs * kRowBytes;
+                d.vadd = 0;
+                d.mask = (koff == T - 1 && cur.klast) ? ktail_bad : 0;
+            }
+        } else {
+            d.rs = rc;
+            if constexpr (MN) {
+                d.so   = 0;
+                d.vadd = (kidx + cur.k0) * kTileK * ld * 2;
+                d.mask  = oc + mn_col(0) >= ld ? bad_off : 0;
+                d.mask1 = oc + mn_col(1) >= ld ? bad_off : 0;
+            } else {
+                d.so   = (kidx + cur.k0) * kRowBytes;
+                d.vadd = 0;
+                d.mask = 0;
+            }
+        }
+        return d;
+    };
+    // Lane offset of DMA j of operand b_op for source d.
+    auto dma_voff = [&](auto b_op, auto j, const DmaSrc &d, auto checked) -> int {
+        constexpr bool B  = decltype(b_op)::value;
+        constexpr bool MN = B ? B_MN : A_MN;
+        const int      vo = voff[(B && !kSameOff) ? 1 : 0][j];
+        if constexpr (MN)
+            return (vo + d.vadd) | (mn_swz(j) ? d.mask1 : d.mask);
+        else if constexpr (decltype(checked)::value)
+            return vo | d.mask;
+        else
+            return vo;
+    };
+    // DMA with its own M0 write (prologue).
+    auto dma_now = [&](uint32_t dst, auto b_op, auto j, int kidx) {
+        sched_fence();
+        const DmaSrc d = dma_src(b_op, kidx, std::true_type{});
+        dma16(dst + j * 4096, dma_voff(b_op, j, d, std::true_type{}), d.rs, d.so);
+        sched_fence();
+    };
+    // DMA whose M0 was written before the slot's MFMA; cold: with the SGPR wait states.
+    auto dma_go = [&](auto b_op, const DmaSrc &d, auto j, auto checked, auto cold) {
+        sched_fence();
+        dma16_m0<decltype(cold)::value ? 4 : 0>(dma_voff(b_op, j, d, checked), d.rs, d.so);
+        sched_fence();
+    };
+    using A_OP = std::false_type;
+    using B_OP = std::true_type;
+
+    // ---- prologue of a tile that starts cold: A(0), B(0..2), the first DMAs of A(1) ----------
+    auto issue_prologue = [&]() {
+        refresh();
+        sfor<0, kLoads>([&](auto j) { dma_now(a_dst[0], A_OP{}, j, 0); });
+        sfor<0, kLoads>([&](auto j) { dma_now(b_dst[0], B_OP{}, j, 0); });
+        sfor<0, kLoads>([&](auto j) { dma_now(b_dst[1], B_OP{}, j, 1); });
+        sfor<0, kLoads>([&](auto j) { dma_now(b_dst[2], B_OP{}, j, 2); });
+        sfor<0, P::early>([&](auto j) { dma_now(a_dst[1], A_OP{}, j, 1); });
+    };
+    // Then B(0) and A(0) row 0 into registers. VM: DMAs/stores issued after B(1)'s last.
+    auto finish_prologue = [&]<int VM>() {
+        wait_vm_lds_barrier<VM>(); // A(0), B(0), B(1) landed everywhere
+        sfor<0, 8>([&](auto ni) {
+            sfor<0, reads_per_frag(B_MN)>([&](auto r) {
+                read_frag.template operator()<B_MN, r>(fb[0][ni], b_rd[0], ni);
+            });
+        });
+        sfor<0, reads_per_frag(A_MN)>([&](auto r) {
+            read_frag.template operator()<A_MN, r>(fa[0], a_rd[0], ic<0>{});
+        });
+        wait_vm_lds_barrier<63>(); // every wave holds B(0): its stage may be refilled
+    };
+
+    // ---- register epilogue: 1 KB stores of 8 rows x 128 B (whole cache lines) ----------------
+    // Lane l holds C^T blocks: row l%16, columns 4q..4q+3 of each 16 x 16 block (q = l/16).
+    // One v_permlane16_swap per dword between blocks 2j and 2j+1 gives chunk X_j: every lane
+    // holds 8 consecutive columns of its row, q = 0, 2 from block 2j, q = 1, 3 from block 2j+1,
+    // columns 0-7 (q < 2) or 8-15; 4 lanes cover 64 bytes of a row. Two DPP row shifts then
+    // pair X_2h with X_2h+1 so that a store covers whole 128-byte rows:
+    //   Z_A: lanes l%16 < 8 keep X_2h (row l%16), lanes l%16 >= 8 take X_2h+1 of lane l-8;
+    //   Z_B: lanes l%16 >= 8 keep X_2h+1 (row l%16), lanes l%16 < 8 take X_2h of lane l+8.
+    // Z_A holds rows 0-7 and Z_B rows 8-15 of the block, columns 64h..64h+63.
+    float prev_scale = 1.0f; // fp8: scale of the tile whose accumulators the fused stores take
+    auto  pack_chunk = [&](auto r, auto j) -> u32x4 {
+        // reads of these accumulators may not move above this point
+        asm volatile("" : "+a"(acc[r][2 * j]), "+a"(acc[r][2 * j + 1]));
+        f32x4 v0 = acc[r][2 * j], v1 = acc[r][2 * j + 1];
+        if constexpr (F8) {
+            v0 *= prev_scale;
+            v1 *= prev_scale;
+        }
+        const u32x2 p0 = pack4<F16>(v0);
+        const u32x2 p1 = pack4<F16>(v1);
+        const auto  s0 = __builtin_amdgcn_permlane16_swap(p0[0], p1[0], false, false);
+        const auto  s1 = __builtin_amdgcn_permlane16_swap(p0[1], p1[1], false, false);
+        return u32x4{s0[0], s1[0], s0[1], s1[1]};
+    };
+    auto pack_pair = [&](auto r, auto h, u32x4 &za, u32x4 &zb) {
+        const u32x4 x0 = pack_chunk(r, ic<2 * h>{});
+        const u32x4 x1 = pack_chunk(r, ic<2 * h + 1>{});
+        sfor<0, 4>([&](auto i) {
+            // row_shr:8 into banks 2-3, row_shl:8 into banks 0-1
+            za[int(i)] = __builtin_amdgcn_update_dpp(x0[int(i)], x1[int(i)], 0x118, 0xf, 0xc, false);
+            zb[int(i)] = __builtin_amdgcn_update_dpp(x1[int(i)], x0[int(i)], 0x108, 0xf, 0x3, false);
+        });
+    };
+    // Store s = 2h + half of row block r. Chunks past n_valid get an out-of-range offset
+    // (N % 8 == 0, so a 16-byte chunk is either all valid or all past N).
+    auto store_line = [&](const u32x4 &d, int r, int s_, const __amdgpu_buffer_rsrc_t &crs,
+                          int n_valid) {
+        const int h  = s_ >> 1, half = s_ & 1;
+        const int vo = ecol + 64 * h < n_valid
+                           ? voffc + r * blk_stride + half * (blk_stride >> 1) + h * 128
+                           : static_cast<int>(0x80000000u);
+        __builtin_amdgcn_raw_buffer_store_b128(d, crs, vo, 0, kStoreCpol);
+    };
+    // ---- epilogue through LDS: accumulators -> 16-bit -> LDS (528-byte row stride) -> every wave
+    // streams 64 whole rows, two 512-byte rows per 16-byte-per-lane store. Needs all of LDS.
+    auto epilogue_lds = [&](const Tile &tl) {
+        wait_vm_lds_barrier<0>(); // trailing DMAs landed, every wave is done reading LDS
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" ::: "memory"); // MFMA -> VALU read distance
+        {
+            int row = wm * 128 + (lane & 15);
+            fresh_v(row);
+            const int col = wn * 128 + (lane >> 4) * 4;
+            const int off = row * kCStride + col * 2;
+            sfor<0, 8>([&](auto mi) {
+                sfor<0, 8>([&](auto ni) {
+                    asm volatile("" : "+a"(acc[mi][ni]));
+                    f32x4 v = acc[mi][ni];
+                    if constexpr (F8)
+                        v *= tl.scale;
+                    *reinterpret_cast<u32x2 *>(smem + off + mi * 16 * kCStride + ni * 16 * 2) = pack4<F16>(v);
+                });
+            });
+        }
+        wait_vm_lds_barrier<63>();
+        int row = wave * 64 + (lane >> 5);
+        fresh_v(row);
+        const int chunk = lane & 31;
+        const int loff  = row * kCStride + chunk * 16;
+        const int goff  = chunk * 8 < tl.n_valid ? (row * N + chunk * 8) * 2 : static_cast<int>(0x80000000u);
+        const __amdgpu_buffer_rsrc_t crs = c_rsrc(tl);
+        sfor<0, 2>([&](auto half) {
+            i32x4 d[16];
+            sfor<0, 16>([&](auto i) { d[i] = lds_read(loff + (half * 16 + i) * 2 * kCStride); });
+            sfor<0, 16>([&](auto i) {
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    __builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, d[i]), crs,
+                    goff + (half * 16 + i) * 2 * N * 2, 0, /*nt*/ 2);
+            });
+        });
+        wait_vm_lds_barrier<63>(); // every wave is done reading the staged C
+    };
+    // ---- split-K unit: its fp32 accumulators to the workspace slab of unit u (256 KB), in
+    // register order: wave w, block (mi, ni), lane l at float 65536 u + 16384 w + 256 (8 mi + ni)
+    // + 4 l (whole 1 KB per store instruction). split_reduce_kernel adds the slabs of a tile.
+    auto store_partial = [&](int u) {
+        wait_vm_lds_barrier<0>(); // trailing DMAs landed, every wave is done reading LDS
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" ::: "memory"); // MFMA -> VALU read distance
+        float *dst = args.ws + static_cast<int64_t>(u) * 65536 + wave * 16384 + lane * 4;
+        sfor<0, 8>([&](auto mi) {
+            sfor<0, 8>([&](auto ni) {
+                asm volatile("" : "+a"(acc[mi][ni]));
+                f32x4 *d = reinterpret_cast<f32x4 *>(dst + (mi * 8 + ni) * 256);
+                if constexpr (kPartialNt)
+                    __builtin_nontemporal_store(acc[mi][ni], d);
+                else
+                    *d = acc[mi][ni];
+            });
+        });
+    };
+
+    // ---- one K step ---------------------------------------------------------------------------
+    // SA = kt % 2 (A logical stage, w register set), SB = kt % 3 (B logical stage).
+    // FUSE: first step of a tile whose predecessor's accumulators are still to be stored (row
+    // blocks 1-7 here; block 0 before the step), to prev_crs / prev_n. Nothing to store before
+    // the first tile: zero-length resource, the stores are dropped.
+    const __amdgpu_buffer_rsrc_t null_crs =
+        __builtin_amdgcn_make_buffer_rsrc(cur.c_ptr, static_cast<short>(0), 0, 0x00020000);
+    __amdgpu_buffer_rsrc_t prev_crs = null_crs;
+    int                    prev_n   = 0;
+    u32x4                  pair[2];
+    // Store s (0-3) of the previous tile's row block r: packed with the next one for even s.
+    auto epi_store = [&](auto r, auto s_) {
+        sched_fence();
+        if constexpr (s_ % 2 == 0)
+            pack_pair(r, ic<s_ / 2>{}, pair[0], pair[1]);
+        store_line(pair[s_ % 2], r, s_, prev_crs, prev_n);
+        sched_fence();
+    };
+    auto step = [&]<int SA, int SB, bool FIRST, bool CHECKED, bool FUSE>(int kt) {
+        // kt is uniform; saying so keeps the checked tail's comparisons and resource selects
+        // scalar when the compiler would otherwise carry kt through a branch merge in a VGPR.
+        kt = __builtin_amdgcn_readfirstlane(kt);
+        constexpr int NX = SA ^ 1;
+        constexpr int SB_NEXT = (SB + 1) % 3;
+        using chk = std::integral_constant<bool, CHECKED>;
+        const DmaSrc src_a1 = dma_src(A_OP{}, kt + 1, chk{}); // A(kt+1)
+        const DmaSrc src_b3 = dma_src(B_OP{}, kt + 3, chk{}); // B(kt+3)
+        const DmaSrc src_a2 = dma_src(A_OP{}, kt + 2, chk{}); // A(kt+2)
+        sfor<0, 8>([&](auto mi_) {
+            constexpr int mi = decltype(mi_)::value;
+            sfor<0, P::slots>([&](auto idx_) {
+                constexpr int idx = decltype(idx_)::value;
+                constexpr int kh = idx / 8, ni = idx % 8; // fp8: one MFMA per (mi, ni), kh = 0
+                constexpr int dk = P::dma_kind(mi, idx), dj = P::dma_j(mi, idx);
+                if constexpr (dk == 1)
+                    set_m0<dj * 4096>(a_dst[NX]); // the MFMA below is the wait state
+                else if constexpr (dk == 2)
+                    set_m0<dj * 4096>(b_dst[SB]);
+                else if constexpr (dk == 3)
+                    set_m0<dj * 4096>(a_dst[SA]);
+                sched_fence();
+                if constexpr (F8) {
+                    const i32x8 bw = __builtin_shufflevector(fb[SA][ni][0], fb[SA][ni][1], 0, 1, 2, 3, 4, 5, 6, 7);
+                    const i32x8 ax = __builtin_shufflevector(fa[mi & 1][0], fa[mi & 1][1], 0, 1, 2, 3, 4, 5, 6, 7);
+                    mfma8<mode_b_e5(MODE), mode_a_e5(MODE), FIRST>(acc[mi][ni], bw, ax);
+                } else if constexpr (FIRST && kh == 0)
+                    mfma_first<F16>(acc[mi][ni], fb[SA][ni][0], fa[mi & 1][0]);
+                else
+                    mfma<F16>(acc[mi][ni], fb[SA][ni][kh], fa[mi & 1][kh]);
+                sched_fence();
+                if constexpr (mi == kBarRow && idx == P::bar) {
+                    wait_vm_lds_barrier<P::vm_at_barrier()>();
+                    sched_fence();
+                }
+                if constexpr (P::read_a_next(mi, idx) >= 0) {
+                    read_frag.template operator()<A_MN, P::read_a_next(mi, idx)>(fa[(mi + 1) & 1], a_rd[SA],
+                                                                                 ic<mi + 1>{});
+                    sched_fence();
+                }
+                if constexpr (P::read_b_next(mi, idx) >= 0) {
+                    read_frag.template operator()<B_MN, P::read_b_next(mi, idx)>(fb[NX][mi], b_rd[SB_NEXT],
+                                                                                 ic<mi>{});
+                    sched_fence();
+                }
+                if constexpr (P::read_a_row0(mi, idx) >= 0) {
+                    read_frag.template operator()<A_MN, P::read_a_row0(mi, idx)>(fa[0], a_rd[NX], ic<0>{});
+                    sched_fence();
+                }
+                if constexpr (FUSE && P::epi(mi, idx) >= 0)
+                    epi_store(ic<mi + 1>{}, ic<P::epi(mi, idx)>{});
+                using cold = std::integral_constant<bool, FUSE>;
+                if constexpr (dk == 1)
+                    dma_go(A_OP{}, src_a1, ic<dj>{}, chk{}, cold{});
+                else if constexpr (dk == 2)
+                    dma_go(B_OP{}, src_b3, ic<dj>{}, chk{}, cold{});
+                else if constexpr (dk == 3)
+                    dma_go(A_OP{}, src_a2, ic<dj>{}, chk{}, cold{});
+            });
+        });
+    };
+
+    // ---- the persistent loop ------------------------------------------------------------------
+    // Cross-tile: one prologue, before the first tile. Per-tile: a prologue at the top of every
+    // tile (a single copy of it, so the fragment registers have one definition in the loop).
+    if constexpr (CROSS) {
+        set_stages();
+        issue_prologue();
+        finish_prologue.template operator()<kLoads + P::early>();
+    }
+    while (true) {
+        if constexpr (!CROSS) {
+            set_stages();
+            issue_prologue();
+            finish_prologue.template operator()<kLoads + P::early>();
+        }
+        refresh();
+        if constexpr (CROSS) {
+            // First step: stores the previous tile's accumulators while it overwrites them (to
+            // nowhere for the first tile). Always the same code, so the accumulators never
+            // merge across branches and stay in AGPRs.
+            sfor<0, 4>([&](auto s_) { epi_store(ic<0>{}, s_); });
+            step.template operator()<0, 0, true, true, true>(0);
+        } else {
+            step.template operator()<0, 0, true, true, false>(0);
+        }
+        int kt = 1; // kt % 6 == 1 at the top of each block of six steps
+        // Unchecked: every prefetch of the block (up to kt + 8) is a full step before T-1.
+        for (; kt + 9 < T; kt += 6) {
+            refresh();
+            step.template operator()<1, 1, false, false, false>(kt);
+            step.template operator()<0, 2, false, false, false>(kt + 1);
+            step.template operator()<1, 0, false, false, false>(kt + 2);
+            step.template operator()<0, 1, false, false, false>(kt + 3);
+            step.template operator()<1, 2, false, false, false>(kt + 4);
+            step.template operator()<0, 0, false, false, false>(kt + 5);
+        }
+        const int  t_next = t + gridDim.x;
+        const bool more   = t_next < total_units;
+        cross_next        = CROSS && more;
+        if (cross_next)
+            nxt = make_tile(t_next);
+        for (; kt < T; kt += 6) { // at most 9 steps left; with CROSS the last three prefetch `nxt`
+            refresh();
+            step.template operator()<1, 1, false, true, false>(kt);
+            if (kt + 1 < T) step.template operator()<0, 2, false, true, false>(kt + 1);
+            if (kt + 2 < T) step.template operator()<1, 0, false, true, false>(kt + 2);
+            if (kt + 3 < T) step.template operator()<0, 1, false, true, false>(kt + 3);
+            if (kt + 4 < T) step.template operator()<1, 2, false, true, false>(kt + 4);
+            if (kt + 5 < T) step.template operator()<0, 0, false, true, false>(kt + 5);
+        }
+        if constexpr (CROSS) {
+            if (!cross_next)
+                break; // last tile of the workgroup: stored after the loop
+            {
+                // The next tile's first steps are in flight or in LDS, B(0) of it is in the w
+                // register set T % 2 and row 0 of A(0) in fa[0]: continue without a prologue.
+                prev_crs   = c_rsrc(cur);
+                prev_n     = cur.n_valid;
+                prev_scale = cur.scale;
+                cur      = nxt;
+                t        = t_next;
+                rot_a    = (rot_a + T) & 1;
+                rot_b    = rot_b + T % 3;
+                rot_b    = rot_b >= 3 ? rot_b - 3 : rot_b;
+                set_stages();
+                if (T & 1) // the first step reads w set 0
+                    sfor<0, 8>([&](auto ni) { sfor<0, 2>([&](auto h) { fb[0][ni][h] = fb[1][ni][h]; }); });
+                if constexpr (LAYOUT == kWgrad) // the next group's K-step count
+                    T = __builtin_amdgcn_readfirstlane(cur.T);
+                continue;
+            }
+        }
+        if constexpr (!CROSS) {
+            // Store this tile through LDS (split-K: its partial sums to the workspace); the next
+            // one starts cold at the top of the loop (the stores were issued before its DMAs and
+            // complete first).
+            if (splits > 1)
+                store_partial(t);
+            else
+                epilogue_lds(cur);
+            if (!more)
+                return;
+            t   = t_next;
+            cur = make_tile(t);
+            T   = __builtin_amdgcn_readfirstlane(cur.T);
+        }
+    }
+    if constexpr (CROSS)
+        epilogue_lds(cur);
+}
+
+} // namespace
+} // namespace gg
