@@ -10,7 +10,8 @@ namespace {
 // ---------------------------------------------------------------------------------------
 // Split-K reduction: block b takes 256 16-byte positions (b % 64) of logical tile b / 64.
 // Position p of a slab is wave p / 4096, accumulator block (mi, ni) = ((p / 64) % 64) / 8, % 8,
-// lane p % 64, which hold C row 128 (wave / 2) + 16 mi + lane % 16, columns
+// lane p % 64, which hold C row 16 (wave / 2) + 32 mi + lane % 16 (the interleaved row blocks of a
+// K-major A; split-K serves the forward and dgrad layouts only), columns
 // 128 (wave % 2) + 16 ni + 4 (lane / 16) .. +3 of the tile.
 // ---------------------------------------------------------------------------------------
 template <bool F16, bool F8>
@@ -21,7 +22,7 @@ __global__ void __launch_bounds__(256) split_reduce_kernel(const KernelArgs args
     const GroupEntry ge   = args.groups[g];
     const int        p    = (blockIdx.x & 63) * 256 + static_cast<int>(threadIdx.x);
     const int        wv   = p >> 12, blk = (p >> 6) & 63, l = p & 63;
-    const int        row  = (wv >> 1) * 128 + (blk >> 3) * 16 + (l & 15);
+    const int        row  = (wv >> 1) * 16 + (blk >> 3) * 32 + (l & 15);
     const int        col  = (wv & 1) * 128 + (blk & 7) * 16 + (l >> 4) * 4;
     const int        N    = args.n;
     const int64_t    slab = static_cast<int64_t>(args.total_tiles) * 65536; // floats per split

@@ -489,6 +489,23 @@ constexpr int plan_epi(int mi, int idx) {
     return (mi < 7 && idx % 4 == 2) ? (idx - 2) / 4 : -1;
 }
 
+// Partial tiles: a wave skips the MFMAs of its 16-row blocks that hold no valid output (1), or
+// computes every block (0).
+#ifndef GG_TAIL_SKIP
+#define GG_TAIL_SKIP 1
+#endif
+constexpr bool kTailSkip = GG_TAIL_SKIP;
+
+// The row blocks (bit mi) of wave (wm, wn) that hold a valid output in a tile of m_valid rows and
+// n_valid columns: none when the wave's 128 columns (128 wn ..) are all past n_valid. Row block
+// mi of the wave is tile rows 16 (2 mi + wm) .. +16 when interleaved (ILV), 128 wm + 16 mi ..
+// otherwise.
+template <bool ILV> __device__ __forceinline__ uint32_t active_rows(int m_valid, int n_valid, int wm, int wn) {
+    const int nb_m = (m_valid + 15) >> 4; // 16-row blocks with a valid row
+    const int ra   = min(8, max(0, ILV ? (nb_m - wm + 1) >> 1 : nb_m - 8 * wm));
+    return n_valid > 128 * wn ? (1u << ra) - 1 : 0u;
+}
+
 // MODE: layout (forward, dgrad, wgrad: operand layouts and tile mapping) and input format.
 // CROSS: cross-tile pipeline (needs k_tiles >= kCrossMinSteps); otherwise every tile starts
 // with a prologue and ends with the LDS-staged epilogue.
@@ -500,6 +517,15 @@ grouped_gemm_kernel(const KernelArgs args) {
     constexpr int  LAYOUT = mode_layout(MODE);
     constexpr int  ES     = F8 ? 1 : 2;        // input bytes per element
     constexpr int  KS     = kRowBytes / ES;    // contraction values per K step
+    // Row blocks of a wave: interleaved (wave wm's block mi is tile rows 16 (2 mi + wm) ..) when A
+    // is K-major, so that the valid rows of a partial tile split evenly between the wm = 0 and
+    // wm = 1 waves; contiguous (128 wm + 16 mi ..) for the MN-major A of wgrad.
+    constexpr bool ILV    = !A_MN;
+    constexpr int  A_BLK  = ILV ? 32 : 16; // tile rows between a wave's consecutive row blocks
+    // Partial tiles skip their empty row blocks in the forward layout. (dgrad and wgrad compute
+    // every block: with the row branches their instances stopped LLVM's AMDGPU backend with an
+    // "illegal VGPR to SGPR copy".)
+    constexpr bool kThin  = kTailSkip && LAYOUT == kFwd;
     using P = std::conditional_t<F8, Plan8<reads_per_frag(A_MN), reads_per_frag(B_MN)>,
                                  Plan<reads_per_frag(A_MN), reads_per_frag(B_MN)>>;
     static_assert(!(F8 && F16), "fp8 writes bf16");
@@ -584,7 +610,7 @@ grouped_gemm_kernel(const KernelArgs args) {
         const int off = fr_row * kRowBytes +
                         (((F8 ? 2 * fr_q + (kh ^ (fr_q & 1)) : kh * 4 + fr_q) ^ (fr_row & 7)) * 16);
         const int mn  = (lane >> 4) * (F8 ? 8192 : 4096) + (lane & 15) * 8 + (kh ? -128 : 128) * (fr_q & 1);
-        frag_a[kh]    = A_MN ? wm * 1024 + mn : wm * 128 * kRowBytes + off;
+        frag_a[kh]    = A_MN ? wm * 1024 + mn : wm * (ILV ? 16 : 128) * kRowBytes + off;
         frag_b[kh]    = B_MN ? wn * 1024 + mn : wn * 128 * kRowBytes + off;
     });
 
@@ -592,8 +618,8 @@ grouped_gemm_kernel(const KernelArgs args) {
     // row 8 half + l%8 at column ecol + 64 h (see pack_pair).
     const int q    = lane >> 4;
     const int ecol = wn * 128 + ((lane >> 3) & 1) * 32 + (q & 1) * 16 + (q >> 1) * 8;
-    int       voffc = ((wm * 128 + (lane & 7)) * N + ecol) * 2;
-    const int blk_stride = 16 * N * 2; // bytes between 16-row blocks of C
+    int       voffc = ((wm * (ILV ? 16 : 128) + (lane & 7)) * N + ecol) * 2;
+    const int blk_stride = A_BLK * N * 2; // bytes between a wave's 16-row blocks of C
 
     // Logical stage L of an operand (the K step's index mod 2 for A, mod 3 for B within the
     // tile) lives in physical stage (L + rot) mod n. A tile that follows with prefetched data
@@ -645,9 +671,9 @@ grouped_gemm_kernel(const KernelArgs args) {
     };
     // LDS read op r (Plan numbering) of the fragment of 16-row block blk into f (per k-half),
     // from the logical stage whose read bases are rd.
-    auto read_frag = [&]<bool MN, int R>(i32x4(&f)[2], const int(&rd)[2], auto blk) {
+    auto read_frag = [&]<bool MN, int R, int BLK_ROWS = 16>(i32x4(&f)[2], const int(&rd)[2], auto blk) {
         if constexpr (!MN) {
-            f[R] = lds_read(rd[R] + blk * 16 * kRowBytes);
+            f[R] = lds_read(rd[R] + blk * BLK_ROWS * kRowBytes);
         } else {
             constexpr int kh = R >> 1, half = R & 1;
             const u32x2   v  = lds_read_tr(rd[blk & 1] + kh * (F8 ? 4096 : 16384) + half * 2048 + blk * 128);
@@ -670,6 +696,7 @@ grouped_gemm_kernel(const KernelArgs args) {
         int       k0;             // first K step (split-K: the split's range), 0 otherwise
         int       klast;          // the range ends with the problem's last (maybe partial) K step
         float     scale;          // fp8: x scale * w[g] scale (1 otherwise)
+        uint32_t  rows;           // this wave's row blocks (bit mi) that hold a valid output
     };
     const int bad_off = static_cast<int>(0x80000000u);
     int       g       = 0; // group hint of locate_tile (logical tiles only grow)
@@ -725,6 +752,7 @@ grouped_gemm_kernel(const KernelArgs args) {
         }
         if constexpr (F8)
             tl.scale = args.x_scale[0] * args.w_scale[g];
+        tl.rows = __builtin_amdgcn_readfirstlane(active_rows<ILV>(tl.m_valid, tl.n_valid, wm, wn));
         return tl;
     };
     auto c_rsrc = [&](const Tile &tl) {
@@ -844,7 +872,7 @@ grouped_gemm_kernel(const KernelArgs args) {
             });
         });
         sfor<0, reads_per_frag(A_MN)>([&](auto r) {
-            read_frag.template operator()<A_MN, r>(fa[0], a_rd[0], ic<0>{});
+            read_frag.template operator()<A_MN, r, A_BLK>(fa[0], a_rd[0], ic<0>{});
         });
         wait_vm_lds_barrier<63>(); // every wave holds B(0): its stage may be refilled
     };
@@ -888,7 +916,7 @@ grouped_gemm_kernel(const KernelArgs args) {
                           int n_valid) {
         const int h  = s_ >> 1, half = s_ & 1;
         const int vo = ecol + 64 * h < n_valid
-                           ? voffc + r * blk_stride + half * (blk_stride >> 1) + h * 128
+                           ? voffc + r * blk_stride + half * (8 * N * 2) + h * 128
                            : static_cast<int>(0x80000000u);
         __builtin_amdgcn_raw_buffer_store_b128(d, crs, vo, 0, kStoreCpol);
     };
@@ -898,7 +926,7 @@ grouped_gemm_kernel(const KernelArgs args) {
         wait_vm_lds_barrier<0>(); // trailing DMAs landed, every wave is done reading LDS
         asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" ::: "memory"); // MFMA -> VALU read distance
         {
-            int row = wm * 128 + (lane & 15);
+            int row = wm * (ILV ? 16 : 128) + (lane & 15);
             fresh_v(row);
             const int col = wn * 128 + (lane >> 4) * 4;
             const int off = row * kCStride + col * 2;
@@ -908,7 +936,7 @@ grouped_gemm_kernel(const KernelArgs args) {
                     f32x4 v = acc[mi][ni];
                     if constexpr (F8)
                         v *= tl.scale;
-                    *reinterpret_cast<u32x2 *>(smem + off + mi * 16 * kCStride + ni * 16 * 2) = pack4<F16>(v);
+                    *reinterpret_cast<u32x2 *>(smem + off + mi * A_BLK * kCStride + ni * 16 * 2) = pack4<F16>(v);
                 });
             });
         }
@@ -967,6 +995,19 @@ grouped_gemm_kernel(const KernelArgs args) {
         store_line(pair[s_ % 2], r, s_, prev_crs, prev_n);
         sched_fence();
     };
+    // MFMA idx of row mi of a K step (w register set SA; FIRST: the tile's first step, C = 0).
+    auto row_mfma = [&]<int SA, bool FIRST>(auto mi_, auto idx_) {
+        constexpr int mi = decltype(mi_)::value, idx = decltype(idx_)::value;
+        constexpr int kh = idx / 8, ni = idx % 8; // fp8: one MFMA per (mi, ni), kh = 0
+        if constexpr (F8) {
+            const i32x8 bw = __builtin_shufflevector(fb[SA][ni][0], fb[SA][ni][1], 0, 1, 2, 3, 4, 5, 6, 7);
+            const i32x8 ax = __builtin_shufflevector(fa[mi & 1][0], fa[mi & 1][1], 0, 1, 2, 3, 4, 5, 6, 7);
+            mfma8<mode_b_e5(MODE), mode_a_e5(MODE), FIRST>(acc[mi][ni], bw, ax);
+        } else if constexpr (FIRST && kh == 0)
+            mfma_first<F16>(acc[mi][ni], fb[SA][ni][0], fa[mi & 1][0]);
+        else
+            mfma<F16>(acc[mi][ni], fb[SA][ni][kh], fa[mi & 1][kh]);
+    };
     auto step = [&]<int SA, int SB, bool FIRST, bool CHECKED, bool FUSE>(int kt) {
         // kt is uniform; saying so keeps the checked tail's comparisons and resource selects
         // scalar when the compiler would otherwise carry kt through a branch merge in a VGPR.
@@ -981,7 +1022,6 @@ grouped_gemm_kernel(const KernelArgs args) {
             constexpr int mi = decltype(mi_)::value;
             sfor<0, P::slots>([&](auto idx_) {
                 constexpr int idx = decltype(idx_)::value;
-                constexpr int kh = idx / 8, ni = idx % 8; // fp8: one MFMA per (mi, ni), kh = 0
                 constexpr int dk = P::dma_kind(mi, idx), dj = P::dma_j(mi, idx);
                 if constexpr (dk == 1)
                     set_m0<dj * 4096>(a_dst[NX]); // the MFMA below is the wait state
@@ -990,21 +1030,14 @@ grouped_gemm_kernel(const KernelArgs args) {
                 else if constexpr (dk == 3)
                     set_m0<dj * 4096>(a_dst[SA]);
                 sched_fence();
-                if constexpr (F8) {
-                    const i32x8 bw = __builtin_shufflevector(fb[SA][ni][0], fb[SA][ni][1], 0, 1, 2, 3, 4, 5, 6, 7);
-                    const i32x8 ax = __builtin_shufflevector(fa[mi & 1][0], fa[mi & 1][1], 0, 1, 2, 3, 4, 5, 6, 7);
-                    mfma8<mode_b_e5(MODE), mode_a_e5(MODE), FIRST>(acc[mi][ni], bw, ax);
-                } else if constexpr (FIRST && kh == 0)
-                    mfma_first<F16>(acc[mi][ni], fb[SA][ni][0], fa[mi & 1][0]);
-                else
-                    mfma<F16>(acc[mi][ni], fb[SA][ni][kh], fa[mi & 1][kh]);
+                row_mfma.template operator()<SA, FIRST>(mi_, idx_);
                 sched_fence();
                 if constexpr (mi == kBarRow && idx == P::bar) {
                     wait_vm_lds_barrier<P::vm_at_barrier()>();
                     sched_fence();
                 }
                 if constexpr (P::read_a_next(mi, idx) >= 0) {
-                    read_frag.template operator()<A_MN, P::read_a_next(mi, idx)>(fa[(mi + 1) & 1], a_rd[SA],
+                    read_frag.template operator()<A_MN, P::read_a_next(mi, idx), A_BLK>(fa[(mi + 1) & 1], a_rd[SA],
                                                                                  ic<mi + 1>{});
                     sched_fence();
                 }
@@ -1014,7 +1047,7 @@ grouped_gemm_kernel(const KernelArgs args) {
                     sched_fence();
                 }
                 if constexpr (P::read_a_row0(mi, idx) >= 0) {
-                    read_frag.template operator()<A_MN, P::read_a_row0(mi, idx)>(fa[0], a_rd[NX], ic<0>{});
+                    read_frag.template operator()<A_MN, P::read_a_row0(mi, idx), A_BLK>(fa[0], a_rd[NX], ic<0>{});
                     sched_fence();
                 }
                 if constexpr (FUSE && P::epi(mi, idx) >= 0)
@@ -1027,6 +1060,62 @@ grouped_gemm_kernel(const KernelArgs args) {
                 else if constexpr (dk == 3)
                     dma_go(A_OP{}, src_a2, ic<dj>{}, chk{}, cold{});
             });
+        });
+    };
+
+    // ---- one K step of a partial tile (kThin) -------------------------------------------------
+    // The same memory operations and barrier as a checked step, in the same order, so the waves
+    // of a workgroup stay in step whichever kind of step each runs; but each row issues its
+    // memory operations first (every DMA with its own M0 write and wait states) and then its 16
+    // MFMAs behind one uniform branch on the wave's row mask. A skipped row block keeps stale
+    // accumulators, which no store writes: its rows are past m_valid (outside the C resource) or
+    // the wave's columns are all past n_valid (out-of-range chunk offsets). The row's reads fill
+    // the next row's x fragments and the next step's w fragments, never the ones its MFMAs read.
+    auto step_thin = [&]<int SA, int SB>(int kt) {
+        kt = __builtin_amdgcn_readfirstlane(kt);
+        constexpr int NX = SA ^ 1;
+        constexpr int SB_NEXT = (SB + 1) % 3;
+        uint32_t rows_w = __builtin_amdgcn_readfirstlane(cur.rows);
+        fresh_s(rows_w); // tested next to each row's branch
+        sfor<0, 8>([&](auto mi_) {
+            constexpr int mi = decltype(mi_)::value;
+            sfor<0, P::slots>([&](auto idx_) {
+                constexpr int idx = decltype(idx_)::value;
+                constexpr int dk = P::dma_kind(mi, idx), dj = P::dma_j(mi, idx);
+                if constexpr (mi == kBarRow && idx == P::bar) {
+                    sched_fence();
+                    wait_vm_lds_barrier<P::vm_at_barrier()>();
+                    sched_fence();
+                }
+                if constexpr (P::read_a_next(mi, idx) >= 0) {
+                    read_frag.template operator()<A_MN, P::read_a_next(mi, idx), A_BLK>(fa[(mi + 1) & 1], a_rd[SA],
+                                                                                 ic<mi + 1>{});
+                    sched_fence();
+                }
+                if constexpr (P::read_b_next(mi, idx) >= 0) {
+                    read_frag.template operator()<B_MN, P::read_b_next(mi, idx)>(fb[NX][mi], b_rd[SB_NEXT],
+                                                                                 ic<mi>{});
+                    sched_fence();
+                }
+                if constexpr (P::read_a_row0(mi, idx) >= 0) {
+                    read_frag.template operator()<A_MN, P::read_a_row0(mi, idx), A_BLK>(fa[0], a_rd[NX], ic<0>{});
+                    sched_fence();
+                }
+                if constexpr (dk == 1)
+                    dma_now(a_dst[NX], A_OP{}, ic<dj>{}, kt + 1);
+                else if constexpr (dk == 2)
+                    dma_now(b_dst[SB], B_OP{}, ic<dj>{}, kt + 3);
+                else if constexpr (dk == 3)
+                    dma_now(a_dst[SA], A_OP{}, ic<dj>{}, kt + 2);
+            });
+            sched_fence();
+            if (rows_w & (1u << mi)) {
+                sfor<0, P::slots>([&](auto idx_) {
+                    row_mfma.template operator()<SA, false>(mi_, idx_);
+                    sched_fence();
+                });
+            }
+            sched_fence();
         });
     };
 
@@ -1045,6 +1134,13 @@ grouped_gemm_kernel(const KernelArgs args) {
             finish_prologue.template operator()<kLoads + P::early>();
         }
         refresh();
+        const int  t_next = t + gridDim.x;
+        const bool more   = t_next < total_units;
+        // A partial tile (kThin: this wave has row blocks without a valid output) runs its steps
+        // after the first as thin steps (step_thin) in a loop of their own; a full tile never
+        // enters it. Loops in sequence, not branches around whole steps, so the accumulators
+        // stay in place.
+        const bool thin = kThin && __builtin_amdgcn_readfirstlane(cur.rows) != 0xffu;
         if constexpr (CROSS) {
             // First step: stores the previous tile's accumulators while it overwrites them (to
             // nowhere for the first tile). Always the same code, so the accumulators never
@@ -1056,7 +1152,7 @@ grouped_gemm_kernel(const KernelArgs args) {
         }
         int kt = 1; // kt % 6 == 1 at the top of each block of six steps
         // Unchecked: every prefetch of the block (up to kt + 8) is a full step before T-1.
-        for (; kt + 9 < T; kt += 6) {
+        for (; !thin && kt + 9 < T; kt += 6) {
             refresh();
             step.template operator()<1, 1, false, false, false>(kt);
             step.template operator()<0, 2, false, false, false>(kt + 1);
@@ -1065,12 +1161,10 @@ grouped_gemm_kernel(const KernelArgs args) {
             step.template operator()<1, 2, false, false, false>(kt + 4);
             step.template operator()<0, 0, false, false, false>(kt + 5);
         }
-        const int  t_next = t + gridDim.x;
-        const bool more   = t_next < total_units;
-        cross_next        = CROSS && more;
+        cross_next = CROSS && more;
         if (cross_next)
             nxt = make_tile(t_next);
-        for (; kt < T; kt += 6) { // at most 9 steps left; with CROSS the last three prefetch `nxt`
+        for (; !thin && kt < T; kt += 6) { // with CROSS the last three steps prefetch `nxt`
             refresh();
             step.template operator()<1, 1, false, true, false>(kt);
             if (kt + 1 < T) step.template operator()<0, 2, false, true, false>(kt + 1);
@@ -1078,6 +1172,17 @@ grouped_gemm_kernel(const KernelArgs args) {
             if (kt + 3 < T) step.template operator()<0, 1, false, true, false>(kt + 3);
             if (kt + 4 < T) step.template operator()<1, 2, false, true, false>(kt + 4);
             if (kt + 5 < T) step.template operator()<0, 0, false, true, false>(kt + 5);
+        }
+        if constexpr (kThin) {
+            for (; kt < T; kt += 6) {
+                refresh();
+                step_thin.template operator()<1, 1>(kt);
+                if (kt + 1 < T) step_thin.template operator()<0, 2>(kt + 1);
+                if (kt + 2 < T) step_thin.template operator()<1, 0>(kt + 2);
+                if (kt + 3 < T) step_thin.template operator()<0, 1>(kt + 3);
+                if (kt + 4 < T) step_thin.template operator()<1, 2>(kt + 4);
+                if (kt + 5 < T) step_thin.template operator()<0, 0>(kt + 5);
+            }
         }
         if constexpr (CROSS) {
             if (!cross_next)
