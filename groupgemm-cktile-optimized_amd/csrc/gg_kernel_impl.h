@@ -1077,6 +1077,16 @@ grouped_gemm_kernel(const KernelArgs args) {
         constexpr int SB_NEXT = (SB + 1) % 3;
         uint32_t rows_w = __builtin_amdgcn_readfirstlane(cur.rows);
         fresh_s(rows_w); // tested next to each row's branch
+        using chk = std::true_type;
+        const DmaSrc src_a1 = dma_src(A_OP{}, kt + 1, chk{}); // A(kt+1)
+        const DmaSrc src_b3 = dma_src(B_OP{}, kt + 3, chk{}); // B(kt+3)
+        const DmaSrc src_a2 = dma_src(A_OP{}, kt + 2, chk{}); // A(kt+2)
+        // DMA with its own M0 write and the SGPR wait states
+        auto dma_row = [&](uint32_t dst, auto b_op, auto j, const DmaSrc &d) {
+            sched_fence();
+            dma16(dst + j * 4096, dma_voff(b_op, j, d, chk{}), d.rs, d.so);
+            sched_fence();
+        };
         sfor<0, 8>([&](auto mi_) {
             constexpr int mi = decltype(mi_)::value;
             sfor<0, P::slots>([&](auto idx_) {
@@ -1102,11 +1112,11 @@ grouped_gemm_kernel(const KernelArgs args) {
                     sched_fence();
                 }
                 if constexpr (dk == 1)
-                    dma_now(a_dst[NX], A_OP{}, ic<dj>{}, kt + 1);
+                    dma_row(a_dst[NX], A_OP{}, ic<dj>{}, src_a1);
                 else if constexpr (dk == 2)
-                    dma_now(b_dst[SB], B_OP{}, ic<dj>{}, kt + 3);
+                    dma_row(b_dst[SB], B_OP{}, ic<dj>{}, src_b3);
                 else if constexpr (dk == 3)
-                    dma_now(a_dst[SA], A_OP{}, ic<dj>{}, kt + 2);
+                    dma_row(a_dst[SA], A_OP{}, ic<dj>{}, src_a2);
             });
             sched_fence();
             if (rows_w & (1u << mi)) {
@@ -1136,11 +1146,12 @@ grouped_gemm_kernel(const KernelArgs args) {
         refresh();
         const int  t_next = t + gridDim.x;
         const bool more   = t_next < total_units;
-        // A partial tile (kThin: this wave has row blocks without a valid output) runs its steps
-        // after the first as thin steps (step_thin) in a loop of their own; a full tile never
-        // enters it. Loops in sequence, not branches around whole steps, so the accumulators
-        // stay in place.
-        const bool thin = kThin && __builtin_amdgcn_readfirstlane(cur.rows) != 0xffu;
+        // A partial tile in which this wave has at most 4 row blocks with a valid output (kThin)
+        // runs its steps after the first as thin steps (step_thin) in a loop of their own; a
+        // full tile never enters it. (A thin step's memory operations do not overlap its MFMAs:
+        // with 5 or more rows it is no faster than a full step.) Loops in sequence, not branches
+        // around whole steps, so the accumulators stay in place.
+        const bool thin = kThin && __builtin_amdgcn_readfirstlane(cur.rows) <= 0xfu;
         if constexpr (CROSS) {
             // First step: stores the previous tile's accumulators while it overwrites them (to
             // nowhere for the first tile). Always the same code, so the accumulators never
