@@ -19,10 +19,10 @@ Prints ONE JSON line on stdout. Besides the driver's fields it carries:
                of the same workload on this host; a reported baseline only.
   clock_power  gfx clock (MHz) and socket power (W) sampled through amdsmi during a separate
                sustained window of the same launches after the timed region (--power-seconds,
-               default 1 s; the timed region itself runs without a sampling thread), its own
-               TFLOPS, and the dense peak scaled to the sampled clock. The MI355X is power-capped,
-               so the clock under a sustained GEMM sits well below 2.4 GHz; the reference records
-               the same two figures (scripts/power.py:1-9).
+               default 1 s; the timed region itself runs without a sampling thread) and that
+               window's TFLOPS; the reference records the same two figures (scripts/power.py:1-9).
+               "consistent" says whether the sampled clock could sustain the measured MFMA rate;
+               only then is the dense peak scaled to it reported.
 Human-readable progress goes to stderr.
 """
 from __future__ import annotations
@@ -184,11 +184,17 @@ def sustained_clock_power(be, sh, stream, flops, ms, seconds, peak):
     res["tflops"] = round(flops * n / (w_ms * 1e-3) / 1e12, 2)
     res["power_cap_w"] = sampler.power_cap_w
     mhz = res.get("gfx_mhz")
-    if mhz:
+    # The readings are only kept as measured when they could be true: the window's TFLOPS may not
+    # exceed the dense peak scaled to the sampled clock (peak x MHz / 2400). On this pool's boxes
+    # amdsmi's clock and power often do not follow the load (readings of a few hundred MHz under a
+    # full-rate GEMM); the effective clock over a launch comes from the GRBM cycle counters
+    # instead (rocprofv3 --pmc GRBM_GUI_ACTIVE, profiles/).
+    res["consistent"] = bool(mhz) and res["tflops"] <= peak * mhz / 2400.0
+    if res["consistent"]:
         at_clk = peak * mhz / 2400.0
         res["peak_at_clock_tflops"] = round(at_clk, 1)
         res["frac_at_clock"] = round(res["tflops"] / at_clk, 4)
-    res["source"] = "amdsmi: clock_info(GFX).clk, power_info.current_socket_power"
+    res["source"] = "amdsmi: clock_info(GFX).clk, power_info.current_socket_power, gpu_metrics current_gfxclks"
     return res
 
 

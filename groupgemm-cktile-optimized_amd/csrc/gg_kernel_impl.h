@@ -13,7 +13,11 @@
 //
 // Work decomposition
 //   * Output tile 256 x 256, K step 64. One workgroup = 4 waves, one per SIMD; wave (wm, wn)
-//     owns the 128 x 128 sub-tile rows wm*128.., cols wn*128.. as 8 x 8 MFMA tiles of 16 x 16.
+//     owns 8 x 8 MFMA blocks of 16 x 16: columns wn*128.., and the row blocks 2*mi + wm
+//     (interleaved, so the valid rows of a partial tile split evenly between wm = 0 and 1;
+//     contiguous rows wm*128.. for wgrad's transposed A).
+//   * A wave whose blocks in a partial tile hold at most 4 row blocks with a valid output
+//     skips the MFMAs of the others (thin K steps, forward layouts).
 //   * v_mfma_f32_16x16x32_{bf16,f16}. The w fragment is the first source and the x fragment
 //     the second, so each 16 x 16 accumulator holds C^T: lane l has row l%16 of the block and
 //     the four consecutive columns 4*(l/16)..+3, i.e. 8 contiguous output bytes.
