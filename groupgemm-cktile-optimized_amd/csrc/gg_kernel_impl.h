@@ -500,15 +500,6 @@ constexpr int plan_epi(int mi, int idx) {
 #endif
 constexpr bool kTailSkip = GG_TAIL_SKIP;
 
-// The row blocks (bit mi) of wave (wm, wn) that hold a valid output in a tile of m_valid rows and
-// n_valid columns: none when the wave's 128 columns (128 wn ..) are all past n_valid. Row block
-// mi of the wave is tile rows 16 (2 mi + wm) .. +16 when interleaved (ILV), 128 wm + 16 mi ..
-// otherwise.
-template <bool ILV> __device__ __forceinline__ uint32_t active_rows(int m_valid, int n_valid, int wm, int wn) {
-    const int nb_m = (m_valid + 15) >> 4; // 16-row blocks with a valid row
-    const int ra   = min(8, max(0, ILV ? (nb_m - wm + 1) >> 1 : nb_m - 8 * wm));
-    return n_valid > 128 * wn ? (1u << ra) - 1 : 0u;
-}
 
 // MODE: layout (forward, dgrad, wgrad: operand layouts and tile mapping) and input format.
 // CROSS: cross-tile pipeline (needs k_tiles >= kCrossMinSteps); otherwise every tile starts
@@ -756,7 +747,7 @@ grouped_gemm_kernel(const KernelArgs args) {
         }
         if constexpr (F8)
             tl.scale = args.x_scale[0] * args.w_scale[g];
-        tl.rows = __builtin_amdgcn_readfirstlane(active_rows<ILV>(tl.m_valid, tl.n_valid, wm, wn));
+        tl.rows = __builtin_amdgcn_readfirstlane(active_rows(ILV, tl.m_valid, tl.n_valid, wm, wn));
         return tl;
     };
     auto c_rsrc = [&](const Tile &tl) {

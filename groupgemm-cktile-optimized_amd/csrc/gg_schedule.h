@@ -65,6 +65,18 @@ GG_HD void band_coords(int local, int m_tiles, int n_tiles, int band, int *tm, i
     *tm                = b * band + (p - (p / h) * h);
 }
 
+// Partial tiles: the row blocks (bit mi) of wave (wm, wn) of the 2 x 2 wave grid that hold a
+// valid output in a tile of m_valid rows and n_valid columns; none when the wave's 128 columns
+// (128 wn ..) are all past n_valid. Row block mi of the wave is tile rows 16 (2 mi + wm) .. +16
+// when interleaved (ilv, a K-major A), 128 wm + 16 mi .. otherwise. The kernel skips the MFMAs of
+// the other row blocks (thin K steps).
+GG_HD uint32_t active_rows(bool ilv, int m_valid, int n_valid, int wm, int wn) {
+    const int nb_m = (m_valid + 15) >> 4; // 16-row blocks with a valid row
+    int       ra   = ilv ? (nb_m - wm + 1) >> 1 : nb_m - 8 * wm;
+    ra             = ra < 0 ? 0 : (ra > 8 ? 8 : ra);
+    return n_valid > 128 * wn ? (1u << ra) - 1 : 0u;
+}
+
 // Ceil division for non-negative values.
 GG_HD int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 

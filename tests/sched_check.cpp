@@ -6,7 +6,10 @@
 //     tiles of a full band touch at most `band` M-tiles and ceil(32 / band) + 1 N-tiles;
 //   * the whole kernel walk (workgroup w handles slots w, w + grid, ...; remap; locate_tile
 //     with its forward-only group hint) covers every (group, M-tile, N-tile) exactly once,
-//     with empty groups owning nothing, and each workgroup's logical tiles only increase.
+//     with empty groups owning nothing, and each workgroup's logical tiles only increase;
+//   * active_rows: for every tile size (1..256 valid rows and columns, both row mappings) each
+//     16 x 16 block that holds a valid output belongs to exactly one wave's active row blocks,
+//     and every active block holds a valid row (no MFMA skipped that a stored output needs).
 #include <cstdio>
 #include <cstdlib>
 #include <set>
@@ -117,7 +120,42 @@ static void check_walk(const std::vector<int64_t> &group_m, int64_t n, int grid,
           seen.size(), (long long)want);
 }
 
+// Blocks of the 256 x 256 tile: wave (wm, wn), row block mi -> tile rows, column blocks ni of
+// the wave -> columns 128 wn + 16 ni. A block with a valid output must be active in exactly one
+// wave; an active block must contain a valid row and a valid column of the wave.
+static void check_active_rows(bool ilv) {
+    for (int mv = 1; mv <= 256; ++mv)
+        for (int nv = 8; nv <= 256; nv += 8) {
+            std::vector<int> cover(16 * 16, 0);
+            for (int wm = 0; wm < 2; ++wm)
+                for (int wn = 0; wn < 2; ++wn) {
+                    const uint32_t rows = gg::active_rows(ilv, mv, nv, wm, wn);
+                    CHECK((rows & (rows + 1)) == 0 && rows <= 0xffu, "row mask not a prefix: %x", rows);
+                    for (int mi = 0; mi < 8; ++mi) {
+                        const int r0 = ilv ? 16 * (2 * mi + wm) : 128 * wm + 16 * mi;
+                        const bool act = (rows >> mi) & 1;
+                        if (act)
+                            CHECK(r0 < mv && 128 * wn < nv, "active block without valid output (ilv=%d m=%d n=%d wm=%d wn=%d mi=%d)",
+                                  ilv, mv, nv, wm, wn, mi);
+                        for (int ni = 0; ni < 8; ++ni) {
+                            const int c0 = 128 * wn + 16 * ni;
+                            if (act && c0 < nv)
+                                ++cover[(r0 / 16) * 16 + c0 / 16];
+                        }
+                    }
+                }
+            for (int rb = 0; rb < 16; ++rb)
+                for (int cb = 0; cb < 16; ++cb) {
+                    const bool valid = 16 * rb < mv && 16 * cb < nv;
+                    CHECK(cover[rb * 16 + cb] == (valid ? 1 : 0), "block (%d, %d) covered %d times (ilv=%d m=%d n=%d)",
+                          rb, cb, cover[rb * 16 + cb], ilv, mv, nv);
+                }
+        }
+}
+
 int main() {
+    check_active_rows(true);
+    check_active_rows(false);
     for (int n_xcd : {1, 8})
         for (int grid : {1, 8, 24, 100, 224, 256})
             for (int total = 1; total <= 1100; total += (total < 300 ? 1 : 37))
