@@ -17,7 +17,7 @@
 //     (interleaved, so the valid rows of a partial tile split evenly between wm = 0 and 1;
 //     contiguous rows wm*128.. for wgrad's transposed A).
 //   * A wave whose blocks in a partial tile hold at most 4 row blocks with a valid output
-//     skips the MFMAs of the others (thin K steps, forward layouts).
+//     skips the MFMAs of the others (thin K steps).
 //   * v_mfma_f32_16x16x32_{bf16,f16}. The w fragment is the first source and the x fragment
 //     the second, so each 16 x 16 accumulator holds C^T: lane l has row l%16 of the block and
 //     the four consecutive columns 4*(l/16)..+3, i.e. 8 contiguous output bytes.
@@ -517,10 +517,8 @@ grouped_gemm_kernel(const KernelArgs args) {
     // wm = 1 waves; contiguous (128 wm + 16 mi ..) for the MN-major A of wgrad.
     constexpr bool ILV    = !A_MN;
     constexpr int  A_BLK  = ILV ? 32 : 16; // tile rows between a wave's consecutive row blocks
-    // Partial tiles skip their empty row blocks in the forward layout. (dgrad and wgrad compute
-    // every block: with the row branches their instances stopped LLVM's AMDGPU backend with an
-    // "illegal VGPR to SGPR copy".)
-    constexpr bool kThin  = kTailSkip && LAYOUT == kFwd;
+    // Partial tiles skip their empty row blocks (thin K steps), in every layout.
+    constexpr bool kThin  = kTailSkip;
     using P = std::conditional_t<F8, Plan8<reads_per_frag(A_MN), reads_per_frag(B_MN)>,
                                  Plan<reads_per_frag(A_MN), reads_per_frag(B_MN)>>;
     static_assert(!(F8 && F16), "fp8 writes bf16");
