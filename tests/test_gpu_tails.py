@@ -149,3 +149,48 @@ def test_fp8_dgrad_tails(pkg):
         refs.append(go[row:row + m].float() @ w[g].float())
         row += m
     _check(out, torch.cat(refs), "fp8 dgrad")
+
+
+def _run_plan(pkg, kind, dt, n, k, gm, go, other, out, **kw):
+    s = torch.cuda.current_stream(DEV).cuda_stream
+    plan = pkg.BackwardPlan(kind, dt, n, k, gm, go.data_ptr(), other.data_ptr(), out.data_ptr(), s, **kw)
+    plan.run(s)
+    torch.cuda.synchronize(DEV)
+    detail = plan.detail()
+    plan.release()
+    return detail
+
+
+def test_wgrad_cross_tile_tails(pkg):
+    # > 256 tiles and every group >= 4 K steps of 64 rows: the cross-tile variant, with a 8-row
+    # tail (N = 2056 output rows, contiguous row blocks) and an 8-column tail (K = 2056)
+    gm, n, k = [300, 517, 640, 1000], 2056, 2056
+    print(f"[tails] wgrad cross-tile: N={n} K={k} group_m={gm}", flush=True)
+    go, x = _rand((sum(gm), n), 17), _rand((sum(gm), k), 18)
+    out = torch.full((len(gm), n, k), float("nan"), dtype=torch.bfloat16, device=DEV)
+    detail = _run_plan(pkg, "wgrad", pkg.DType.BF16, n, k, gm, go, x, out)
+    assert "cross-tile" in detail, detail
+    row = 0
+    for g, m in enumerate(gm):
+        ref = go[row:row + m].float().t().contiguous() @ x[row:row + m].float()
+        _check(out[g], ref, f"wgrad cross-tile group {g}")
+        row += m
+
+
+def test_fp8_wgrad_cross_tile_tails(pkg):
+    # fp8 K steps are 128 rows: every group >= 4 steps; N = K = 2064 (16-row and 16-column tails)
+    gm, n, k = [600, 1000, 513, 1400], 2064, 2064
+    print(f"[tails] fp8 wgrad cross-tile: N={n} K={k} group_m={gm}", flush=True)
+    go = _rand((sum(gm), n), 19).to(torch.float8_e5m2)
+    x = _rand((sum(gm), k), 20).to(torch.float8_e4m3fn)
+    gs = torch.tensor([0.5], dtype=torch.float32, device=DEV)
+    xs = torch.linspace(0.5, 1.5, len(gm), dtype=torch.float32, device=DEV)
+    out = torch.full((len(gm), n, k), float("nan"), dtype=torch.bfloat16, device=DEV)
+    detail = _run_plan(pkg, "wgrad", pkg.DType.FP8_E5M2, n, k, gm, go, x, out, other_dtype=pkg.DType.FP8_E4M3,
+                       grad_scale=gs.data_ptr(), other_scale=xs.data_ptr())
+    assert "cross-tile" in detail, detail
+    row = 0
+    for g, m in enumerate(gm):
+        ref = (go[row:row + m].float().t().contiguous() @ x[row:row + m].float()) * (0.5 * float(xs[g]))
+        _check(out[g], ref, f"fp8 wgrad cross-tile group {g}")
+        row += m
