@@ -37,6 +37,7 @@ struct gg_plan {
     const int64_t      *d_lens      = nullptr;
     const int64_t      *d_offs      = nullptr;
     gg::TableHeader    *d_header    = nullptr; // follows the table in the d_groups allocation
+    bool                in_kernel_table = false; // the GEMM builds the table (no table launch)
     float              *d_ws        = nullptr; // split-K partial sums (args.ws)
     int64_t             in_rows     = 0;       // device-size plans: rows of the inputs
 };
@@ -708,6 +709,16 @@ int gg_prepare_device_lens_op(int op, int a_dtype, int b_dtype, int group_num, i
         ka.total_tiles = 0;
         ka.d_total     = &plan->d_header->total_tiles;
     }
+    // At most kInKernelTableGroups groups: the GEMM builds the table itself (one group per lane of
+    // every wave) and writes the header, so a run is one launch.
+    if (group_num <= gg::kInKernelTableGroups) {
+        plan->in_kernel_table = true;
+        ka.d_lens             = group_lens;
+        ka.d_offs             = group_offs;
+        ka.lens_rows          = total_m;
+        ka.d_header           = plan->d_header;
+        ka.d_total            = nullptr;
+    }
     const int n_xcd = xcd_count(prop);
     ka.n_xcd        = plan->grid % n_xcd == 0 ? n_xcd : 1;
     plan->detail = "mi355x " + what + " persistent 256x256x" + std::to_string(f8 ? 128 : 64) + " grid=" +
@@ -715,7 +726,7 @@ int gg_prepare_device_lens_op(int op, int a_dtype, int b_dtype, int group_num, i
                    (op == GG_OP_WGRAD ? std::to_string(plan->total_tiles) : std::string("device")) +
                    " xcd=" + std::to_string(ka.n_xcd) +
                    (gg::uses_cross_tile(ka, plan->grid, plan->mode) ? " cross-tile" : " per-tile") +
-                   " (device group sizes)";
+                   (plan->in_kernel_table ? " (device group sizes, in-kernel table)" : " (device group sizes)");
     *plan_out = plan;
     return GG_OK;
 }
@@ -725,12 +736,14 @@ int gg_run(const gg_plan *plan, void *stream) {
         return fail(GG_ERR_INVALID, "plan is null");
     const hipStream_t s = static_cast<hipStream_t>(stream);
     if (plan->device_lens && plan->d_groups != nullptr) {
-        hipError_t e = gg::launch_build_group_table(plan->d_lens, plan->d_offs, plan->group_num,
-                                                    plan->in_rows, plan->args.n_tiles,
-                                                    plan->d_groups, plan->d_header, s,
-                                                    plan->args.m_out);
-        if (e != hipSuccess)
-            return hip_fail(e, "group table launch");
+        hipError_t e = hipSuccess;
+        if (!plan->in_kernel_table) {
+            e = gg::launch_build_group_table(plan->d_lens, plan->d_offs, plan->group_num, plan->in_rows,
+                                             plan->args.n_tiles, plan->d_groups, plan->d_header, s,
+                                             plan->args.m_out);
+            if (e != hipSuccess)
+                return hip_fail(e, "group table launch");
+        }
         e = gg::launch_grouped_gemm(plan->args, plan->dtype == GG_DTYPE_FP16, plan->grid, s, plan->mode);
         if (e != hipSuccess)
             return hip_fail(e, "grouped GEMM launch");

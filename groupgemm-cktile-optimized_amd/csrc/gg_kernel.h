@@ -19,6 +19,18 @@ enum InFormat : int {
 };
 constexpr int make_mode(int layout, int format) { return layout + 4 * format; }
 
+// Header of a device-built group table (follows the group_num entries).
+struct TableHeader {
+    int total_tiles; // tiles over all groups (0 if the count overflowed)
+    int first_bad;   // first group whose length or offset was out of range, -1 if none
+    int overflow;    // 1 if the tile count exceeded 32 bits (nothing is computed then)
+    int reserved;
+};
+
+// Device-resident group sizes of at most this many groups: the grouped GEMM builds the group
+// table itself (one group per lane of every wave), with no separate table launch.
+constexpr int kInKernelTableGroups = 64;
+
 // Kernel arguments, passed by value in the kernarg segment. Everything a workgroup needs
 // to find its tiles: the device group table plus the problem-wide sizes.
 // Kernel terms: out (rows x N) = A (rows x K) B^T (N x K) per group, K the contraction.
@@ -48,14 +60,13 @@ struct KernelArgs {
                                    // then total_tiles holds it
     int               splits;      // split-K: K ranges per tile (1 = none; per-tile variant only)
     float            *ws;          // split-K: fp32 partial sums, splits * total_tiles * 256 KB
-};
-
-// Header of a device-built group table (follows the group_num entries).
-struct TableHeader {
-    int total_tiles; // tiles over all groups (0 if the count overflowed)
-    int first_bad;   // first group whose length or offset was out of range, -1 if none
-    int overflow;    // 1 if the tile count exceeded 32 bits (nothing is computed then)
-    int reserved;
+    // In-kernel group table (device-resident sizes, group_num <= kInKernelTableGroups): every
+    // wave builds its table from lens / offs at its start, with the rules of
+    // build_group_table_kernel, and workgroup 0 writes the header. Null: the table in `groups`.
+    const int64_t    *d_lens;      // [group_num] rows per group (device)
+    const int64_t    *d_offs;      // [group_num + 1] first rows, or null for back-to-back groups
+    int64_t           lens_rows;   // rows of the inputs: groups outside [0, lens_rows) are invalid
+    TableHeader      *d_header;    // written by workgroup 0: tile count and the first bad group
 };
 
 // Whether a launch takes the cross-tile pipeline variant (several tiles per workgroup, enough

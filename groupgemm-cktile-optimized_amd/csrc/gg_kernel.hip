@@ -53,15 +53,6 @@ __global__ void __launch_bounds__(256) split_reduce_kernel(const KernelArgs args
 // Group table from device-resident group sizes (one wave, groups in chunks of 64).
 // The same facts as the host's build_group_table: first row, rows and first tile per group.
 // ---------------------------------------------------------------------------------------
-__device__ __forceinline__ int64_t wave_inclusive_sum(int64_t v, int lane) {
-    for (int d = 1; d < 64; d <<= 1) {
-        const int64_t u = __shfl_up(v, d, 64);
-        if (lane >= d)
-            v += u;
-    }
-    return v;
-}
-
 __global__ void __launch_bounds__(64)
 build_group_table_kernel(const int64_t *lens, const int64_t *offs, int group_num, int64_t total_m,
                          int n_tiles, GroupEntry *table, TableHeader *header, int out_rows) {
@@ -154,7 +145,7 @@ bool uses_cross_tile(const KernelArgs &args, int grid, int mode) {
     // next tile inside the current one)
     const int steps = mode_layout(mode) == kWgrad ? args.min_steps : args.k_tiles;
     return kCrossAllowed && args.splits <= 1 && steps >= kCrossMinSteps &&
-           (args.d_total != nullptr || args.total_tiles > grid);
+           (args.d_total != nullptr || args.d_lens != nullptr || args.total_tiles > grid);
 }
 
 

@@ -493,6 +493,59 @@ constexpr int plan_epi(int mi, int idx) {
     return (mi < 7 && idx % 4 == 2) ? (idx - 2) / 4 : -1;
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ int64_t wave_inclusive_sum(int64_t v, int lane) {
+    for (int d = 1; d < 64; d <<= 1) {
+        const int64_t u = __shfl_up(v, d, 64);
+        if (lane >= d)
+            v += u;
+    }
+    return v;
+}
+
+// One group of an in-kernel group table: lane g holds group g (g < group_num <= 64).
+struct LaneGroup {
+    int64_t row0;  // first row (0 for an invalid group)
+    int     m;     // rows (0 for an invalid group)
+    int     tile0; // first logical tile
+    int     tiles; // tiles the group owns
+};
+
+// The group table of device-resident sizes for at most 64 groups, one group per lane, by the
+// rules of build_group_table_kernel: a negative length, or rows outside [0, total_m), make a
+// group invalid (no rows; forward / dgrad: no tiles; wgrad: its out_rows x N tiles, written as
+// zeros). Returns the lane's group; *total (uniform) is the tile count, 0 with *overflow set when
+// it exceeds 32 bits; *first_bad the first invalid group or -1.
+__device__ __forceinline__ LaneGroup lane_group_table(const int64_t *lens, const int64_t *offs, int group_num,
+                                                      int64_t total_m, int n_tiles, int out_rows, int lane,
+                                                      int *total, int *first_bad, int *overflow) {
+    const bool live = lane < group_num;
+    int64_t    m    = live ? lens[lane] : 0;
+    bool       ok   = m >= 0 && m <= INT32_MAX;
+    if (!ok)
+        m = 0;
+    const int64_t rows_incl = wave_inclusive_sum(m, lane);
+    const int64_t row0      = offs != nullptr ? (live ? offs[lane] : 0) : rows_incl - m;
+    ok                      = ok && row0 >= 0 && row0 <= total_m && m <= total_m - row0;
+    const int64_t tiles     = out_rows > 0 ? (live ? cdiv(out_rows, kTileM) * n_tiles : 0)
+                                           : (ok ? cdiv(m, kTileM) * n_tiles : 0);
+    const int64_t tiles_incl = wave_inclusive_sum(tiles, lane);
+    // the total from lane 63, read into scalar registers (a shuffle would leave it in a VGPR and
+    // every value derived from it, the tile loop's bounds included, with it)
+    const int64_t all = static_cast<int64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(tiles_incl), 63))) |
+                        (static_cast<int64_t>(__builtin_amdgcn_readlane(static_cast<int>(tiles_incl >> 32), 63)) << 32);
+    const uint64_t bad = __ballot(live && !ok);
+    *first_bad = bad != 0 ? static_cast<int>(__builtin_ctzll(bad)) : -1;
+    *overflow  = all > INT32_MAX ? 1 : 0;
+    *total     = all > INT32_MAX ? 0 : static_cast<int>(all);
+    LaneGroup lg;
+    lg.row0  = ok ? row0 : 0;
+    lg.m     = ok ? static_cast<int>(m) : 0;
+    lg.tile0 = static_cast<int>(min<int64_t>(tiles_incl - tiles, INT32_MAX));
+    lg.tiles = static_cast<int>(min<int64_t>(tiles, INT32_MAX));
+    return lg;
+}
+
 // Partial tiles: a wave skips the MFMAs of its 16-row blocks that hold no valid output (1), or
 // computes every block (0).
 #ifndef GG_TAIL_SKIP
@@ -531,10 +584,26 @@ grouped_gemm_kernel(const KernelArgs args) {
     const int wm = wave >> 1, wn = wave & 1;
     const int K = args.k, N = args.n;
     int       T = args.k_tiles; // K steps of the current tile (per group for wgrad)
+    // In-kernel group table (device-resident sizes, at most 64 groups): every wave builds it,
+    // lane g holding group g; workgroup 0 reports the tile count and the first invalid group.
+    const bool in_kernel_table = args.d_lens != nullptr;
+    LaneGroup  lgrp{0, 0, 0, 0};
+    int        lg_total = 0;
+    if (in_kernel_table) {
+        int first_bad, overflow;
+        lgrp = lane_group_table(args.d_lens, args.d_offs, args.group_num, args.lens_rows, args.n_tiles,
+                                LAYOUT == kWgrad ? args.m_out : 0, lane, &lg_total, &first_bad, &overflow);
+        if (blockIdx.x == 0 && threadIdx.x == 0) {
+            args.d_header->total_tiles = lg_total;
+            args.d_header->first_bad   = first_bad;
+            args.d_header->overflow    = overflow;
+            args.d_header->reserved    = 0;
+        }
+    }
     // Tile count: from the kernel arguments, or from a group table built on the device.
-    const int total_tiles = args.d_total != nullptr
-                                ? __builtin_amdgcn_readfirstlane(*args.d_total)
-                                : args.total_tiles;
+    const int total_tiles = in_kernel_table         ? lg_total
+                            : args.d_total != nullptr ? __builtin_amdgcn_readfirstlane(*args.d_total)
+                                                      : args.total_tiles;
     // Work units: a tile, or with split-K (per-tile variant only) one K range of a tile; unit
     // u = split * total_tiles + tile.
     const int splits      = CROSS ? 1 : args.splits;
@@ -697,10 +766,23 @@ grouped_gemm_kernel(const KernelArgs args) {
         // split-K: one unit per workgroup, no L2 sharing across rounds to arrange
         const int split = splits > 1 ? t / total_tiles : 0;
         const int L     = splits > 1 ? t - split * total_tiles : xcd_remap(t, total_tiles, gridDim.x, args.n_xcd);
-        int       tm, tn;
-        locate_tile(L, args.groups, args.group_num, args.n_tiles, args.band, &g, &tm, &tn,
-                    LAYOUT == kWgrad ? args.m_out : 0);
-        const GroupEntry ge = args.groups[g];
+        int        tm, tn;
+        GroupEntry ge;
+        if (in_kernel_table) {
+            // the one lane whose group owns logical tile L
+            const uint64_t hit = __ballot(lane < args.group_num && lgrp.tile0 <= L && L - lgrp.tile0 < lgrp.tiles);
+            g                  = __builtin_amdgcn_readfirstlane(static_cast<int>(__builtin_ctzll(hit)));
+            ge.row0  = static_cast<int64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(lgrp.row0), g))) |
+                      (static_cast<int64_t>(__builtin_amdgcn_readlane(static_cast<int>(lgrp.row0 >> 32), g)) << 32);
+            ge.m     = __builtin_amdgcn_readlane(lgrp.m, g);
+            ge.tile0 = __builtin_amdgcn_readlane(lgrp.tile0, g);
+            const int m_tiles = ((LAYOUT == kWgrad ? args.m_out : ge.m) + kTileM - 1) / kTileM;
+            band_coords(L - ge.tile0, m_tiles, args.n_tiles, args.band, &tm, &tn);
+        } else {
+            locate_tile(L, args.groups, args.group_num, args.n_tiles, args.band, &g, &tm, &tn,
+                        LAYOUT == kWgrad ? args.m_out : 0);
+            ge = args.groups[g];
+        }
         const uint8_t   *xa = static_cast<const uint8_t *>(args.x); // A storage (bytes)
         const uint8_t   *wb = static_cast<const uint8_t *>(args.w); // B storage (bytes)
         Tile             tl;

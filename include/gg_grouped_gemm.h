@@ -150,8 +150,9 @@ int gg_plan_tiles(const gg_plan *plan);
  *   total_m:    rows of x and out. A group with a negative length, or rows outside
  *               [0, total_m), gets no work (its rows are not written) and is reported by
  *               gg_plan_device_status.
- * Each gg_run is two launches: a one-wave table build, then the grouped GEMM. k == 0 zeroes
- * all total_m rows of out. Same shape requirements as gg_prepare.
+ * With group_num <= 64 each gg_run is one launch (the grouped GEMM builds the group table
+ * itself); with more groups it is two: a one-wave table build, then the grouped GEMM. k == 0
+ * zeroes all total_m rows of out. Same shape requirements as gg_prepare.
  */
 int gg_prepare_device_lens(int dtype, int group_num, int64_t total_m, int64_t n, int64_t k,
                            const int64_t *group_lens, const int64_t *group_offs, const void *x,
