@@ -372,3 +372,69 @@ def test_device_sizes_backward_bad_sizes_and_wrappers(pkg):
     assert ((gx[300:800].float() - ref).abs() <= ATOL + RTOL * ref.abs()).all()
     with pytest.raises(pkg.GGError):
         pkg.grouped_gemm_dgrad(go, w, torch.tensor([300, 500, 900], dtype=torch.int64, device=DEV))
+
+
+# ---- the in-kernel table (at most 64 groups) and the table kernel (more) --------------------
+@pytest.mark.parametrize("b", [64, 65, 130])
+def test_table_paths_match_host_sizes(pkg, b):
+    """Up to 64 groups the grouped GEMM builds the group table itself (one launch); above, a
+    table kernel runs first. Both give the bits of the host-size plan, with ragged and empty
+    groups, and report the tile count."""
+    gen = torch.Generator().manual_seed(b)
+    gm = torch.randint(0, 700, (b,), generator=gen).tolist()
+    for g in range(0, b, 9):
+        gm[g] = 0
+    n, k = 520, 448
+    x, w = _inputs(pkg, 0, sum(gm), b, n, k, seed_x=60 + b, seed_w=61 + b)
+    lens = torch.tensor(gm, dtype=torch.int64, device=DEV)
+    print(f"[device-lens] {b} groups, {sum(gm)} rows: N={n} K={k}", flush=True)
+    plan = DevicePlan(pkg, 0, x, w, lens)
+    detail = plan.be.detail()
+    assert ("in-kernel table" in detail) == (b <= 64), detail
+    st, tiles, msg = plan.run()
+    assert st == pkg.GG_OK, msg
+    assert tiles == sum((m + 255) // 256 for m in gm) * ((n + 255) // 256), (tiles, detail)
+    host = _host_plan_out(pkg, 0, x, w, gm)
+    assert torch.equal(plan.out.view(torch.int16), host.view(torch.int16)), detail
+    plan.close()
+
+
+@pytest.mark.parametrize("b", [64, 65])
+def test_table_paths_report_bad_sizes(pkg, b):
+    """Both table paths name the first group whose rows do not fit, and compute the others."""
+    gm = [40] * b
+    gm[b - 3] = -1
+    total = 40 * (b - 1)
+    x, w = _inputs(pkg, 0, total, b, 264, 128, seed_x=70, seed_w=71)
+    plan = DevicePlan(pkg, 0, x, w, torch.tensor(gm, dtype=torch.int64, device=DEV))
+    st, _, msg = plan.run()
+    assert st == pkg.GG_ERR_INVALID and f"group {b - 3}" in msg, msg
+    _check_group(x, w, plan.out, 0, 0, 40)
+    _check_group(x, w, plan.out, b - 1, 40 * (b - 2), 40)
+    plan.close()
+
+
+@pytest.mark.parametrize("kind", ["dgrad", "wgrad"])
+def test_table_kernel_backward_matches_host_sizes(pkg, kind):
+    """dgrad / wgrad with more than 64 groups (the table kernel path) give the host plan's bits."""
+    gen = torch.Generator().manual_seed(80)
+    gm = torch.randint(0, 300, (70,), generator=gen).tolist()
+    gm[5] = 0
+    n, k = 264, 392
+    rows = sum(gm)
+    go = torch.randn((rows, n), generator=gen).to(torch.bfloat16).to(DEV)
+    other = torch.randn((len(gm), n, k) if kind == "dgrad" else (rows, k), generator=gen).to(torch.bfloat16).to(DEV)
+    shape = (rows, k) if kind == "dgrad" else (len(gm), n, k)
+    out = torch.full(shape, float("nan"), dtype=torch.bfloat16, device=DEV)
+    lens = torch.tensor(gm, dtype=torch.int64, device=DEV)
+    plan = pkg.DeviceLensPlan(pkg.OP_DGRAD if kind == "dgrad" else pkg.OP_WGRAD, pkg.DType.BF16, pkg.DType.BF16,
+                              len(gm), rows, n, k, lens.data_ptr(), 0, go.data_ptr(), other.data_ptr(),
+                              out.data_ptr(), _stream(), 0, 0)
+    plan.run(_stream())
+    st, _, msg = plan.status(_stream())
+    detail = plan.detail()
+    plan.release()
+    assert st == pkg.GG_OK, msg
+    assert "in-kernel table" not in detail, detail
+    host = _host_backward(pkg, kind, None, gm, n, k, go, other, None, None)
+    assert torch.equal(out.view(torch.int16), host.view(torch.int16)), f"bits differ from host plan ({detail})"
