@@ -570,8 +570,10 @@ grouped_gemm_kernel(const KernelArgs args) {
     // wm = 1 waves; contiguous (128 wm + 16 mi ..) for the MN-major A of wgrad.
     constexpr bool ILV    = !A_MN;
     constexpr int  A_BLK  = ILV ? 32 : 16; // tile rows between a wave's consecutive row blocks
-    // Partial tiles skip their empty row blocks (thin K steps), in every layout.
-    constexpr bool kThin  = kTailSkip;
+    // Partial tiles skip their empty row blocks (thin K steps), in every layout, in the cross-tile
+    // variant: with one tile per workgroup (the per-tile variant's usual case) the full tiles set
+    // the launch time whatever the partial ones save, and the per-tile instances stay smaller.
+    constexpr bool kThin  = kTailSkip && CROSS;
     using P = std::conditional_t<F8, Plan8<reads_per_frag(A_MN), reads_per_frag(B_MN)>,
                                  Plan<reads_per_frag(A_MN), reads_per_frag(B_MN)>>;
     static_assert(!(F8 && F16), "fp8 writes bf16");
