@@ -1,10 +1,11 @@
 """Partial tiles on the GPU: every residue of a tile's valid rows and columns, in every layout.
 
-A tile with fewer than 256 valid rows or columns skips the MFMAs of its 16 x 16 blocks that hold
-no valid output, and the waves of a K-major A take interleaved 16-row blocks (wave wm's block mi
-is tile rows 16 (2 mi + wm) ..). These tests cover the row counts 1 .. 256 at every residue mod
-32 (both waves' shares, a wave with no block at all), column tails of 8 .. 248, and both kernel
-variants (per-tile: one tile per workgroup; cross-tile: several tiles per workgroup, where a
+The waves of a K-major A take interleaved 16-row blocks (wave wm's block mi is tile rows
+16 (2 mi + wm) ..), and in the cross-tile variant a tile with at most 128 valid rows (or a wave
+whose columns are all past N) skips the MFMAs of its row blocks that hold no valid output (thin
+K steps). These tests cover the row counts 1 .. 256 at every residue mod 32 (both waves' shares,
+a wave with no block at all), column tails of 8 .. 248, and both kernel variants (per-tile: one
+tile per workgroup, every block computed; cross-tile: several tiles per workgroup, where a
 partial tile's stale accumulators must never reach the next tile's stores), for the forward,
 dgrad, wgrad, fp8, split-K and device-size paths.
 
