@@ -117,6 +117,7 @@ void fill_args(gg_plan *plan, int n_xcd) {
     a.w_scale   = nullptr;
     a.splits    = 1;
     a.ws        = nullptr;
+    a.tile_n    = gg::kTileN;
 }
 
 // Split-K for problems whose tiles cannot fill the GPU (fewer than half as many tiles as CUs):
@@ -154,6 +155,37 @@ int choose_splits(int tiles, int k_tiles, int cus) {
         }
     }
     return cost <= (1.0 - kMinSplitGain) * unsplit ? best : 1;
+}
+
+// Narrow tiles (256 x 224) for a forward plan of one round that leaves CUs idle: when the plan is
+// not split and the 224-wide tiling still fits in one round, it gives more workgroups 7/8 of a
+// tile each (1 x 2048 x 7168: 224 tiles of 256 x 256 on 256 CUs, 256 tiles of 256 x 224). The
+// group table is rebuilt for the narrow tile count. GG_NARROW=0 in the environment turns this
+// off.
+int use_narrow_tiles(gg_plan *plan, const int64_t *group_m, const hipDeviceProp_t &prop, hipStream_t s) {
+    gg::KernelArgs &a   = plan->args;
+    const char     *env = std::getenv("GG_NARROW");
+    if ((env != nullptr && std::atoi(env) == 0) || a.splits > 1 || plan->total_tiles >= prop.multiProcessorCount)
+        return GG_OK;
+    const int64_t               n_tiles = gg::cdiv(plan->n, gg::kNarrowTileN);
+    std::vector<gg::GroupEntry> table(static_cast<size_t>(plan->group_num));
+    const int64_t tiles = gg::build_group_table(group_m, plan->group_num, n_tiles, table.data());
+    if (tiles <= plan->total_tiles || tiles > prop.multiProcessorCount)
+        return GG_OK;
+    hipError_t e = hipMemcpyAsync(plan->d_groups, table.data(), table.size() * sizeof(gg::GroupEntry),
+                                  hipMemcpyHostToDevice, s);
+    if (e == hipSuccess)
+        e = hipStreamSynchronize(s);
+    if (e != hipSuccess)
+        return hip_fail(e, "narrow group table upload");
+    plan->total_tiles = static_cast<int>(tiles);
+    plan->grid        = plan->total_tiles;
+    a.total_tiles     = plan->total_tiles;
+    a.n_tiles         = static_cast<int>(n_tiles);
+    a.tile_n          = gg::kNarrowTileN;
+    const int n_xcd   = xcd_count(prop);
+    a.n_xcd           = plan->grid % n_xcd == 0 ? n_xcd : 1;
+    return GG_OK;
 }
 
 // Picks the plan's split count (plan->args filled, k_tiles set) and allocates the partial sums.
@@ -256,7 +288,11 @@ int gg_prepare(int dtype, int group_num, int64_t n, int64_t k, const int64_t *gr
             free_plan(plan);
             return GG_ERR_HIP;
         }
-        plan->detail      = "mi355x persistent 256x256x64 " +
+        if (use_narrow_tiles(plan, group_m, prop, s) != GG_OK) {
+            free_plan(plan);
+            return GG_ERR_HIP;
+        }
+        plan->detail      = "mi355x persistent 256x" + std::to_string(a.tile_n) + "x64 " +
                        std::string(dtype == GG_DTYPE_BF16 ? "bf16" : "fp16") +
                        " grid=" + std::to_string(plan->grid) +
                        " tiles=" + std::to_string(plan->total_tiles) +

@@ -11,10 +11,17 @@ namespace gg {
 
 template <bool F16, int MODE>
 void launch_mode(const KernelArgs &args, bool cross, dim3 g, dim3 b, hipStream_t stream) {
-    if (cross)
+    if (cross) {
         hipLaunchKernelGGL((grouped_gemm_kernel<F16, true, MODE>), g, b, 0, stream, args);
-    else
-        hipLaunchKernelGGL((grouped_gemm_kernel<F16, false, MODE>), g, b, 0, stream, args);
+        return;
+    }
+    if constexpr (MODE == make_mode(kFwd, kIn16)) {
+        if (args.tile_n == kNarrowTileN) {
+            hipLaunchKernelGGL((grouped_gemm_kernel<F16, false, MODE, true>), g, b, 0, stream, args);
+            return;
+        }
+    }
+    hipLaunchKernelGGL((grouped_gemm_kernel<F16, false, MODE>), g, b, 0, stream, args);
 }
 
 // part -> (fp16 MFMA, mode); the dispatch's switch in gg_kernel.hip covers the same 14 pairs

@@ -67,6 +67,8 @@ struct KernelArgs {
     const int64_t    *d_offs;      // [group_num + 1] first rows, or null for back-to-back groups
     int64_t           lens_rows;   // rows of the inputs: groups outside [0, lens_rows) are invalid
     TableHeader      *d_header;    // written by workgroup 0: tile count and the first bad group
+    int               tile_n;      // output columns per tile: kTileN, or kNarrowTileN (per-tile
+                                   // 16-bit forward plans of one round; n_tiles counts these)
 };
 
 // Whether a launch takes the cross-tile pipeline variant (several tiles per workgroup, enough

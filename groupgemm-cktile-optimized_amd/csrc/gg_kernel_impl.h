@@ -557,7 +557,12 @@ constexpr bool kTailSkip = GG_TAIL_SKIP;
 // MODE: layout (forward, dgrad, wgrad: operand layouts and tile mapping) and input format.
 // CROSS: cross-tile pipeline (needs k_tiles >= kCrossMinSteps); otherwise every tile starts
 // with a prologue and ends with the LDS-staged epilogue.
-template <bool F16, bool CROSS, int MODE>
+// NARROW (per-tile forward only): tiles of 256 x 224 instead of 256 x 256, for one-round problems
+// whose 256-wide tiles leave CUs idle (1 x 2048 x 7168: 224 tiles of 256 x 256, 256 of 256 x 224).
+// Each wave takes 7 column blocks (columns 112 wn + 16 ni); the 8th block's MFMAs are compiled
+// out, and the memory schedule is unchanged: the B DMAs of rows 224-255 fall outside the tile's
+// bounded resource (zeros, no traffic), and the LDS epilogue drops chunks past n_valid.
+template <bool F16, bool CROSS, int MODE, bool NARROW = false>
 __global__ void __launch_bounds__(kThreads, 1) __attribute__((amdgpu_waves_per_eu(1, 1)))
 grouped_gemm_kernel(const KernelArgs args) {
     constexpr bool A_MN   = mode_a_mn(MODE), B_MN = mode_b_mn(MODE);
@@ -568,6 +573,10 @@ grouped_gemm_kernel(const KernelArgs args) {
     // Row blocks of a wave: interleaved (wave wm's block mi is tile rows 16 (2 mi + wm) ..) when A
     // is K-major, so that the valid rows of a partial tile split evenly between the wm = 0 and
     // wm = 1 waves; contiguous (128 wm + 16 mi ..) for the MN-major A of wgrad.
+    static_assert(!NARROW || (!CROSS && MODE == make_mode(kFwd, kIn16)), "narrow tiles: per-tile 16-bit forward");
+    constexpr int  TN     = NARROW ? kNarrowTileN : kTileN; // output columns per tile
+    constexpr int  WCOLS  = TN / 2;                          // columns per wave (wn)
+    constexpr int  NBLK   = WCOLS / 16;                      // column blocks per wave with MFMAs
     constexpr bool ILV    = !A_MN;
     constexpr int  A_BLK  = ILV ? 32 : 16; // tile rows between a wave's consecutive row blocks
     // Partial tiles skip their empty row blocks (thin K steps), in every layout, in the cross-tile
@@ -675,7 +684,7 @@ grouped_gemm_kernel(const KernelArgs args) {
                         (((F8 ? 2 * fr_q + (kh ^ (fr_q & 1)) : kh * 4 + fr_q) ^ (fr_row & 7)) * 16);
         const int mn  = (lane >> 4) * (F8 ? 8192 : 4096) + (lane & 15) * 8 + (kh ? -128 : 128) * (fr_q & 1);
         frag_a[kh]    = A_MN ? wm * 1024 + mn : wm * (ILV ? 16 : 128) * kRowBytes + off;
-        frag_b[kh]    = B_MN ? wn * 1024 + mn : wn * 128 * kRowBytes + off;
+        frag_b[kh]    = B_MN ? wn * 1024 + mn : wn * WCOLS * kRowBytes + off;
     });
 
     // Register epilogue: in store s = 2h + half of a 16-row block, lane l writes 16 bytes of
@@ -788,8 +797,8 @@ grouped_gemm_kernel(const KernelArgs args) {
         const uint8_t   *xa = static_cast<const uint8_t *>(args.x); // A storage (bytes)
         const uint8_t   *wb = static_cast<const uint8_t *>(args.w); // B storage (bytes)
         Tile             tl;
-        tl.n_valid         = min(kTileN, N - tn * kTileN);
-        const int64_t col0 = static_cast<int64_t>(tn) * kTileN;
+        tl.n_valid         = min(TN, N - tn * TN);
+        const int64_t col0 = static_cast<int64_t>(tn) * TN;
         tl.o0a = tl.o0b = 0;
         // K range of the unit: steps [k0, k1) of k_tiles, balanced over the splits
         const int k0 = split * args.k_tiles / splits, k1 = (split + 1) * args.k_tiles / splits;
@@ -1005,10 +1014,10 @@ grouped_gemm_kernel(const KernelArgs args) {
         {
             int row = wm * (ILV ? 16 : 128) + (lane & 15);
             fresh_v(row);
-            const int col = wn * 128 + (lane >> 4) * 4;
+            const int col = wn * WCOLS + (lane >> 4) * 4;
             const int off = row * kCStride + col * 2;
             sfor<0, 8>([&](auto mi) {
-                sfor<0, 8>([&](auto ni) {
+                sfor<0, NBLK>([&](auto ni) { // narrow tiles: the 8th block is another wave's columns
                     asm volatile("" : "+a"(acc[mi][ni]));
                     f32x4 v = acc[mi][ni];
                     if constexpr (F8)
@@ -1076,7 +1085,9 @@ grouped_gemm_kernel(const KernelArgs args) {
     auto row_mfma = [&]<int SA, bool FIRST>(auto mi_, auto idx_) {
         constexpr int mi = decltype(mi_)::value, idx = decltype(idx_)::value;
         constexpr int kh = idx / 8, ni = idx % 8; // fp8: one MFMA per (mi, ni), kh = 0
-        if constexpr (F8) {
+        if constexpr (ni >= NBLK) {
+            // narrow tiles: no 8th column block
+        } else if constexpr (F8) {
             const i32x8 bw = __builtin_shufflevector(fb[SA][ni][0], fb[SA][ni][1], 0, 1, 2, 3, 4, 5, 6, 7);
             const i32x8 ax = __builtin_shufflevector(fa[mi & 1][0], fa[mi & 1][1], 0, 1, 2, 3, 4, 5, 6, 7);
             mfma8<mode_b_e5(MODE), mode_a_e5(MODE), FIRST>(acc[mi][ni], bw, ax);

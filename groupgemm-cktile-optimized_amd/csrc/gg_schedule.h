@@ -34,6 +34,7 @@ constexpr int kTileM = 256; // output rows per tile (tokens)
 constexpr int kTileN = 256; // output columns per tile (w rows)
 constexpr int kTileK = 64;  // K per main-loop step: one 128-byte cache line per operand row
 constexpr int kBand  = 4;   // M-tiles per band of the in-group order
+constexpr int kNarrowTileN = 224; // output columns of a narrow tile (one-round forward problems)
 
 // Logical tile index of physical slot `t` (t = round * grid + workgroup).
 // Bijective on [0, total): every full round maps onto itself, and the last, partial round
