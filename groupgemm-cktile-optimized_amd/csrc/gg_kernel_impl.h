@@ -28,6 +28,8 @@
 //   * Two variants: cross-tile (a workgroup's tiles run as one continuous K pipeline and a
 //     finished tile is stored from registers during the next tile's first step) and per-tile
 //     (prologue and LDS-staged epilogue around every tile, for one tile per workgroup).
+//   * Narrow tiles (NARROW, per-tile 16-bit forward only): 256 x 224, each wave 7 column
+//     blocks; the host picks them for one-round plans that leave CUs idle.
 //
 // LDS (160 KB, all of it): A (x rows) 2 stages + B (w rows) 3 stages of 256 rows x 128 B.
 // Row r keeps its 16-byte chunk c at chunk position c ^ (r % 8): the eight lanes that a
