@@ -118,6 +118,7 @@ void fill_args(gg_plan *plan, int n_xcd) {
     a.splits    = 1;
     a.ws        = nullptr;
     a.tile_n    = gg::kTileN;
+    a.tile_m    = gg::kTileM;
 }
 
 // Split-K for problems whose tiles cannot fill the GPU (fewer than half as many tiles as CUs):
@@ -165,7 +166,8 @@ int choose_splits(int tiles, int k_tiles, int cus) {
 int use_narrow_tiles(gg_plan *plan, const int64_t *group_m, const hipDeviceProp_t &prop, hipStream_t s) {
     gg::KernelArgs &a   = plan->args;
     const char     *env = std::getenv("GG_NARROW");
-    if ((env != nullptr && std::atoi(env) == 0) || a.splits > 1 || plan->total_tiles >= prop.multiProcessorCount)
+    if ((env != nullptr && *env != '\0' && std::atoi(env) == 0) || a.splits > 1 || a.tile_m != gg::kTileM ||
+        plan->total_tiles >= prop.multiProcessorCount)
         return GG_OK;
     const int64_t               n_tiles = gg::cdiv(plan->n, gg::kNarrowTileN);
     std::vector<gg::GroupEntry> table(static_cast<size_t>(plan->group_num));
@@ -185,6 +187,76 @@ int use_narrow_tiles(gg_plan *plan, const int64_t *group_m, const hipDeviceProp_
     a.tile_n          = gg::kNarrowTileN;
     const int n_xcd   = xcd_count(prop);
     a.n_xcd           = plan->grid % n_xcd == 0 ? n_xcd : 1;
+    return GG_OK;
+}
+
+// Modelled time, in full 256 x 256 tile steps, of the busiest workgroup when tiles of tile_m rows
+// are dealt to the grid in the kernel's order (xcd_remap over the group table's banded order).
+// A tile's cost by its valid rows m, fitted to MI355X timings of partial tiles (one launch
+// per row count, 256 groups, cross-tile): with 256-row tiles 1 for a full tile, 0.86-1 for
+// 129-255 rows, and 0.70-0.85 for at most 128 rows (thin steps); with short tiles (at most 192
+// rows, six row blocks per wave) the same below 129 rows and 0.85-0.88 above.
+double busiest_workgroup(const int64_t *group_m, int group_num, int64_t n_tiles, int tile_m, int tiles,
+                         int grid, int n_xcd) {
+    std::vector<float> cost(static_cast<size_t>(tiles));
+    int                L = 0;
+    for (int g = 0; g < group_num; ++g) {
+        const int m_tiles = static_cast<int>(gg::cdiv(group_m[g], tile_m));
+        for (int local = 0; local < m_tiles * n_tiles; ++local, ++L) {
+            int tm, tn;
+            gg::band_coords(local, m_tiles, static_cast<int>(n_tiles), gg::kBand, &tm, &tn);
+            const double m = static_cast<double>(std::min<int64_t>(tile_m, group_m[g] - int64_t(tm) * tile_m));
+            double       c;
+            if (m <= 128)
+                c = 0.70 + 0.15 * m / 128;
+            else if (tile_m < gg::kTileM)
+                c = 0.85 + 0.03 * (m - 128) / 64;
+            else
+                c = m >= gg::kTileM ? 1.0 : 0.86 + 0.14 * (m - 128) / 128;
+            cost[static_cast<size_t>(L)] = static_cast<float>(c);
+        }
+    }
+    std::vector<double> load(static_cast<size_t>(grid), 0.0);
+    for (int t = 0; t < tiles; ++t)
+        load[static_cast<size_t>(t % grid)] += cost[static_cast<size_t>(gg::xcd_remap(t, tiles, grid, n_xcd))];
+    return *std::max_element(load.begin(), load.end());
+}
+
+// Short tiles (at most 192 x 256) for a 16-bit forward plan whose groups keep their M-tile
+// counts with fewer rows per tile (gg::short_tile_rows): the same tiles, and the same total
+// loads, but no group ends in a nearly empty tile next to full ones. Taken when the modelled
+// busiest workgroup is at least 3 % faster (32 groups of 520 rows, N = K = 2880: three tiles of
+// 176 rows per group; 4.71 -> 4.36 tile steps). The group table is rebuilt for the tile rows.
+// GG_SHORT=0 in the environment turns this off, GG_SHORT=1 takes short tiles whenever the tile
+// counts allow.
+int use_short_tiles(gg_plan *plan, const int64_t *group_m, hipStream_t s) {
+    gg::KernelArgs &a   = plan->args;
+    const char     *env = std::getenv("GG_SHORT");
+    const int       opt = env != nullptr && *env != '\0' ? std::atoi(env) : -1;
+    if (opt == 0 || a.splits > 1 || a.tile_n != gg::kTileN)
+        return GG_OK;
+    const int rows = gg::short_tile_rows(group_m, plan->group_num);
+    if (rows <= 0)
+        return GG_OK;
+    if (opt != 1) {
+        const double wide  = busiest_workgroup(group_m, plan->group_num, a.n_tiles, gg::kTileM,
+                                               plan->total_tiles, plan->grid, a.n_xcd);
+        const double short_ = busiest_workgroup(group_m, plan->group_num, a.n_tiles, rows,
+                                                plan->total_tiles, plan->grid, a.n_xcd);
+        if (short_ > 0.97 * wide)
+            return GG_OK;
+    }
+    std::vector<gg::GroupEntry> table(static_cast<size_t>(plan->group_num));
+    const int64_t tiles = gg::build_group_table(group_m, plan->group_num, a.n_tiles, table.data(), 0, rows);
+    if (tiles != plan->total_tiles)
+        return fail(GG_ERR_INVALID, "short tiles changed the tile count");
+    hipError_t e = hipMemcpyAsync(plan->d_groups, table.data(), table.size() * sizeof(gg::GroupEntry),
+                                  hipMemcpyHostToDevice, s);
+    if (e == hipSuccess)
+        e = hipStreamSynchronize(s);
+    if (e != hipSuccess)
+        return hip_fail(e, "short group table upload");
+    a.tile_m = rows;
     return GG_OK;
 }
 
@@ -288,11 +360,15 @@ int gg_prepare(int dtype, int group_num, int64_t n, int64_t k, const int64_t *gr
             free_plan(plan);
             return GG_ERR_HIP;
         }
+        if (const int st2 = use_short_tiles(plan, group_m, s); st2 != GG_OK) {
+            free_plan(plan);
+            return st2;
+        }
         if (use_narrow_tiles(plan, group_m, prop, s) != GG_OK) {
             free_plan(plan);
             return GG_ERR_HIP;
         }
-        plan->detail      = "mi355x persistent 256x" + std::to_string(a.tile_n) + "x64 " +
+        plan->detail      = "mi355x persistent " + std::to_string(a.tile_m) + "x" + std::to_string(a.tile_n) + "x64 " +
                        std::string(dtype == GG_DTYPE_BF16 ? "bf16" : "fp16") +
                        " grid=" + std::to_string(plan->grid) +
                        " tiles=" + std::to_string(plan->total_tiles) +

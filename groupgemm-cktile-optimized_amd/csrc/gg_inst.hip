@@ -1,27 +1,43 @@
 // One instance unit of the persistent grouped GEMM: the (input type, mode) pair GG_PART selects,
-// both variants (cross-tile and per-tile). The Makefile compiles this file once per part, in
-// parallel; gg_kernel.hip's dispatch calls launch_mode of every part.
+// both variants (cross-tile and per-tile), or (parts 14, 15) the short-tile forward instances.
+// The Makefile compiles this file once per part, in parallel; gg_kernel.hip's dispatch calls
+// launch_mode of every part.
 #include "gg_kernel_impl.h"
 
 #ifndef GG_PART
-#error "GG_PART selects the instance (0-13)"
+#error "GG_PART selects the instance (0-15)"
 #endif
 
 namespace gg {
 
 template <bool F16, int MODE>
 void launch_mode(const KernelArgs &args, bool cross, dim3 g, dim3 b, hipStream_t stream) {
+    if constexpr (MODE == make_mode(kFwd, kIn16)) {
+        if (args.tile_m != kTileM) {
+            launch_short<F16>(args, cross, g, b, stream);
+            return;
+        }
+    }
     if (cross) {
         hipLaunchKernelGGL((grouped_gemm_kernel<F16, true, MODE>), g, b, 0, stream, args);
         return;
     }
     if constexpr (MODE == make_mode(kFwd, kIn16)) {
         if (args.tile_n == kNarrowTileN) {
-            hipLaunchKernelGGL((grouped_gemm_kernel<F16, false, MODE, true>), g, b, 0, stream, args);
+            hipLaunchKernelGGL((grouped_gemm_kernel<F16, false, MODE, kShapeNarrow>), g, b, 0, stream, args);
             return;
         }
     }
     hipLaunchKernelGGL((grouped_gemm_kernel<F16, false, MODE>), g, b, 0, stream, args);
+}
+
+template <bool F16>
+void launch_short(const KernelArgs &args, bool cross, dim3 g, dim3 b, hipStream_t stream) {
+    constexpr int MODE = make_mode(kFwd, kIn16);
+    if (cross)
+        hipLaunchKernelGGL((grouped_gemm_kernel<F16, true, MODE, kShapeShort>), g, b, 0, stream, args);
+    else
+        hipLaunchKernelGGL((grouped_gemm_kernel<F16, false, MODE, kShapeShort>), g, b, 0, stream, args);
 }
 
 // part -> (fp16 MFMA, mode); the dispatch's switch in gg_kernel.hip covers the same 14 pairs
@@ -53,6 +69,10 @@ template void launch_mode<false, make_mode(kWgrad, kInE4M3)>(const KernelArgs &,
 template void launch_mode<false, make_mode(kWgrad, kInE5M2)>(const KernelArgs &, bool, dim3, dim3, hipStream_t);
 #elif GG_PART == 13
 template void launch_mode<false, make_mode(kWgrad, kInE5M2xE4M3)>(const KernelArgs &, bool, dim3, dim3, hipStream_t);
+#elif GG_PART == 14
+template void launch_short<false>(const KernelArgs &, bool, dim3, dim3, hipStream_t);
+#elif GG_PART == 15
+template void launch_short<true>(const KernelArgs &, bool, dim3, dim3, hipStream_t);
 #else
 #error "GG_PART out of range"
 #endif

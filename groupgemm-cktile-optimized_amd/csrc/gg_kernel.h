@@ -69,7 +69,14 @@ struct KernelArgs {
     TableHeader      *d_header;    // written by workgroup 0: tile count and the first bad group
     int               tile_n;      // output columns per tile: kTileN, or kNarrowTileN (per-tile
                                    // 16-bit forward plans of one round; n_tiles counts these)
+    int               tile_m;      // output rows per tile: kTileM, or at most kShortTileM (16-bit
+                                   // forward plans whose groups keep their M-tile counts; the
+                                   // group table counts these)
 };
+
+// Tile shapes of the forward kernel: 256 x 256; narrow 256 x 224 (per-tile, one-round plans);
+// short tile_m x 256 with tile_m <= kShortTileM (6 row blocks per wave).
+enum TileShape { kShapeWide = 0, kShapeNarrow = 1, kShapeShort = 2 };
 
 // Whether a launch takes the cross-tile pipeline variant (several tiles per workgroup, enough
 // K steps) rather than a prologue and an LDS-staged epilogue per tile.
@@ -79,6 +86,9 @@ bool uses_cross_tile(const KernelArgs &args, int grid, int mode = 0);
 // instantiated in the instance units (gg_inst.hip, one (F16, MODE) pair per unit).
 template <bool F16, int MODE>
 void launch_mode(const KernelArgs &args, bool cross, dim3 g, dim3 b, hipStream_t stream);
+// Short-tile instances of the 16-bit forward kernel (instance units of their own).
+template <bool F16>
+void launch_short(const KernelArgs &args, bool cross, dim3 g, dim3 b, hipStream_t stream);
 
 // Enqueue the persistent grouped GEMM: `grid` workgroups of 256 threads on `stream`.
 // fp16 selects the f16 MFMA, otherwise bf16 (16-bit formats); mode = make_mode(layout, format)

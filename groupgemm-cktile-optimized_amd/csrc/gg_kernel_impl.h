@@ -28,8 +28,11 @@
 //   * Two variants: cross-tile (a workgroup's tiles run as one continuous K pipeline and a
 //     finished tile is stored from registers during the next tile's first step) and per-tile
 //     (prologue and LDS-staged epilogue around every tile, for one tile per workgroup).
-//   * Narrow tiles (NARROW, per-tile 16-bit forward only): 256 x 224, each wave 7 column
+//   * Narrow tiles (kShapeNarrow, per-tile 16-bit forward only): 256 x 224, each wave 7 column
 //     blocks; the host picks them for one-round plans that leave CUs idle.
+//   * Short tiles (kShapeShort, 16-bit forward): at most 192 x 256 (tile_m rows), each wave 6
+//     row blocks; the host picks them when every group keeps its M-tile count (520 rows: three
+//     tiles of 176 instead of 256 + 256 + 8).
 //
 // LDS (160 KB, all of it): A (x rows) 2 stages + B (w rows) 3 stages of 256 rows x 128 B.
 // Row r keeps its 16-byte chunk c at chunk position c ^ (r % 8): the eight lanes that a
@@ -559,12 +562,17 @@ constexpr bool kTailSkip = GG_TAIL_SKIP;
 // MODE: layout (forward, dgrad, wgrad: operand layouts and tile mapping) and input format.
 // CROSS: cross-tile pipeline (needs k_tiles >= kCrossMinSteps); otherwise every tile starts
 // with a prologue and ends with the LDS-staged epilogue.
-// NARROW (per-tile forward only): tiles of 256 x 224 instead of 256 x 256, for one-round problems
-// whose 256-wide tiles leave CUs idle (1 x 2048 x 7168: 224 tiles of 256 x 256, 256 of 256 x 224).
-// Each wave takes 7 column blocks (columns 112 wn + 16 ni); the 8th block's MFMAs are compiled
-// out, and the memory schedule is unchanged: the B DMAs of rows 224-255 fall outside the tile's
-// bounded resource (zeros, no traffic), and the LDS epilogue drops chunks past n_valid.
-template <bool F16, bool CROSS, int MODE, bool NARROW = false>
+// SHAPE kShapeNarrow (per-tile forward only): tiles of 256 x 224 instead of 256 x 256, for
+// one-round problems whose 256-wide tiles leave CUs idle (1 x 2048 x 7168: 224 tiles of 256 x 256,
+// 256 of 256 x 224). Each wave takes 7 column blocks (columns 112 wn + 16 ni); the 8th block's
+// MFMAs are compiled out, and the memory schedule is unchanged: the B DMAs of rows 224-255 fall
+// outside the tile's bounded resource (zeros, no traffic), and the LDS epilogue drops chunks past
+// n_valid.
+// SHAPE kShapeShort (forward): tiles of args.tile_m <= 192 rows x 256. Each wave takes its
+// first 6 interleaved row blocks (tile rows up to 191); the MFMAs, x fragment reads and stores
+// of blocks 6 and 7 are compiled out and the memory schedule is unchanged: the A DMAs of rows
+// past tile_m fall outside the bounded resource (zeros, no traffic).
+template <bool F16, bool CROSS, int MODE, int SHAPE = kShapeWide>
 __global__ void __launch_bounds__(kThreads, 1) __attribute__((amdgpu_waves_per_eu(1, 1)))
 grouped_gemm_kernel(const KernelArgs args) {
     constexpr bool A_MN   = mode_a_mn(MODE), B_MN = mode_b_mn(MODE);
@@ -575,11 +583,16 @@ grouped_gemm_kernel(const KernelArgs args) {
     // Row blocks of a wave: interleaved (wave wm's block mi is tile rows 16 (2 mi + wm) ..) when A
     // is K-major, so that the valid rows of a partial tile split evenly between the wm = 0 and
     // wm = 1 waves; contiguous (128 wm + 16 mi ..) for the MN-major A of wgrad.
+    constexpr bool NARROW = SHAPE == kShapeNarrow;
+    constexpr bool SHORT  = SHAPE == kShapeShort;
     static_assert(!NARROW || (!CROSS && MODE == make_mode(kFwd, kIn16)), "narrow tiles: per-tile 16-bit forward");
+    static_assert(!SHORT || MODE == make_mode(kFwd, kIn16), "short tiles: 16-bit forward");
     constexpr int  TN     = NARROW ? kNarrowTileN : kTileN; // output columns per tile
     constexpr int  WCOLS  = TN / 2;                          // columns per wave (wn)
     constexpr int  NBLK   = WCOLS / 16;                      // column blocks per wave with MFMAs
+    constexpr int  RB     = SHORT ? kShortTileM / 32 : 8;    // row blocks per wave with MFMAs
     constexpr bool ILV    = !A_MN;
+    static_assert(!SHORT || ILV, "short tiles: interleaved row blocks");
     constexpr int  A_BLK  = ILV ? 32 : 16; // tile rows between a wave's consecutive row blocks
     // Partial tiles skip their empty row blocks (thin K steps), in every layout, in the cross-tile
     // variant: with one tile per workgroup (the per-tile variant's usual case) the full tiles set
@@ -599,7 +612,7 @@ grouped_gemm_kernel(const KernelArgs args) {
     int       T = args.k_tiles; // K steps of the current tile (per group for wgrad)
     // In-kernel group table (device-resident sizes, at most 64 groups): every wave builds it,
     // lane g holding group g; workgroup 0 reports the tile count and the first invalid group.
-    const bool in_kernel_table = args.d_lens != nullptr;
+    const bool in_kernel_table = !SHORT && args.d_lens != nullptr; // short tiles: host tables only
     LaneGroup  lgrp{0, 0, 0, 0};
     int        lg_total = 0;
     if (in_kernel_table) {
@@ -793,7 +806,7 @@ grouped_gemm_kernel(const KernelArgs args) {
             band_coords(L - ge.tile0, m_tiles, args.n_tiles, args.band, &tm, &tn);
         } else {
             locate_tile(L, args.groups, args.group_num, args.n_tiles, args.band, &g, &tm, &tn,
-                        LAYOUT == kWgrad ? args.m_out : 0);
+                        LAYOUT == kWgrad ? args.m_out : 0, SHORT ? args.tile_m : kTileM);
             ge = args.groups[g];
         }
         const uint8_t   *xa = static_cast<const uint8_t *>(args.x); // A storage (bytes)
@@ -824,8 +837,9 @@ grouped_gemm_kernel(const KernelArgs args) {
             tl.k0    = 0;
             tl.klast = 1;
         } else {
-            tl.m_valid         = min(kTileM, ge.m - tm * kTileM);
-            const int64_t row0 = ge.row0 + static_cast<int64_t>(tm) * kTileM;
+            const int TM       = SHORT ? args.tile_m : kTileM; // rows per tile
+            tl.m_valid         = min(TM, ge.m - tm * TM);
+            const int64_t row0 = ge.row0 + static_cast<int64_t>(tm) * TM;
             tl.rsrc_a = dma_rsrc(xa + row0 * args.lda * ES, static_cast<uint32_t>(tl.m_valid) * args.lda * ES);
             if constexpr (LAYOUT == kFwd) {
                 tl.rsrc_b = dma_rsrc(wb + (static_cast<int64_t>(g) * N + col0) * args.ldb * ES,
@@ -1018,7 +1032,7 @@ grouped_gemm_kernel(const KernelArgs args) {
             fresh_v(row);
             const int col = wn * WCOLS + (lane >> 4) * 4;
             const int off = row * kCStride + col * 2;
-            sfor<0, 8>([&](auto mi) {
+            sfor<0, RB>([&](auto mi) { // short tiles: blocks 6 and 7 are past the tile
                 sfor<0, NBLK>([&](auto ni) { // narrow tiles: the 8th block is another wave's columns
                     asm volatile("" : "+a"(acc[mi][ni]));
                     f32x4 v = acc[mi][ni];
@@ -1087,8 +1101,8 @@ grouped_gemm_kernel(const KernelArgs args) {
     auto row_mfma = [&]<int SA, bool FIRST>(auto mi_, auto idx_) {
         constexpr int mi = decltype(mi_)::value, idx = decltype(idx_)::value;
         constexpr int kh = idx / 8, ni = idx % 8; // fp8: one MFMA per (mi, ni), kh = 0
-        if constexpr (ni >= NBLK) {
-            // narrow tiles: no 8th column block
+        if constexpr (ni >= NBLK || mi >= RB) {
+            // narrow tiles: no 8th column block; short tiles: no row blocks 6 and 7
         } else if constexpr (F8) {
             const i32x8 bw = __builtin_shufflevector(fb[SA][ni][0], fb[SA][ni][1], 0, 1, 2, 3, 4, 5, 6, 7);
             const i32x8 ax = __builtin_shufflevector(fa[mi & 1][0], fa[mi & 1][1], 0, 1, 2, 3, 4, 5, 6, 7);
@@ -1126,7 +1140,7 @@ grouped_gemm_kernel(const KernelArgs args) {
                     wait_vm_lds_barrier<P::vm_at_barrier()>();
                     sched_fence();
                 }
-                if constexpr (P::read_a_next(mi, idx) >= 0) {
+                if constexpr (P::read_a_next(mi, idx) >= 0 && mi + 1 < RB) {
                     read_frag.template operator()<A_MN, P::read_a_next(mi, idx), A_BLK>(fa[(mi + 1) & 1], a_rd[SA],
                                                                                  ic<mi + 1>{});
                     sched_fence();
@@ -1140,7 +1154,7 @@ grouped_gemm_kernel(const KernelArgs args) {
                     read_frag.template operator()<A_MN, P::read_a_row0(mi, idx), A_BLK>(fa[0], a_rd[NX], ic<0>{});
                     sched_fence();
                 }
-                if constexpr (FUSE && P::epi(mi, idx) >= 0)
+                if constexpr (FUSE && P::epi(mi, idx) >= 0 && mi + 1 < RB)
                     epi_store(ic<mi + 1>{}, ic<P::epi(mi, idx)>{});
                 using cold = std::integral_constant<bool, FUSE>;
                 if constexpr (dk == 1)
@@ -1187,7 +1201,7 @@ grouped_gemm_kernel(const KernelArgs args) {
                     wait_vm_lds_barrier<P::vm_at_barrier()>();
                     sched_fence();
                 }
-                if constexpr (P::read_a_next(mi, idx) >= 0) {
+                if constexpr (P::read_a_next(mi, idx) >= 0 && mi + 1 < RB) {
                     read_frag.template operator()<A_MN, P::read_a_next(mi, idx), A_BLK>(fa[(mi + 1) & 1], a_rd[SA],
                                                                                  ic<mi + 1>{});
                     sched_fence();

@@ -35,6 +35,7 @@ constexpr int kTileN = 256; // output columns per tile (w rows)
 constexpr int kTileK = 64;  // K per main-loop step: one 128-byte cache line per operand row
 constexpr int kBand  = 4;   // M-tiles per band of the in-group order
 constexpr int kNarrowTileN = 224; // output columns of a narrow tile (one-round forward problems)
+constexpr int kShortTileM  = 192; // most output rows of a short tile (6 row blocks per wave)
 
 // Logical tile index of physical slot `t` (t = round * grid + workgroup).
 // Bijective on [0, total): every full round maps onto itself, and the last, partial round
@@ -81,6 +82,23 @@ GG_HD uint32_t active_rows(bool ilv, int m_valid, int n_valid, int wm, int wn) {
 // Ceil division for non-negative values.
 GG_HD int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Short tiles: the fewest rows per M-tile, a multiple of 16, that leave every group with the
+// M-tile count of 256-row tiles; 0 when that needs more than kShortTileM rows (or no group has
+// rows). A group of 520 rows takes three tiles of 176 rows instead of 256 + 256 + 8.
+inline int short_tile_rows(const int64_t *group_m, int group_num) {
+    int64_t rows = 0;
+    for (int g = 0; g < group_num; ++g) {
+        if (group_m[g] <= 0)
+            continue;
+        const int64_t tiles = cdiv(group_m[g], kTileM);
+        const int64_t need  = cdiv(cdiv(group_m[g], tiles), 16) * 16;
+        rows                = need > rows ? need : rows;
+        if (rows > kShortTileM)
+            return 0;
+    }
+    return static_cast<int>(rows);
+}
+
 // Per-group entry of the device-resident group table (16 bytes). Built by the host plan
 // from group_m (the reference builds the same facts per group in
 // ck_grouped_gemm.cpp:166-188: row offset, M, tile range).
@@ -95,7 +113,7 @@ struct GroupEntry {
 // has out_rows rows whatever its size (the weight gradient, one [out_rows, N] block per group,
 // zero for an empty group); otherwise a group's output rows are its own rows.
 inline int64_t build_group_table(const int64_t *group_m, int group_num, int64_t n_tiles,
-                                 GroupEntry *table, int64_t out_rows = 0) {
+                                 GroupEntry *table, int64_t out_rows = 0, int tile_m = kTileM) {
     int64_t row = 0, tiles = 0;
     for (int g = 0; g < group_num; ++g) {
         if (group_m[g] < 0 || group_m[g] > INT32_MAX)
@@ -103,7 +121,7 @@ inline int64_t build_group_table(const int64_t *group_m, int group_num, int64_t 
         table[g].row0  = row;
         table[g].m     = static_cast<int32_t>(group_m[g]);
         table[g].tile0 = static_cast<int32_t>(tiles);
-        tiles += cdiv(out_rows > 0 ? out_rows : group_m[g], kTileM) * n_tiles;
+        tiles += cdiv(out_rows > 0 ? out_rows : group_m[g], tile_m) * n_tiles;
         row += group_m[g];
         if (tiles > INT32_MAX)
             return -1;
@@ -113,14 +131,15 @@ inline int64_t build_group_table(const int64_t *group_m, int group_num, int64_t 
 
 // Group and (M-tile, N-tile) of logical tile L. *g is a hint: the group of a smaller L seen
 // before (0 at the start); logical tiles only grow for one workgroup, so the scan only moves
-// forward. Empty groups own no tiles and are stepped over. out_rows as in build_group_table.
+// forward. Empty groups own no tiles and are stepped over. out_rows and tile_m as in
+// build_group_table.
 GG_HD void locate_tile(int L, const GroupEntry *groups, int group_num, int n_tiles, int band,
-                       int *g, int *tm, int *tn, int out_rows = 0) {
+                       int *g, int *tm, int *tn, int out_rows = 0, int tile_m = kTileM) {
     int gi = *g;
     while (gi + 1 < group_num && groups[gi + 1].tile0 <= L)
         ++gi;
     *g                = gi;
-    const int m_tiles = ((out_rows > 0 ? out_rows : groups[gi].m) + kTileM - 1) / kTileM;
+    const int m_tiles = ((out_rows > 0 ? out_rows : groups[gi].m) + tile_m - 1) / tile_m;
     band_coords(L - groups[gi].tile0, m_tiles, n_tiles, band, tm, tn);
 }
 

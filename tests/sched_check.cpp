@@ -90,12 +90,13 @@ static void check_band(int m_tiles, int n_tiles, int band) {
 
 // out_rows > 0: the weight-gradient walk, where every group (empty ones included) owns an
 // out_rows x n output.
+// tile_m: rows per M-tile (short tiles: fewer than 256).
 static void check_walk(const std::vector<int64_t> &group_m, int64_t n, int grid, int n_xcd,
-                       int64_t out_rows = 0) {
+                       int64_t out_rows = 0, int tile_m = gg::kTileM) {
     const int64_t n_tiles = gg::cdiv(n, gg::kTileN);
     std::vector<gg::GroupEntry> table(group_m.size());
     const int64_t total = gg::build_group_table(group_m.data(), (int)group_m.size(), n_tiles,
-                                                table.data(), out_rows);
+                                                table.data(), out_rows, tile_m);
     CHECK(total >= 0, "table build failed");
     std::set<std::tuple<int, int, int>> seen;
     for (int wg = 0; wg < grid; ++wg) {
@@ -106,16 +107,16 @@ static void check_walk(const std::vector<int64_t> &group_m, int64_t n, int grid,
             prevL = L;
             int tm, tn;
             gg::locate_tile(L, table.data(), (int)group_m.size(), (int)n_tiles, gg::kBand, &g, &tm,
-                            &tn, (int)out_rows);
+                            &tn, (int)out_rows, tile_m);
             const int64_t rows = out_rows > 0 ? out_rows : group_m[g];
             CHECK(rows > 0, "tile assigned to empty group %d", g);
-            CHECK(tm * gg::kTileM < rows && tn * gg::kTileN < n, "tile outside group");
+            CHECK(tm * tile_m < rows && tn * gg::kTileN < n, "tile outside group");
             CHECK(seen.insert({g, tm, tn}).second, "tile (%d,%d,%d) twice", g, tm, tn);
         }
     }
     int64_t want = 0;
     for (int64_t m : group_m)
-        want += gg::cdiv(out_rows > 0 ? out_rows : m, gg::kTileM) * n_tiles;
+        want += gg::cdiv(out_rows > 0 ? out_rows : m, tile_m) * n_tiles;
     CHECK((int64_t)seen.size() == want && want == total, "walk covers %zu of %lld tiles",
           seen.size(), (long long)want);
 }
@@ -153,7 +154,35 @@ static void check_active_rows(bool ilv) {
         }
 }
 
+// Short tiles: the rows per tile short_tile_rows picks keep every group's M-tile count and are
+// the fewest (multiple of 16) that do; the short walk covers every tile once.
+static void check_short(const std::vector<int64_t> &group_m, int64_t n, int want_rows) {
+    const int rows = gg::short_tile_rows(group_m.data(), (int)group_m.size());
+    CHECK(rows == want_rows, "short_tile_rows = %d, want %d", rows, want_rows);
+    if (rows <= 0)
+        return;
+    CHECK(rows % 16 == 0 && rows <= gg::kShortTileM, "short rows %d", rows);
+    for (int64_t m : group_m)
+        CHECK(gg::cdiv(m, rows) == gg::cdiv(m, gg::kTileM), "group of %lld rows changes its tile count", (long long)m);
+    bool fewer_ok = rows <= 16;
+    if (!fewer_ok)
+        for (int64_t m : group_m)
+            if (m > 0 && gg::cdiv(m, rows - 16) != gg::cdiv(m, gg::kTileM))
+                fewer_ok = true; // 16 rows fewer would add a tile to some group
+    CHECK(fewer_ok, "short rows %d are not the fewest", rows);
+    check_walk(group_m, n, 256, 8, 0, rows);
+    check_walk(group_m, n, 24, 8, 0, rows);
+}
+
 int main() {
+    check_short(std::vector<int64_t>(32, 520), 2880, 176); // config 5a: 3 x 176 instead of 256 + 256 + 8
+    check_short({300, 0, 260, 130}, 1000, 160);
+    check_short({100, 7, 1}, 264, 112);
+    check_short({513, 1}, 512, 176);
+    check_short(std::vector<int64_t>(8, 4096), 4096, 0);   // full tiles: nothing to gain
+    check_short({520, 256}, 2880, 0);                      // a group of exactly 256 rows
+    check_short({0, 0}, 64, 0);
+
     check_active_rows(true);
     check_active_rows(false);
     for (int n_xcd : {1, 8})
