@@ -222,7 +222,7 @@ double busiest_workgroup(const int64_t *group_m, int group_num, int64_t n_tiles,
     return *std::max_element(load.begin(), load.end());
 }
 
-// Short tiles (at most 192 x 256) for a 16-bit forward plan whose groups keep their M-tile
+// Short tiles (at most 192 x 256) for a 16-bit forward or dgrad plan whose groups keep their M-tile
 // counts with fewer rows per tile (gg::short_tile_rows): the same tiles, and the same total
 // loads, but no group ends in a nearly empty tile next to full ones. Taken when the modelled
 // busiest workgroup is at least 3 % faster (32 groups of 520 rows, N = K = 2880: three tiles of
@@ -521,7 +521,14 @@ static int prepare_backward(int layout, int dtype_a, int dtype_b, int group_num,
             free_plan(plan);
             return GG_ERR_HIP;
         }
-        plan->detail = "mi355x " + what + " persistent 256x256x" + std::to_string(f8 ? 128 : 64) + " " +
+        if (dgrad && !f8) { // short tiles: the output rows are the groups' tokens
+            if (const int st2 = use_short_tiles(plan, group_m, s); st2 != GG_OK) {
+                free_plan(plan);
+                return st2;
+            }
+        }
+        plan->detail = "mi355x " + what + " persistent " + std::to_string(ka.tile_m) + "x256x" +
+                       std::to_string(f8 ? 128 : 64) + " " +
                        (f8 ? "bf16-out" : dtype_a == GG_DTYPE_BF16 ? "bf16" : "fp16") +
                        " grid=" + std::to_string(plan->grid) + " tiles=" + std::to_string(plan->total_tiles) +
                        " xcd=" + std::to_string(ka.n_xcd) +

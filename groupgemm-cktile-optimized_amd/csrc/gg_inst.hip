@@ -1,20 +1,20 @@
 // One instance unit of the persistent grouped GEMM: the (input type, mode) pair GG_PART selects,
-// both variants (cross-tile and per-tile), or (parts 14, 15) the short-tile forward instances.
+// both variants (cross-tile and per-tile), or (parts 14-17) the short-tile instances.
 // The Makefile compiles this file once per part, in parallel; gg_kernel.hip's dispatch calls
 // launch_mode of every part.
 #include "gg_kernel_impl.h"
 
 #ifndef GG_PART
-#error "GG_PART selects the instance (0-15)"
+#error "GG_PART selects the instance (0-17)"
 #endif
 
 namespace gg {
 
 template <bool F16, int MODE>
 void launch_mode(const KernelArgs &args, bool cross, dim3 g, dim3 b, hipStream_t stream) {
-    if constexpr (MODE == make_mode(kFwd, kIn16)) {
+    if constexpr (has_short_tiles(MODE)) {
         if (args.tile_m != kTileM) {
-            launch_short<F16>(args, cross, g, b, stream);
+            launch_short<F16, MODE>(args, cross, g, b, stream);
             return;
         }
     }
@@ -31,9 +31,8 @@ void launch_mode(const KernelArgs &args, bool cross, dim3 g, dim3 b, hipStream_t
     hipLaunchKernelGGL((grouped_gemm_kernel<F16, false, MODE>), g, b, 0, stream, args);
 }
 
-template <bool F16>
+template <bool F16, int MODE>
 void launch_short(const KernelArgs &args, bool cross, dim3 g, dim3 b, hipStream_t stream) {
-    constexpr int MODE = make_mode(kFwd, kIn16);
     if (cross)
         hipLaunchKernelGGL((grouped_gemm_kernel<F16, true, MODE, kShapeShort>), g, b, 0, stream, args);
     else
@@ -70,9 +69,13 @@ template void launch_mode<false, make_mode(kWgrad, kInE5M2)>(const KernelArgs &,
 #elif GG_PART == 13
 template void launch_mode<false, make_mode(kWgrad, kInE5M2xE4M3)>(const KernelArgs &, bool, dim3, dim3, hipStream_t);
 #elif GG_PART == 14
-template void launch_short<false>(const KernelArgs &, bool, dim3, dim3, hipStream_t);
+template void launch_short<false, make_mode(kFwd, kIn16)>(const KernelArgs &, bool, dim3, dim3, hipStream_t);
 #elif GG_PART == 15
-template void launch_short<true>(const KernelArgs &, bool, dim3, dim3, hipStream_t);
+template void launch_short<true, make_mode(kFwd, kIn16)>(const KernelArgs &, bool, dim3, dim3, hipStream_t);
+#elif GG_PART == 16
+template void launch_short<false, make_mode(kDgrad, kIn16)>(const KernelArgs &, bool, dim3, dim3, hipStream_t);
+#elif GG_PART == 17
+template void launch_short<true, make_mode(kDgrad, kIn16)>(const KernelArgs &, bool, dim3, dim3, hipStream_t);
 #else
 #error "GG_PART out of range"
 #endif

@@ -69,9 +69,9 @@ struct KernelArgs {
     TableHeader      *d_header;    // written by workgroup 0: tile count and the first bad group
     int               tile_n;      // output columns per tile: kTileN, or kNarrowTileN (per-tile
                                    // 16-bit forward plans of one round; n_tiles counts these)
-    int               tile_m;      // output rows per tile: kTileM, or at most kShortTileM (16-bit
-                                   // forward plans whose groups keep their M-tile counts; the
-                                   // group table counts these)
+    int               tile_m;      // output rows per tile: kTileM, or at most kShortTileM
+                                   // (16-bit forward and dgrad plans whose groups keep their
+                                   // M-tile counts; the group table counts these)
 };
 
 // Tile shapes of the forward kernel: 256 x 256; narrow 256 x 224 (per-tile, one-round plans);
@@ -86,9 +86,13 @@ bool uses_cross_tile(const KernelArgs &args, int grid, int mode = 0);
 // instantiated in the instance units (gg_inst.hip, one (F16, MODE) pair per unit).
 template <bool F16, int MODE>
 void launch_mode(const KernelArgs &args, bool cross, dim3 g, dim3 b, hipStream_t stream);
-// Short-tile instances of the 16-bit forward kernel (instance units of their own).
-template <bool F16>
+// Short-tile instances (16-bit forward and dgrad; instance units of their own).
+template <bool F16, int MODE>
 void launch_short(const KernelArgs &args, bool cross, dim3 g, dim3 b, hipStream_t stream);
+// Modes with short-tile instances. (fp8 forward ran 6 % slower with them on config 5a's shapes.)
+constexpr bool has_short_tiles(int mode) {
+    return mode == make_mode(kFwd, kIn16) || mode == make_mode(kDgrad, kIn16);
+}
 
 // Enqueue the persistent grouped GEMM: `grid` workgroups of 256 threads on `stream`.
 // fp16 selects the f16 MFMA, otherwise bf16 (16-bit formats); mode = make_mode(layout, format)

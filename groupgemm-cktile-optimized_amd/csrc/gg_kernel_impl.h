@@ -30,7 +30,7 @@
 //     (prologue and LDS-staged epilogue around every tile, for one tile per workgroup).
 //   * Narrow tiles (kShapeNarrow, per-tile 16-bit forward only): 256 x 224, each wave 7 column
 //     blocks; the host picks them for one-round plans that leave CUs idle.
-//   * Short tiles (kShapeShort, 16-bit forward): at most 192 x 256 (tile_m rows), each wave 6
+//   * Short tiles (kShapeShort; 16-bit forward and dgrad): at most 192 x 256 (tile_m rows), each wave 6
 //     row blocks; the host picks them when every group keeps its M-tile count (520 rows: three
 //     tiles of 176 instead of 256 + 256 + 8).
 //
@@ -568,7 +568,7 @@ constexpr bool kTailSkip = GG_TAIL_SKIP;
 // MFMAs are compiled out, and the memory schedule is unchanged: the B DMAs of rows 224-255 fall
 // outside the tile's bounded resource (zeros, no traffic), and the LDS epilogue drops chunks past
 // n_valid.
-// SHAPE kShapeShort (forward): tiles of args.tile_m <= 192 rows x 256. Each wave takes its
+// SHAPE kShapeShort (16-bit forward and dgrad): tiles of args.tile_m <= 192 rows x 256. Each wave takes its
 // first 6 interleaved row blocks (tile rows up to 191); the MFMAs, x fragment reads and stores
 // of blocks 6 and 7 are compiled out and the memory schedule is unchanged: the A DMAs of rows
 // past tile_m fall outside the bounded resource (zeros, no traffic).
@@ -586,7 +586,8 @@ grouped_gemm_kernel(const KernelArgs args) {
     constexpr bool NARROW = SHAPE == kShapeNarrow;
     constexpr bool SHORT  = SHAPE == kShapeShort;
     static_assert(!NARROW || (!CROSS && MODE == make_mode(kFwd, kIn16)), "narrow tiles: per-tile 16-bit forward");
-    static_assert(!SHORT || MODE == make_mode(kFwd, kIn16), "short tiles: 16-bit forward");
+    static_assert(!SHORT || MODE == make_mode(kFwd, kIn16) || MODE == make_mode(kDgrad, kIn16),
+                  "short tiles: 16-bit forward and dgrad");
     constexpr int  TN     = NARROW ? kNarrowTileN : kTileN; // output columns per tile
     constexpr int  WCOLS  = TN / 2;                          // columns per wave (wn)
     constexpr int  NBLK   = WCOLS / 16;                      // column blocks per wave with MFMAs

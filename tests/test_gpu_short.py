@@ -13,7 +13,8 @@ Cases:
 - ragged and empty groups with a one-round per-tile plan and K % 64 = 8, in fp16;
 - enough tiles for the cross-tile variant, with thin short tiles (groups of 1-112 rows) and a
   column tail;
-- 513-row groups next to 1-row ones (160 tiles: one round, not split).
+- 513-row groups next to 1-row ones (160 tiles: one round, not split);
+- dgrad on config 5a's shapes (bf16, fp16), whose output rows are the tokens.
 """
 import pytest
 import torch
@@ -74,3 +75,48 @@ def test_short_tiles_match_wide(pkg, monkeypatch, case):
         bad = int(((got - ref).abs() > ATOL + RTOL * ref.abs()).sum())
         assert bad == 0, f"group {gi}: {bad} outputs off"
         row += m
+
+
+def _env(monkeypatch, env):
+    if env is None:
+        monkeypatch.delenv("GG_SHORT", raising=False)
+    else:
+        monkeypatch.setenv("GG_SHORT", env)
+
+
+def _dgrad(pkg, go, w, gm, env, monkeypatch):
+    # grad_x [sum(M), K] = grad_out [sum(M), N] @ w[g] [N, K]: output rows are the group's tokens
+    _env(monkeypatch, env)
+    b, n, k = w.shape
+    out = torch.full((go.shape[0], k), float("nan"), dtype=go.dtype, device=DEV)
+    s = torch.cuda.current_stream(DEV).cuda_stream
+    dt = pkg.DType.BF16 if go.dtype == torch.bfloat16 else pkg.DType.FP16
+    plan = pkg.BackwardPlan("dgrad", dt, n, k, gm, go.data_ptr(), w.data_ptr(), out.data_ptr(), s)
+    plan.run(s)
+    torch.cuda.synchronize(DEV)
+    detail = plan.detail()
+    plan.release()
+    return out, detail
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_short_tiles_dgrad(pkg, monkeypatch, dt):
+    gm, n, k = [520] * 32, 2880, 2880  # config 5a's shapes: the model picks short tiles
+    print(f"[short] dgrad: dtype={dt} groups={len(gm)} N={n} K={k}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(80)
+    go = torch.randn((sum(gm), n), generator=g, device=DEV).to(dt)
+    w = torch.randn((len(gm), n, k), generator=g, device=DEV).to(dt)
+    short, d_short = _dgrad(pkg, go, w, gm, None, monkeypatch)
+    wide, d_wide = _dgrad(pkg, go, w, gm, "0", monkeypatch)
+    assert "persistent 176x256x64" in d_short, d_short
+    assert "persistent 256x256x64" in d_wide, d_wide
+    assert torch.equal(short.view(torch.int16), wide.view(torch.int16)), (d_short, d_wide)
+    row = 0
+    for gi, m in enumerate(gm):
+        ref = go[row:row + m].float() @ w[gi].float()
+        got = short[row:row + m].float()
+        assert not torch.isnan(got).any(), f"group {gi}: unwritten outputs"
+        bad = int(((got - ref).abs() > ATOL + RTOL * ref.abs()).sum())
+        assert bad == 0, f"group {gi}: {bad} outputs off"
+        row += m
+
