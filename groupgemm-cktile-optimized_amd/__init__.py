@@ -61,6 +61,11 @@ C_API = {
                                                  ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                                  ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                                  ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)]),
+    "gg_run_device_lens_noalloc": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                                  ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p,
+                                                  ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                                  ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                                  ctypes.c_void_p]),
     "gg_prepare_dgrad_fp8": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int64,
                                             ctypes.c_int64, ctypes.POINTER(ctypes.c_int64), ctypes.c_void_p,
                                             ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
@@ -324,6 +329,18 @@ class DeviceLensPlan:
             self.release()
         except Exception:
             pass
+
+
+def run_device_lens_noalloc(op: int, a_dtype: DType, b_dtype: DType, group_num: int, total_m: int, n: int,
+                            k: int, group_lens: int, group_offs: int, a: int, b: int, out: int, stream: int = 0,
+                            a_scale: int = 0, b_scale: int = 0) -> None:
+    """gg_run_device_lens_noalloc: DeviceLensPlan(...).run(stream) in one call that allocates no
+    device memory (the group table lives in the library's per-GPU scratch array; at most 8192
+    groups; calls that overlap on one GPU race on it)."""
+    lib = load_library()
+    _check(lib.gg_run_device_lens_noalloc(op, int(a_dtype), int(b_dtype), group_num, total_m, n, k, group_lens,
+                                          group_offs or None, a, b, a_scale or None, b_scale or None, out,
+                                          stream))
 
 
 def _device_sizes(group_m, group_offs, b):

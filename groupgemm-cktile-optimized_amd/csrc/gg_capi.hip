@@ -10,6 +10,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -282,6 +283,277 @@ void free_plan(gg_plan *plan) {
     if (plan->d_ws != nullptr)
         (void)hipFree(plan->d_ws);
     delete plan;
+}
+
+} // namespace
+
+namespace {
+
+// ---------------------------------------------------------------------------------------
+// Device-resident group sizes: the plan builder shared by gg_prepare_device_lens_op (a plan that
+// owns its table, hipMalloc'd) and gg_run_device_lens_noalloc (one call that allocates nothing:
+// the table and its header live in the device's `scratch` array below).
+// ---------------------------------------------------------------------------------------
+
+// Scratch of the allocation-free entry point: the group table (16 bytes per group) and its
+// header. One copy per GPU, held until the process ends; every call on a GPU shares it, so
+// calls that overlap on one GPU (two streams, two host threads) race on it. Host code never
+// names `scratch` in a kernel argument or copy: it uses the device address that
+// hipGetSymbolAddress gives for the current device (noalloc_device).
+constexpr int    kNoAllocMaxGroups  = 8192;
+constexpr size_t kNoAllocTableBytes = size_t(kNoAllocMaxGroups) * sizeof(gg::GroupEntry);
+constexpr size_t kScratchBytes      = kNoAllocTableBytes + 256; // + the TableHeader, padded
+static_assert(sizeof(gg::TableHeader) <= 256, "the header fits behind the largest table");
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+// What the allocation-free entry point keeps per device: the scratch address and the launch
+// facts of hipGetDeviceProperties (queried once, not per call).
+struct NoAllocDevice {
+    void *scratch = nullptr;
+    int   cus     = 0;
+    int   n_xcd   = 1;
+};
+constexpr int kNoAllocMaxDevices = 64;
+std::mutex    g_noalloc_mu;
+NoAllocDevice g_noalloc_dev[kNoAllocMaxDevices];
+
+// The current device's entry, set up on its first use with that device current.
+int noalloc_device(NoAllocDevice *out) {
+    int        dev = 0;
+    hipError_t e   = hipGetDevice(&dev);
+    if (e != hipSuccess)
+        return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= kNoAllocMaxDevices)
+        return fail(GG_ERR_UNSUPPORTED, "device index " + std::to_string(dev) + " beyond " +
+                                            std::to_string(kNoAllocMaxDevices));
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    NoAllocDevice              &d = g_noalloc_dev[dev];
+    if (d.scratch == nullptr) {
+        hipDeviceProp_t prop;
+        if (device_props(&prop) != GG_OK)
+            return GG_ERR_HIP;
+        void *p = nullptr;
+        e       = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess)
+            return hip_fail(e, "hipGetSymbolAddress(scratch)");
+        if (p == nullptr || (reinterpret_cast<uintptr_t>(p) & 255u) != 0)
+            return fail(GG_ERR_HIP, "hipGetSymbolAddress(scratch) gave a null or misaligned address");
+        d.cus     = prop.multiProcessorCount;
+        d.n_xcd   = xcd_count(prop);
+        d.scratch = p;
+    }
+    *out = d;
+    return GG_OK;
+}
+
+// Validates a device-size problem (the rules of gg_prepare_device_lens_op) and fills *plan.
+// noalloc = false: the table and header are one hipMalloc owned by the plan (free_plan releases
+// it, also on failure). noalloc = true: they are the current device's scratch array, and nothing
+// is allocated (no detail text either). A plan without a launch keeps d_groups null.
+int plan_device_lens(gg_plan *plan, bool noalloc, int op, int a_dtype, int b_dtype, int group_num,
+                     int64_t total_m, int64_t n, int64_t k, const int64_t *group_lens, const int64_t *group_offs,
+                     const void *a, const void *b, const float *a_scale, const float *b_scale, void *out) {
+    if (op != GG_OP_FORWARD && op != GG_OP_DGRAD && op != GG_OP_WGRAD)
+        return fail(GG_ERR_INVALID, "op must be GG_OP_FORWARD, GG_OP_DGRAD or GG_OP_WGRAD");
+    if (total_m < 0 || group_num < 0 || n < 0 || k < 0)
+        return fail(GG_ERR_INVALID, "group_num, total_m, n and k must be >= 0");
+    if (group_num > 0 && group_lens == nullptr)
+        return fail(GG_ERR_INVALID, "group_lens is null");
+    // Input formats: two equal 16-bit types, or fp8 (forward: both e4m3 or both e5m2; backward
+    // also an e5m2 gradient with e4m3 w / x).
+    const bool f8     = a_dtype == GG_DTYPE_FP8_E4M3 || a_dtype == GG_DTYPE_FP8_E5M2;
+    int        format = gg::kIn16;
+    if (f8) {
+        if (a_dtype == GG_DTYPE_FP8_E4M3 && b_dtype == GG_DTYPE_FP8_E4M3)
+            format = gg::kInE4M3;
+        else if (a_dtype == GG_DTYPE_FP8_E5M2 && b_dtype == GG_DTYPE_FP8_E5M2)
+            format = gg::kInE5M2;
+        else if (op != GG_OP_FORWARD && a_dtype == GG_DTYPE_FP8_E5M2 && b_dtype == GG_DTYPE_FP8_E4M3)
+            format = gg::kInE5M2xE4M3;
+        else
+            return fail(GG_ERR_INVALID, "unsupported pair of fp8 formats");
+    } else if ((a_dtype != GG_DTYPE_BF16 && a_dtype != GG_DTYPE_FP16) || b_dtype != a_dtype) {
+        return fail(GG_ERR_INVALID, "dtypes must be equal bf16 / fp16 types, or fp8 formats");
+    }
+    const int     layout   = op == GG_OP_FORWARD ? gg::kFwd : op == GG_OP_DGRAD ? gg::kDgrad : gg::kWgrad;
+    // kernel terms (KernelArgs): output columns N_out, contraction K_c, output rows
+    const int64_t n_out    = op == GG_OP_FORWARD ? n : k;
+    const int64_t k_c      = op == GG_OP_FORWARD ? k : op == GG_OP_DGRAD ? n : 0; // wgrad: per group
+    const int64_t out_rows = op == GG_OP_WGRAD ? int64_t(group_num) * n : total_m;
+    const bool    has_output = out_rows > 0 && n_out > 0;
+    const bool    reads      = op == GG_OP_WGRAD ? total_m > 0 : (total_m > 0 && k_c > 0);
+    if (has_output && (out == nullptr || (reads && (a == nullptr || b == nullptr))))
+        return fail(GG_ERR_INVALID, "the inputs and the output must be device pointers");
+    if (f8 && has_output && reads && (a_scale == nullptr || b_scale == nullptr))
+        return fail(GG_ERR_INVALID, "fp8 scales must be device pointers");
+    // 16-byte rows; transposed fp8 operands move 16-column blocks
+    const int64_t align_n = (f8 && op != GG_OP_FORWARD) ? 16 : 8;
+    const int64_t align_k = f8 ? 16 : 8;
+    if (n % align_n != 0)
+        return fail(GG_ERR_UNSUPPORTED, "N must be a multiple of " + std::to_string(align_n));
+    if (k % align_k != 0)
+        return fail(GG_ERR_UNSUPPORTED, "K must be a multiple of " + std::to_string(align_k));
+    if (has_output && (!aligned16(out) || (reads && (!aligned16(a) || !aligned16(b)))))
+        return fail(GG_ERR_UNSUPPORTED, "buffers must be 16-byte aligned");
+    if (k > (int64_t(1) << 21) || n > (int64_t(1) << 21))
+        return fail(GG_ERR_UNSUPPORTED, "N and K must be at most 2097152");
+    const int64_t lim   = int64_t(1) << 31;
+    const int64_t es    = f8 ? 1 : 2;
+    const int64_t steps = f8 ? 128 : gg::kTileK;
+    if (op == GG_OP_DGRAD && (n + steps) * k * es >= lim)
+        return fail(GG_ERR_UNSUPPORTED, "one group's w must be smaller than 2 GiB");
+    // wgrad: a group may hold every row
+    if (op == GG_OP_WGRAD && ((total_m + steps) * n * es >= lim || (total_m + steps) * k * es >= lim))
+        return fail(GG_ERR_UNSUPPORTED, "grad_out and x rows must be smaller than 2 GiB");
+    const int64_t n_tiles = gg::cdiv(n_out, gg::kTileN);
+    // wgrad: output tiles do not depend on the sizes, m_out rows per group
+    const int64_t wgrad_tiles = op == GG_OP_WGRAD ? int64_t(group_num) * gg::cdiv(n, gg::kTileM) * n_tiles : 0;
+    if (wgrad_tiles > INT32_MAX)
+        return fail(GG_ERR_UNSUPPORTED, "too many tiles for 32-bit tile indices");
+
+    plan->mode        = gg::make_mode(layout, format);
+    plan->dtype       = f8 ? GG_DTYPE_BF16 : a_dtype; // output
+    plan->group_num   = group_num;
+    plan->n           = n_out;
+    plan->k           = k_c;
+    plan->total_m     = out_rows;
+    plan->in_rows     = total_m;
+    plan->x           = a;
+    plan->w           = b;
+    plan->out         = out;
+    plan->device_lens = true;
+    plan->d_lens      = group_lens;
+    plan->d_offs      = group_offs;
+    std::string what;
+    if (!noalloc)
+        what = std::string(op == GG_OP_FORWARD ? "" : op == GG_OP_DGRAD ? "dgrad " : "wgrad ") +
+               (format == gg::kIn16     ? std::string(a_dtype == GG_DTYPE_BF16 ? "bf16" : "fp16")
+                : format == gg::kInE4M3 ? std::string("fp8 e4m3")
+                : format == gg::kInE5M2 ? std::string("fp8 e5m2")
+                                        : std::string("fp8 e5m2 x e4m3"));
+    const bool no_launch = !has_output || group_num == 0 || (op != GG_OP_WGRAD && k_c == 0);
+    if (no_launch) {
+        // forward / dgrad with an empty contraction: the run zero-fills the output
+        if (!noalloc)
+            plan->detail = "mi355x " + what + ": no launch (" +
+                           (has_output && group_num > 0
+                                ? (op == GG_OP_FORWARD ? "K = 0, zero fill" : "empty contraction, zero fill")
+                                : "empty output") +
+                           ")";
+        if (!has_output || group_num == 0)
+            plan->total_m = 0;
+        return GG_OK;
+    }
+    int cus = 0, n_xcd = 1;
+    const size_t table_bytes = static_cast<size_t>(group_num) * sizeof(gg::GroupEntry);
+    if (noalloc) {
+        NoAllocDevice d;
+        if (const int st = noalloc_device(&d); st != GG_OK)
+            return st;
+        cus            = d.cus;
+        n_xcd          = d.n_xcd;
+        plan->d_groups = static_cast<gg::GroupEntry *>(d.scratch);
+        plan->d_header = reinterpret_cast<gg::TableHeader *>(static_cast<char *>(d.scratch) + kNoAllocTableBytes);
+    } else {
+        hipDeviceProp_t prop;
+        if (device_props(&prop) != GG_OK)
+            return GG_ERR_HIP;
+        cus   = prop.multiProcessorCount;
+        n_xcd = xcd_count(prop);
+        // Table + header in one allocation; the header is written by every run.
+        const hipError_t e = hipMalloc(&plan->d_groups, table_bytes + sizeof(gg::TableHeader));
+        if (e != hipSuccess) {
+            plan->d_groups = nullptr;
+            return hip_fail(e, "group table allocation");
+        }
+        plan->d_header = reinterpret_cast<gg::TableHeader *>(reinterpret_cast<char *>(plan->d_groups) +
+                                                             table_bytes);
+    }
+    fill_args(plan, 1);
+    gg::KernelArgs &ka = plan->args;
+    ka.k_tiles         = op == GG_OP_WGRAD ? 1 : static_cast<int>(gg::cdiv(k_c, steps));
+    ka.x_scale         = f8 ? a_scale : nullptr;
+    ka.w_scale         = f8 ? b_scale : nullptr;
+    if (op != GG_OP_FORWARD) {
+        ka.lda = static_cast<int>(n);
+        ka.ldb = static_cast<int>(k);
+    }
+    if (op == GG_OP_WGRAD) {
+        // The K-step counts depend on the sizes, so the per-tile variant runs (min_steps = 0).
+        ka.m_out          = static_cast<int>(n);
+        ka.min_steps      = 0;
+        plan->total_tiles = static_cast<int>(wgrad_tiles);
+        plan->grid        = static_cast<int>(std::min<int64_t>(cus, wgrad_tiles));
+        ka.total_tiles    = plan->total_tiles;
+        ka.d_total        = nullptr;
+    } else {
+        // Tile count is unknown here: one workgroup per CU, or fewer if even the largest routing
+        // (every group's rows tiled separately) has fewer tiles.
+        const int64_t max_tiles = (gg::cdiv(total_m, gg::kTileM) + group_num) * n_tiles;
+        plan->grid     = static_cast<int>(std::min<int64_t>(cus, max_tiles));
+        ka.total_tiles = 0;
+        ka.d_total     = &plan->d_header->total_tiles;
+    }
+    // At most kInKernelTableGroups groups: the GEMM builds the table itself (one group per lane of
+    // every wave) and writes the header, so a run is one launch.
+    if (group_num <= gg::kInKernelTableGroups) {
+        plan->in_kernel_table = true;
+        ka.d_lens             = group_lens;
+        ka.d_offs             = group_offs;
+        ka.lens_rows          = total_m;
+        ka.d_header           = plan->d_header;
+        ka.d_total            = nullptr;
+    }
+    ka.n_xcd = plan->grid % n_xcd == 0 ? n_xcd : 1;
+    if (!noalloc)
+        plan->detail = "mi355x " + what + " persistent 256x256x" + std::to_string(f8 ? 128 : 64) + " grid=" +
+                       std::to_string(plan->grid) + " tiles=" +
+                       (op == GG_OP_WGRAD ? std::to_string(plan->total_tiles) : std::string("device")) +
+                       " xcd=" + std::to_string(ka.n_xcd) +
+                       (gg::uses_cross_tile(ka, plan->grid, plan->mode) ? " cross-tile" : " per-tile") +
+                       (plan->in_kernel_table ? " (device group sizes, in-kernel table)" : " (device group sizes)");
+    return GG_OK;
+}
+
+// Enqueue a plan's launches on `stream` (gg_run). zero_kernel: an empty contraction zero-fills
+// the output with a fill kernel instead of hipMemsetAsync (which a captured graph must not
+// hold).
+int run_plan(const gg_plan *plan, void *stream, bool zero_kernel) {
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (plan->device_lens && plan->d_groups != nullptr) {
+        hipError_t e = hipSuccess;
+        if (!plan->in_kernel_table) {
+            e = gg::launch_build_group_table(plan->d_lens, plan->d_offs, plan->group_num, plan->in_rows,
+                                             plan->args.n_tiles, plan->d_groups, plan->d_header, s,
+                                             plan->args.m_out);
+            if (e != hipSuccess)
+                return hip_fail(e, "group table launch");
+        }
+        e = gg::launch_grouped_gemm(plan->args, plan->dtype == GG_DTYPE_FP16, plan->grid, s, plan->mode);
+        if (e != hipSuccess)
+            return hip_fail(e, "grouped GEMM launch");
+        return GG_OK;
+    }
+    if (plan->total_tiles == 0) {
+        // K == 0 with a non-empty output: out = 0.
+        if (plan->total_m > 0 && plan->n > 0 && plan->k == 0) {
+            const size_t     bytes = size_t(plan->total_m) * plan->n * 2;
+            const hipError_t e     = zero_kernel ? gg::launch_zero_fill(plan->out, bytes, s)
+                                                 : hipMemsetAsync(plan->out, 0, bytes, s);
+            if (e != hipSuccess)
+                return hip_fail(e, zero_kernel ? "zero fill launch" : "hipMemsetAsync");
+        }
+        return GG_OK;
+    }
+    hipError_t e = gg::launch_grouped_gemm(plan->args, plan->dtype == GG_DTYPE_FP16, plan->grid, s, plan->mode);
+    if (e != hipSuccess)
+        return hip_fail(e, "grouped GEMM launch");
+    if (plan->args.splits > 1) {
+        e = gg::launch_split_reduce(plan->args, plan->dtype == GG_DTYPE_FP16, s, plan->mode);
+        if (e != hipSuccess)
+            return hip_fail(e, "split-K reduction launch");
+    }
+    return GG_OK;
 }
 
 } // namespace
@@ -691,201 +963,45 @@ int gg_prepare_device_lens_op(int op, int a_dtype, int b_dtype, int group_num, i
                               int64_t k, const int64_t *group_lens, const int64_t *group_offs, const void *a,
                               const void *b, const float *a_scale, const float *b_scale, void *out,
                               void *stream, gg_plan **plan_out) {
+    (void)stream;
     g_last_error.clear();
     if (plan_out == nullptr)
         return fail(GG_ERR_INVALID, "plan_out is null");
     *plan_out = nullptr;
-    if (op != GG_OP_FORWARD && op != GG_OP_DGRAD && op != GG_OP_WGRAD)
-        return fail(GG_ERR_INVALID, "op must be GG_OP_FORWARD, GG_OP_DGRAD or GG_OP_WGRAD");
-    if (total_m < 0 || group_num < 0 || n < 0 || k < 0)
-        return fail(GG_ERR_INVALID, "group_num, total_m, n and k must be >= 0");
-    if (group_num > 0 && group_lens == nullptr)
-        return fail(GG_ERR_INVALID, "group_lens is null");
-    // Input formats: two equal 16-bit types, or fp8 (forward: both e4m3 or both e5m2; backward
-    // also an e5m2 gradient with e4m3 w / x).
-    const bool f8     = a_dtype == GG_DTYPE_FP8_E4M3 || a_dtype == GG_DTYPE_FP8_E5M2;
-    int        format = gg::kIn16;
-    if (f8) {
-        if (a_dtype == GG_DTYPE_FP8_E4M3 && b_dtype == GG_DTYPE_FP8_E4M3)
-            format = gg::kInE4M3;
-        else if (a_dtype == GG_DTYPE_FP8_E5M2 && b_dtype == GG_DTYPE_FP8_E5M2)
-            format = gg::kInE5M2;
-        else if (op != GG_OP_FORWARD && a_dtype == GG_DTYPE_FP8_E5M2 && b_dtype == GG_DTYPE_FP8_E4M3)
-            format = gg::kInE5M2xE4M3;
-        else
-            return fail(GG_ERR_INVALID, "unsupported pair of fp8 formats");
-    } else if ((a_dtype != GG_DTYPE_BF16 && a_dtype != GG_DTYPE_FP16) || b_dtype != a_dtype) {
-        return fail(GG_ERR_INVALID, "dtypes must be equal bf16 / fp16 types, or fp8 formats");
-    }
-    const int     layout   = op == GG_OP_FORWARD ? gg::kFwd : op == GG_OP_DGRAD ? gg::kDgrad : gg::kWgrad;
-    // kernel terms (KernelArgs): output columns N_out, contraction K_c, output rows
-    const int64_t n_out    = op == GG_OP_FORWARD ? n : k;
-    const int64_t k_c      = op == GG_OP_FORWARD ? k : op == GG_OP_DGRAD ? n : 0; // wgrad: per group
-    const int64_t out_rows = op == GG_OP_WGRAD ? int64_t(group_num) * n : total_m;
-    const bool    has_output = out_rows > 0 && n_out > 0;
-    const bool    reads      = op == GG_OP_WGRAD ? total_m > 0 : (total_m > 0 && k_c > 0);
-    if (has_output && (out == nullptr || (reads && (a == nullptr || b == nullptr))))
-        return fail(GG_ERR_INVALID, "the inputs and the output must be device pointers");
-    if (f8 && has_output && reads && (a_scale == nullptr || b_scale == nullptr))
-        return fail(GG_ERR_INVALID, "fp8 scales must be device pointers");
-    // 16-byte rows; transposed fp8 operands move 16-column blocks
-    const int64_t align_n = (f8 && op != GG_OP_FORWARD) ? 16 : 8;
-    const int64_t align_k = f8 ? 16 : 8;
-    if (n % align_n != 0)
-        return fail(GG_ERR_UNSUPPORTED, "N must be a multiple of " + std::to_string(align_n));
-    if (k % align_k != 0)
-        return fail(GG_ERR_UNSUPPORTED, "K must be a multiple of " + std::to_string(align_k));
-    if (has_output && (!aligned16(out) || (reads && (!aligned16(a) || !aligned16(b)))))
-        return fail(GG_ERR_UNSUPPORTED, "buffers must be 16-byte aligned");
-    if (k > (int64_t(1) << 21) || n > (int64_t(1) << 21))
-        return fail(GG_ERR_UNSUPPORTED, "N and K must be at most 2097152");
-    const int64_t lim   = int64_t(1) << 31;
-    const int64_t es    = f8 ? 1 : 2;
-    const int64_t steps = f8 ? 128 : gg::kTileK;
-    if (op == GG_OP_DGRAD && (n + steps) * k * es >= lim)
-        return fail(GG_ERR_UNSUPPORTED, "one group's w must be smaller than 2 GiB");
-    // wgrad: a group may hold every row
-    if (op == GG_OP_WGRAD && ((total_m + steps) * n * es >= lim || (total_m + steps) * k * es >= lim))
-        return fail(GG_ERR_UNSUPPORTED, "grad_out and x rows must be smaller than 2 GiB");
-
     auto *plan = new (std::nothrow) gg_plan;
     if (plan == nullptr)
         return fail(GG_ERR_INVALID, "out of host memory");
-    plan->mode        = gg::make_mode(layout, format);
-    plan->dtype       = f8 ? GG_DTYPE_BF16 : a_dtype; // output
-    plan->group_num   = group_num;
-    plan->n           = n_out;
-    plan->k           = k_c;
-    plan->total_m     = out_rows;
-    plan->in_rows     = total_m;
-    plan->x           = a;
-    plan->w           = b;
-    plan->out         = out;
-    plan->device_lens = true;
-    plan->d_lens      = group_lens;
-    plan->d_offs      = group_offs;
-    const std::string what = std::string(op == GG_OP_FORWARD ? "" : op == GG_OP_DGRAD ? "dgrad " : "wgrad ") +
-                             (format == gg::kIn16     ? std::string(a_dtype == GG_DTYPE_BF16 ? "bf16" : "fp16")
-                              : format == gg::kInE4M3 ? std::string("fp8 e4m3")
-                              : format == gg::kInE5M2 ? std::string("fp8 e5m2")
-                                                      : std::string("fp8 e5m2 x e4m3"));
-    const bool no_launch = !has_output || group_num == 0 || (op != GG_OP_WGRAD && k_c == 0);
-    if (no_launch) {
-        // forward / dgrad with an empty contraction: gg_run zero-fills the output
-        plan->detail = "mi355x " + what + ": no launch (" +
-                       (has_output && group_num > 0
-                            ? (op == GG_OP_FORWARD ? "K = 0, zero fill" : "empty contraction, zero fill")
-                            : "empty output") +
-                       ")";
-        if (!has_output || group_num == 0)
-            plan->total_m = 0;
-        *plan_out = plan;
-        return GG_OK;
+    const int st = plan_device_lens(plan, false, op, a_dtype, b_dtype, group_num, total_m, n, k, group_lens,
+                                    group_offs, a, b, a_scale, b_scale, out);
+    if (st != GG_OK) {
+        free_plan(plan);
+        return st;
     }
-    hipDeviceProp_t prop;
-    if (device_props(&prop) != GG_OK) {
-        delete plan;
-        return GG_ERR_HIP;
-    }
-    // Table + header in one allocation; the header is written by every run.
-    const size_t table_bytes = static_cast<size_t>(group_num) * sizeof(gg::GroupEntry);
-    hipError_t   e           = hipMalloc(&plan->d_groups, table_bytes + sizeof(gg::TableHeader));
-    if (e != hipSuccess) {
-        delete plan;
-        return hip_fail(e, "group table allocation");
-    }
-    plan->d_header = reinterpret_cast<gg::TableHeader *>(reinterpret_cast<char *>(plan->d_groups) +
-                                                         table_bytes);
-    const int64_t n_tiles = gg::cdiv(n_out, gg::kTileN);
-    fill_args(plan, 1);
-    gg::KernelArgs &ka = plan->args;
-    ka.k_tiles         = op == GG_OP_WGRAD ? 1 : static_cast<int>(gg::cdiv(k_c, steps));
-    ka.x_scale         = f8 ? a_scale : nullptr;
-    ka.w_scale         = f8 ? b_scale : nullptr;
-    if (op != GG_OP_FORWARD) {
-        ka.lda = static_cast<int>(n);
-        ka.ldb = static_cast<int>(k);
-    }
-    if (op == GG_OP_WGRAD) {
-        // Output tiles do not depend on the sizes: m_out rows per group. The K-step counts do,
-        // so the per-tile variant runs (min_steps = 0).
-        ka.m_out       = static_cast<int>(n);
-        ka.min_steps   = 0;
-        const int64_t tiles = int64_t(group_num) * gg::cdiv(n, gg::kTileM) * n_tiles;
-        if (tiles > INT32_MAX) {
-            free_plan(plan);
-            return fail(GG_ERR_UNSUPPORTED, "too many tiles for 32-bit tile indices");
-        }
-        plan->total_tiles = static_cast<int>(tiles);
-        plan->grid        = static_cast<int>(std::min<int64_t>(prop.multiProcessorCount, tiles));
-        ka.total_tiles    = plan->total_tiles;
-        ka.d_total        = nullptr;
-    } else {
-        // Tile count is unknown here: one workgroup per CU, or fewer if even the largest routing
-        // (every group's rows tiled separately) has fewer tiles.
-        const int64_t max_tiles = (gg::cdiv(total_m, gg::kTileM) + group_num) * n_tiles;
-        plan->grid     = static_cast<int>(std::min<int64_t>(prop.multiProcessorCount, max_tiles));
-        ka.total_tiles = 0;
-        ka.d_total     = &plan->d_header->total_tiles;
-    }
-    // At most kInKernelTableGroups groups: the GEMM builds the table itself (one group per lane of
-    // every wave) and writes the header, so a run is one launch.
-    if (group_num <= gg::kInKernelTableGroups) {
-        plan->in_kernel_table = true;
-        ka.d_lens             = group_lens;
-        ka.d_offs             = group_offs;
-        ka.lens_rows          = total_m;
-        ka.d_header           = plan->d_header;
-        ka.d_total            = nullptr;
-    }
-    const int n_xcd = xcd_count(prop);
-    ka.n_xcd        = plan->grid % n_xcd == 0 ? n_xcd : 1;
-    plan->detail = "mi355x " + what + " persistent 256x256x" + std::to_string(f8 ? 128 : 64) + " grid=" +
-                   std::to_string(plan->grid) + " tiles=" +
-                   (op == GG_OP_WGRAD ? std::to_string(plan->total_tiles) : std::string("device")) +
-                   " xcd=" + std::to_string(ka.n_xcd) +
-                   (gg::uses_cross_tile(ka, plan->grid, plan->mode) ? " cross-tile" : " per-tile") +
-                   (plan->in_kernel_table ? " (device group sizes, in-kernel table)" : " (device group sizes)");
     *plan_out = plan;
     return GG_OK;
+}
+
+int gg_run_device_lens_noalloc(int op, int a_dtype, int b_dtype, int group_num, int64_t total_m, int64_t n,
+                               int64_t k, const int64_t *group_lens, const int64_t *group_offs, const void *a,
+                               const void *b, const float *a_scale, const float *b_scale, void *out,
+                               void *stream) {
+    g_last_error.clear();
+    if (group_num > kNoAllocMaxGroups)
+        return fail(GG_ERR_UNSUPPORTED, "gg_run_device_lens_noalloc takes at most " +
+                                            std::to_string(kNoAllocMaxGroups) + " groups (got " +
+                                            std::to_string(group_num) + ")");
+    gg_plan plan; // on the stack: its table is the device's scratch array
+    const int st = plan_device_lens(&plan, true, op, a_dtype, b_dtype, group_num, total_m, n, k, group_lens,
+                                    group_offs, a, b, a_scale, b_scale, out);
+    if (st != GG_OK)
+        return st;
+    return run_plan(&plan, stream, true);
 }
 
 int gg_run(const gg_plan *plan, void *stream) {
     if (plan == nullptr)
         return fail(GG_ERR_INVALID, "plan is null");
-    const hipStream_t s = static_cast<hipStream_t>(stream);
-    if (plan->device_lens && plan->d_groups != nullptr) {
-        hipError_t e = hipSuccess;
-        if (!plan->in_kernel_table) {
-            e = gg::launch_build_group_table(plan->d_lens, plan->d_offs, plan->group_num, plan->in_rows,
-                                             plan->args.n_tiles, plan->d_groups, plan->d_header, s,
-                                             plan->args.m_out);
-            if (e != hipSuccess)
-                return hip_fail(e, "group table launch");
-        }
-        e = gg::launch_grouped_gemm(plan->args, plan->dtype == GG_DTYPE_FP16, plan->grid, s, plan->mode);
-        if (e != hipSuccess)
-            return hip_fail(e, "grouped GEMM launch");
-        return GG_OK;
-    }
-    if (plan->total_tiles == 0) {
-        // K == 0 with a non-empty output: out = 0.
-        if (plan->total_m > 0 && plan->n > 0 && plan->k == 0) {
-            const hipError_t e = hipMemsetAsync(plan->out, 0, size_t(plan->total_m) * plan->n * 2, s);
-            if (e != hipSuccess)
-                return hip_fail(e, "hipMemsetAsync");
-        }
-        return GG_OK;
-    }
-    hipError_t e = gg::launch_grouped_gemm(plan->args, plan->dtype == GG_DTYPE_FP16, plan->grid, s, plan->mode);
-    if (e != hipSuccess)
-        return hip_fail(e, "grouped GEMM launch");
-    if (plan->args.splits > 1) {
-        e = gg::launch_split_reduce(plan->args, plan->dtype == GG_DTYPE_FP16, s, plan->mode);
-        if (e != hipSuccess)
-            return hip_fail(e, "split-K reduction launch");
-    }
-    return GG_OK;
+    return run_plan(plan, stream, false);
 }
 
 void gg_release(gg_plan *plan) {

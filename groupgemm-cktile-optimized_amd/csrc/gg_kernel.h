@@ -117,6 +117,10 @@ hipError_t launch_build_group_table(const int64_t *lens, const int64_t *offs, in
 // offs[0] = 0, offs[g + 1] = offs[g] + lens[g]: group offsets from device lengths. One wave.
 hipError_t launch_group_offsets(const int64_t *lens, int64_t *offs, int group_num, hipStream_t stream);
 
+// out[0 .. bytes) = 0 with 16-byte stores (bytes a multiple of 16), as a kernel: a caller may
+// capture it in a graph, where a hipMemsetAsync node must not be recorded.
+hipError_t launch_zero_fill(void *out, size_t bytes, hipStream_t stream);
+
 // Seeded N(0,1) fill (benchmark input generator).
 hipError_t launch_fill_randn(void *p, size_t count, uint64_t seed, bool fp16, hipStream_t stream);
 

@@ -111,6 +111,12 @@ group_offsets_kernel(const int64_t *lens, int64_t *offs, int group_num) {
     }
 }
 
+__global__ void __launch_bounds__(256) zero_fill_kernel(u32x4 *out, size_t n16) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n16; i += stride)
+        out[i] = u32x4{0u, 0u, 0u, 0u};
+}
+
 // ---------------------------------------------------------------------------------------
 // Benchmark input generator: splitmix64 of (seed, index) -> Box-Muller N(0, 1).
 // ---------------------------------------------------------------------------------------
@@ -229,6 +235,18 @@ hipError_t launch_build_group_table(const int64_t *lens, const int64_t *offs, in
 
 hipError_t launch_group_offsets(const int64_t *lens, int64_t *offs, int group_num, hipStream_t stream) {
     hipLaunchKernelGGL(group_offsets_kernel, dim3(1), dim3(64), 0, stream, lens, offs, group_num);
+    return hipGetLastError();
+}
+
+hipError_t launch_zero_fill(void *out, size_t bytes, hipStream_t stream) {
+    if (bytes % 16 != 0 || (reinterpret_cast<uintptr_t>(out) & 15u) != 0)
+        return hipErrorInvalidValue;
+    const size_t n16 = bytes / 16;
+    if (n16 == 0)
+        return hipSuccess;
+    const size_t blocks = std::min<size_t>((n16 + 255) / 256, 4096);
+    hipLaunchKernelGGL(zero_fill_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
+                       static_cast<u32x4 *>(out), n16);
     return hipGetLastError();
 }
 

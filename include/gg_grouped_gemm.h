@@ -203,6 +203,25 @@ int gg_plan_device_status(const gg_plan *plan, void *stream, int *total_tiles);
  */
 int gg_compute_group_offs(const int64_t *group_lens, int64_t *group_offs, int group_num, void *stream);
 
+/*
+ * gg_prepare_device_lens_op + gg_run + gg_release in one call that allocates nothing. No
+ * counterpart in the reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Same arguments,
+ * rules and results as gg_prepare_device_lens_op followed by gg_run on `stream` (the current
+ * device's); the launches are enqueued and the call returns without a sync.
+ * The group table and its header live in a library-owned device array (scratch) of 131,328
+ * bytes per GPU, held until the process ends: group_num is at most 8192 (else
+ * GG_ERR_UNSUPPORTED, nothing launched). Every call on one GPU shares that array, so calls that
+ * overlap on one GPU (other streams, other host threads) race on it; calls on one stream are
+ * ordered. An empty contraction zero-fills the output with a kernel (no hipMemsetAsync). Sizes
+ * found out of range on the device are not reported (their rows are not written): use a
+ * gg_prepare_device_lens_op plan and gg_plan_device_status to check them.
+ */
+int gg_run_device_lens_noalloc(int op, int a_dtype, int b_dtype, int group_num, int64_t total_m, int64_t n,
+                               int64_t k, const int64_t *group_lens, const int64_t *group_offs, const void *a,
+                               const void *b, const float *a_scale, const float *b_scale, void *out,
+                               void *stream);
+
 /* Message of the last failed call on the calling thread ("" if none). */
 const char *gg_last_error(void);
 
