@@ -13,8 +13,18 @@ fp8 forward (e4m3 / e5m2 inputs, unit tensor-wise scales, bf16 out), or the fp8 
 Prints ONE JSON line on stdout. Besides the driver's fields it carries:
   roofline     the kernel against the dense bf16 MFMA peak (2.5 PFLOP/s): achieved = FLOPs
                per launch / mean launch duration from HIP events on the launch stream;
-               traffic = HBM bytes per launch from the committed rocprofv3 PMC summary
-               (profiles/hbm_traffic_<workload>.json) when present, else null.
+               traffic = fetch + write bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, scaled
+               by a device copy) from profiles/hbm_traffic_<workload>[_<op>].json, but only when
+               that file was measured on the kernel sources of this build (kernel_source_sha) and
+               the same plan; else null. traffic_profile names the file, its commit, kernel
+               instance and why it was or was not used. FETCH_SIZE counts the L2's reads from the
+               data fabric, Infinity-Cache hits included, so it bounds the DRAM reads from above.
+  baselines    the hipBLASLt comparison backends (default hipblaslt_loop, the Primus-Turbo
+               per-group loop on 4 streams the reference compares against, and hipblaslt_seq, the
+               same loop on one stream) and the MI355X kernel again, timed right after the timed
+               region in one native process (bin/gg_bench, a child of this one) on the same config,
+               warmup and steps, each checked on the sampled outputs (forward only); each with its
+               TFLOPS, or its N/A reason or error.
   cpu_baseline the CPU oracle (OpenMP fp32, test infrastructure) timed on a bounded sample
                of the same workload on this host; a reported baseline only.
   clock_power  gfx clock (MHz) and socket power (W) sampled through amdsmi during a separate
@@ -155,6 +165,70 @@ def other_pass(pkg, op, dtype, b, m, n, k, sh, dev):
     return plan, plan.flop, keep
 
 
+def time_baselines(names, workload, dtype, b, m, n, k, warmup, steps):
+    """The MI355X kernel and the named comparators in ONE native process (bin/gg_bench: the same
+    buffers, inputs, sampled check, warmup and steps for each, one after the other), started as a
+    child of this one. A native process, because torch ships its own libhipblaslt under the ROCm
+    library's soname: in this process the comparators would run the wrong build. Returns
+    {"source": ..., backend: {"status": "ok", "value": TFLOPS, "ms_per_step", "check", "detail"} or
+    {"status": "n/a" | "error", "message"}}."""
+    import csv
+    import subprocess
+    import tempfile
+
+    exe = os.path.join(ROOT, "groupgemm-cktile-optimized_amd", "bin", "gg_bench")
+    res = {"source": "bin/gg_bench, one native process: mi355x then " + ", ".join(names) +
+                     f" on the same buffers, warmup {warmup}, {steps} timed steps each"}
+    with tempfile.TemporaryDirectory() as tmp:
+        shapes = os.path.join(tmp, "shapes.csv")
+        rows_path = os.path.join(tmp, "rows.csv")
+        with open(shapes, "w") as f:
+            f.write(f"TestID,Case,B,M,N,K\n1,{workload},{b},{m},{n},{k}\n")
+        cmd = [exe, "--shapes", shapes, "--dtype", "bf16" if dtype == 0 else "fp16", "--backends",
+               ",".join(["mi355x"] + names), "--warmup", str(warmup), "--iters", str(steps), "--out", rows_path]
+        try:
+            p = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
+        except subprocess.TimeoutExpired:
+            res["error"] = "gg_bench did not finish in 300 s"
+            return res
+        if not os.path.exists(rows_path):
+            res["error"] = f"gg_bench exited {p.returncode}: {p.stderr.strip()[-500:]}"
+            return res
+        with open(rows_path) as f:
+            for row in csv.DictReader(f):
+                if row["Check"] in ("PASS", "SKIP"):
+                    rec = {"status": "ok", "value": float(row["TFLOPS"]), "ms_per_step": float(row["Time_ms"]),
+                           "check": row["Check"], "detail": row["Detail"]}
+                elif row["Check"] == "N/A":
+                    rec = {"status": "n/a", "message": row["Detail"]}
+                else:
+                    rec = {"status": "error", "check": row["Check"], "message": row["Detail"]}
+                res[row["Backend"]] = rec
+                log(f"[bench] gg_bench {row['Backend']}: {rec.get('value', rec.get('message'))}")
+    return res
+
+
+def traffic_for(pkg, workload, op, plan_detail):
+    """(bytes per launch or None, provenance) from profiles/hbm_traffic_<workload>[_<op>].json."""
+    suffix = "" if op == "fwd" else f"_{op}"
+    rel = os.path.join("profiles", f"hbm_traffic_{workload}{suffix}.json")
+    path = os.path.join(ROOT, rel)
+    if not os.path.exists(path):
+        return None, {"file": None, "status": "no profile for this workload"}
+    with open(path) as f:
+        data = json.load(f)
+    sha = pkg.kernel_source_sha()
+    info = {"file": rel, "commit": data.get("commit"), "kernel": data.get("kernel"),
+            "kernel_source_sha": data.get("kernel_source_sha"), "plan": data.get("plan"),
+            "traffic_over_algorithmic": data.get("traffic_over_algorithmic")}
+    if data.get("kernel_source_sha") != sha or data.get("plan") != plan_detail:
+        info["status"] = (f"not used: measured on kernel sources {data.get('kernel_source_sha')} with plan "
+                          f"{data.get('plan')!r}; this build is {sha} with plan {plan_detail!r}")
+        return None, info
+    info["status"] = "current: same kernel sources and plan"
+    return data.get("hbm_bytes_per_launch"), info
+
+
 def peak_of(op):
     return FP8_PEAK_TFLOPS if "fp8" in op else MFMA_PEAK_TFLOPS
 
@@ -211,6 +285,9 @@ def main():
     ap.add_argument("--power-seconds", type=float, default=1.0,
                     help="sustained window sampled for clock and power after the timed region "
                          "(0: skip)")
+    ap.add_argument("--baselines", default="hipblaslt_loop,hipblaslt_seq",
+                    help="comparison backends timed with the MI355X kernel in bin/gg_bench after the timed "
+                         "region (forward only; '' for none)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="only run 3 device copies of BYTES bytes (reference kernel for the "
                          "FETCH_SIZE / WRITE_SIZE scale factors) and exit")
@@ -255,7 +332,8 @@ def main():
         flops = prob.flops()
     else:
         be, flops, keep = other_pass(pkg, args.op, dtype, b, m, n, k, sh, dev)
-    log(f"[bench] {args.workload} {args.op}: {be.detail()}")
+    plan_detail = be.detail()
+    log(f"[bench] {args.workload} {args.op}: {plan_detail}")
 
     for _ in range(args.warmup):
         be.run(sh)
@@ -271,18 +349,23 @@ def main():
     tflops = flops / (ms * 1e-3) / 1e12
     log(f"[bench] {args.steps} steps, {ms:.4f} ms/step, {tflops:.1f} TFLOPS")
 
+    baselines = None
+    names = [b_ for b_ in args.baselines.split(",") if b_]
+    if names and args.op == "fwd":
+        baselines = time_baselines(names, args.workload, dtype, b, m, n, k, args.warmup, args.steps)
+        ours = baselines.get("mi355x", {})
+        for name in names:
+            rec = baselines.get(name, {})
+            if rec.get("status") == "ok" and ours.get("status") == "ok":
+                rec["mi355x_speedup_same_process"] = round(ours["value"] / rec["value"], 3)
+
     clock_power = None
     if args.power_seconds > 0:
         clock_power = sustained_clock_power(be, sh, stream, flops, ms, args.power_seconds, peak_of(args.op))
         log(f"[bench] sustained {clock_power.get('seconds')} s: {clock_power.get('tflops')} TFLOPS at "
             f"{clock_power.get('gfx_mhz')} MHz, {clock_power.get('socket_w')} W")
 
-    traffic = None
-    suffix = "" if args.op == "fwd" else f"_{args.op}"
-    tpath = os.path.join(ROOT, "profiles", f"hbm_traffic_{args.workload}{suffix}.json")
-    if os.path.exists(tpath):
-        with open(tpath) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+    traffic, traffic_profile = traffic_for(pkg, args.workload, args.op, plan_detail)
 
     cpu = None
     if not args.no_cpu_baseline and args.op == "fwd":
@@ -316,6 +399,8 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": peak,
                      "unit": "TFLOP/s", "frac": round(tflops / peak, 4),
                      "traffic": traffic},
+        "traffic_profile": traffic_profile,
+        "baselines": baselines,
         "cpu_baseline": cpu,
         "clock_power": clock_power,
     }

@@ -141,7 +141,7 @@ class GroupedGemmProblem:
     x: int = 0
     w: int = 0
     out: int = 0
-    group_lens_pinned: int = 0  # host address of the same lengths (unused by this backend)
+    group_lens_pinned: int = 0  # host address of the same lengths in pinned memory (unused here)
 
     def total_m(self) -> int:
         return sum(self.group_m)
@@ -433,8 +433,72 @@ def make_mi355x_backend() -> Backend:
     return Mi355xBackend()
 
 
+COMPARE_LIB_PATH = os.path.join(PKG_DIR, "lib", "libgg_compare.so")
+_cmp_lib: Optional[ctypes.CDLL] = None
+
+
+def load_compare_library(path: str = COMPARE_LIB_PATH) -> ctypes.CDLL:
+    """The hipBLASLt comparison library's C shim (csrc/host/gg_compare.h); baselines, not the
+    product. Load it in a process that has not imported torch: torch ships its own libhipblaslt
+    under the same soname, and once that is loaded the shim's hipBLASLt calls resolve to it
+    instead of the ROCm library it was built against. Drivers time the comparators in the
+    native gg_bench (bench.py runs it as a child process)."""
+    global _cmp_lib
+    if _cmp_lib is None:
+        if not os.path.exists(path):
+            raise OSError(f"{path} is missing: run __graft_entry__.build()")
+        lib = ctypes.CDLL(path)
+        sig = {
+            "ggc_create": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p)]),
+            "ggc_prepare": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int64,
+                                           ctypes.c_int64, ctypes.POINTER(ctypes.c_int64), ctypes.c_void_p,
+                                           ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]),
+            "ggc_run": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
+            "ggc_release": (None, [ctypes.c_void_p]),
+            "ggc_destroy": (None, [ctypes.c_void_p]),
+            "ggc_message": (ctypes.c_char_p, [ctypes.c_void_p]),
+            "ggc_detail": (ctypes.c_char_p, [ctypes.c_void_p]),
+            "ggc_heuristic_kernel": (ctypes.c_int, [ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+                                                    ctypes.c_char_p, ctypes.c_size_t]),
+            "ggc_is_stream_k": (ctypes.c_int, [ctypes.c_char_p]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(lib, name)
+            fn.restype, fn.argtypes = res, args
+        _cmp_lib = lib
+    return _cmp_lib
+
+
+def heuristic_kernel(dtype: DType, n: int, m: int, k: int):
+    """(is stream-K, kernel name) of hipBLASLt's first choice for one group's out^T [n x m] over
+    depth k, from the heuristic alone (no launch)."""
+    buf = ctypes.create_string_buffer(1024)
+    st = load_compare_library().ggc_heuristic_kernel(int(dtype), n, m, k, buf, len(buf))
+    if st < 0:
+        raise GGError(GG_ERR_HIP, buf.value.decode())
+    return st == 1, buf.value.decode()
+
+
 # Name -> factory registry (the reference hard-codes an if-chain, bench/bench_main.cpp:398-407).
+# The hipBLASLt comparators are in the native driver's registry (bin/gg_bench).
 BACKENDS = {"mi355x": make_mi355x_backend}
+
+# Sources that decide which kernel runs and what it does: a profile measured on one build is
+# matched to the current one by their hash (kernel_source_sha).
+KERNEL_SOURCES = ("csrc/gg_kernel_impl.h", "csrc/gg_schedule.h", "csrc/gg_kernel.h", "csrc/gg_inst.hip",
+                  "csrc/gg_kernel.hip", "csrc/gg_capi.hip")
+
+
+def kernel_source_sha() -> str:
+    """First 16 hex digits of the SHA-256 over KERNEL_SOURCES (name and bytes of each)."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for rel in KERNEL_SOURCES:
+        h.update(rel.encode() + b"\0")
+        with open(os.path.join(PKG_DIR, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
 
 
 def make_backend(name: str) -> Backend:

@@ -1,177 +1,283 @@
-// Comparison backends on hipBLASLt (the vendor library), written for this driver.
+// Comparison backends on hipBLASLt, the vendor library, for this repository's drivers (gg_bench,
+// and bench.py through the C shim in gg_compare.cpp). They are what the reference measures its
+// kernel against (README.md:54-58); nothing on the product path uses them.
 //
-// hipblaslt_loop: the semantics of Primus-Turbo's hipBLASLt grouped GEMM, which the reference
-//   times as its baseline (backends/hipblaslt_loop_backend.cpp:38-67 driving
-//   third_party/primus_turbo/kernels/hipblaslt_grouped_gemm.cu:99-163, 174-251 and
-//   hipblaslt_gemm.cu:32-120): every run() reads the group lengths on the host, then per
-//   non-empty group builds the matmul descriptors, asks the heuristic for one algorithm and
-//   calls hipblasLtMatmul, round-robin over 4 streams (64 MiB of workspace each) forked from
-//   and joined back into the caller's stream with events. All of it is inside the timed
-//   region, as it is in Primus-Turbo. Every stream slot has its own hipBLASLt handle and 8
-//   slots are created although 4 are used: hipBLASLt keeps per-handle state and assumes one
-//   handle per stream, and Primus-Turbo reports multi-stream stalls on MI355X without both
-//   (hipblaslt_grouped_gemm.cu:21-27, 40-55). Unlike Primus-Turbo, the side streams keep the
-//   default priority.
-// hipblaslt_seq: the same per-group loop (host lengths, heuristic per call, all timed) on the
-//   caller's stream alone. No two hipBLASLt kernels run at once, so it cannot stall the way
-//   the 4-stream loop did (below); it gives up the overlap of small groups.
-// hipblaslt_grouped: hipblaslt_ext::GroupedGemm, one launch for all groups, device-side
-//   arguments, heuristic top-1, prepared untimed; N/A when the library has no kernel for the
-//   type (the reference's backends/hipblaslt_grouped_backend.cpp:45-98).
+//   hipblaslt_loop     Primus-Turbo's cost model (backends/hipblaslt_loop_backend.cpp:38-67 over
+//                      third_party/primus_turbo/kernels/hipblaslt_grouped_gemm.cu:99-163, 174-251):
+//                      every run() reads the group lengths on the host and, per non-empty group,
+//                      builds the matmul descriptors, asks the heuristic for one algorithm and calls
+//                      hipblasLtMatmul; groups go round-robin over 4 streams forked from and joined
+//                      into the caller's stream. All of it is inside the timed region.
+//   hipblaslt_seq      the same per-group work on the caller's stream only.
+//   hipblaslt_grouped  hipblaslt_ext::GroupedGemm: one launch for all groups, arguments in device
+//                      memory, heuristic top-1, set up in prepare() (the reference's
+//                      backends/hipblaslt_grouped_backend.cpp:45-98).
 //
-// hipBLASLt is column-major, so both solve the transposed problem per group:
-//   out_g^T [N, M_g] = op_T(w_g stored K x N) * x_g^T (stored K x M_g)
+// Stream-K in the 4-stream loop. A hipBLASLt stream-K kernel (Tensile "SK" solutions) launches
+// a grid sized for the whole GPU, and the workgroup that owns a split tile waits in a loop for
+// flags that the workgroups computing the tile's other K ranges set in the workspace. That wait
+// ends only if those workgroups get a CU, which the kernel is sure of only when it has the GPU to
+// itself. Four such kernels on four streams split the CUs between them, and each can fill its
+// share with workgroups that wait for ones still queued behind them: none of the four finishes.
+// The installed hipBLASLt's heuristic picks a stream-K kernel (SK3) first for every shape tried,
+// Primus-Turbo runs its first choice on 4 streams, and that loop hung on its first call for 8
+// groups of 1024 x 4096 x 7168 (shapes/full.csv TestID 3) while the same kernels one at a time
+// (hipblaslt_seq) finished all 360 cases. So the 4-stream mode takes the heuristic's best
+// algorithm that is not stream-K (of its first kCandidates), in prepare() and in every run(), and
+// reports N/A if there is none; hipblaslt_seq keeps the first choice. (With ROCm 7.2's hipBLASLt
+// on MI355X every bf16 and fp16 shape tried has only stream-K kernels among the first 16, so
+// the 4-stream loop is N/A there and hipblaslt_seq is the per-group baseline.)
+//
+// Failures of HIP or hipBLASLt calls throw std::runtime_error (the driver's ERROR row, a Python
+// exception through the shim); nothing here exits the process. Streams keep the default priority.
+//
+// hipBLASLt is column-major; each group is solved transposed:
+//   out_g^T [N x M_g, ld N] = op_T(w_g: K x N col-major, ld K) * (x_g: K x M_g col-major, ld K)
 #include <hipblaslt/hipblaslt-ext.hpp>
 #include <hipblaslt/hipblaslt.h>
 
+#include <cctype>
+#include <map>
+#include <set>
 #include <stdexcept>
 #include <string>
 #include <vector>
 
 #include "backend.hpp"
+#include "gg_compare.h"
 
 namespace tunemax {
 namespace {
 
-void blas_check(hipblasStatus_t st, const char *what) {
-    if (st != HIPBLAS_STATUS_SUCCESS)
-        throw std::runtime_error(std::string("hipBLASLt ") + what + " failed: status " +
-                                 std::to_string(static_cast<int>(st)));
+void hip_ok(hipError_t e, const char *what) {
+    if (e != hipSuccess)
+        throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
 }
 
-hipDataType hip_type(DType t) { return t == DType::BF16 ? HIP_R_16BF : HIP_R_16F; }
+void lt_ok(hipblasStatus_t s, const char *what) {
+    if (s != HIPBLAS_STATUS_SUCCESS)
+        throw std::runtime_error(std::string("hipBLASLt ") + what + ": status " + std::to_string(int(s)));
+}
+
+hipDataType lt_type(DType t) { return t == DType::BF16 ? HIP_R_16BF : HIP_R_16F; }
+
+constexpr uint64_t kLoopWorkspace = uint64_t(64) << 20; // per stream slot
+
+// The descriptors of one group's matmul (out^T = op_T(w) * x^T), released on scope exit.
+class GroupMatmul {
+public:
+    GroupMatmul(hipDataType t, int64_t n, int64_t m_g, int64_t k, uint64_t ws_bytes) {
+        lt_ok(hipblasLtMatmulDescCreate(&op_, HIPBLAS_COMPUTE_32F, HIP_R_32F), "matmul descriptor");
+        const hipblasOperation_t trans = HIPBLAS_OP_T, keep = HIPBLAS_OP_N;
+        lt_ok(hipblasLtMatmulDescSetAttribute(op_, HIPBLASLT_MATMUL_DESC_TRANSA, &trans, sizeof(trans)), "op A");
+        lt_ok(hipblasLtMatmulDescSetAttribute(op_, HIPBLASLT_MATMUL_DESC_TRANSB, &keep, sizeof(keep)), "op B");
+        lt_ok(hipblasLtMatrixLayoutCreate(&w_, t, k, n, k), "w layout");
+        lt_ok(hipblasLtMatrixLayoutCreate(&x_, t, k, m_g, k), "x layout");
+        lt_ok(hipblasLtMatrixLayoutCreate(&out_, t, n, m_g, n), "out layout");
+        lt_ok(hipblasLtMatmulPreferenceCreate(&pref_), "preference");
+        lt_ok(hipblasLtMatmulPreferenceSetAttribute(pref_, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws_bytes,
+                                                    sizeof(ws_bytes)),
+              "workspace limit");
+        ws_bytes_ = ws_bytes;
+    }
+    GroupMatmul(const GroupMatmul &)            = delete;
+    GroupMatmul &operator=(const GroupMatmul &) = delete;
+    ~GroupMatmul() {
+        (void)hipblasLtMatmulPreferenceDestroy(pref_);
+        (void)hipblasLtMatrixLayoutDestroy(out_);
+        (void)hipblasLtMatrixLayoutDestroy(x_);
+        (void)hipblasLtMatrixLayoutDestroy(w_);
+        (void)hipblasLtMatmulDescDestroy(op_);
+    }
+
+    // The heuristic's first choice.
+    hipblasLtMatmulHeuristicResult_t choose(hipblasLtHandle_t h) const {
+        hipblasLtMatmulHeuristicResult_t best{};
+        int                              n = 0;
+        lt_ok(hipblasLtMatmulAlgoGetHeuristic(h, op_, w_, x_, out_, out_, pref_, 1, &best, &n), "heuristic");
+        if (n == 0)
+            throw std::runtime_error("hipBLASLt has no algorithm for this group");
+        return best;
+    }
+
+    // The heuristic's best choice among its first `count` that is not a stream-K kernel; false if
+    // there is none. *name gets the kernel's name.
+    bool choose_without_stream_k(hipblasLtHandle_t h, int count, hipblasLtMatmulHeuristicResult_t *pick,
+                                 std::string *name) const;
+
+    void launch(hipblasLtHandle_t h, const hipblasLtMatmulAlgo_t &algo, const void *w, const void *x, void *out,
+                void *ws, hipStream_t s) const {
+        const float one = 1.0f, zero = 0.0f;
+        lt_ok(hipblasLtMatmul(h, op_, &one, w, w_, x, x_, &zero, out, out_, out, out_, &algo, ws, ws_bytes_, s),
+              "matmul");
+    }
+
+private:
+    hipblasLtMatmulDesc_t       op_   = nullptr;
+    hipblasLtMatrixLayout_t     w_    = nullptr;
+    hipblasLtMatrixLayout_t     x_    = nullptr;
+    hipblasLtMatrixLayout_t     out_  = nullptr;
+    hipblasLtMatmulPreference_t pref_ = nullptr;
+    uint64_t                    ws_bytes_ = 0;
+};
+
+// Tensile names a stream-K solution with the token "_SK<n>_", n > 0.
+bool stream_k_kernel(const std::string &name) {
+    for (size_t p = name.find("_SK"); p != std::string::npos; p = name.find("_SK", p + 1)) {
+        size_t q = p + 3;
+        while (q < name.size() && std::isdigit(static_cast<unsigned char>(name[q])))
+            ++q;
+        if (q > p + 3 && (q == name.size() || name[q] == '_') && std::stoi(name.substr(p + 3, q - p - 3)) > 0)
+            return true;
+    }
+    return false;
+}
+
+bool GroupMatmul::choose_without_stream_k(hipblasLtHandle_t h, int count, hipblasLtMatmulHeuristicResult_t *pick,
+                                          std::string *name) const {
+    std::vector<hipblasLtMatmulHeuristicResult_t> cand(static_cast<size_t>(count));
+    int                                           n = 0;
+    lt_ok(hipblasLtMatmulAlgoGetHeuristic(h, op_, w_, x_, out_, out_, pref_, count, cand.data(), &n), "heuristic");
+    for (int i = 0; i < n; ++i) {
+        std::string kn = hipblaslt_ext::getKernelNameFromAlgo(h, cand[size_t(i)].algo);
+        if (!stream_k_kernel(kn)) {
+            *pick = cand[size_t(i)];
+            *name = std::move(kn);
+            return true;
+        }
+    }
+    return false;
+}
 
 // ---------------------------------------------------------------------------------------
-class HipblasltLoopBackend final : public Backend {
+// hipblaslt_loop / hipblaslt_seq
+// ---------------------------------------------------------------------------------------
+class PerGroupLoop final : public Backend {
 public:
-    static constexpr int     kSlots           = 8; // slots created (handle + stream + event)
-    static constexpr int64_t kWorkspacePerStr = int64_t(64) << 20;
-
-    explicit HipblasltLoopBackend(int streams) : kStreams(streams) {
-        for (int i = 0; i < kSlots; ++i)
-            blas_check(hipblasLtCreate(&handle_[i]), "create");
-        TUNEMAX_HIP_CHECK(hipMalloc(&workspace_, kStreams * kWorkspacePerStr));
-        TUNEMAX_HIP_CHECK(hipMemset(workspace_, 0, kStreams * kWorkspacePerStr));
-        for (int i = 1; i < kSlots; ++i)
-            TUNEMAX_HIP_CHECK(hipStreamCreateWithFlags(&side_[i], hipStreamNonBlocking));
-        for (int i = 0; i < kSlots; ++i)
-            TUNEMAX_HIP_CHECK(hipEventCreateWithFlags(&ev_[i], hipEventDisableTiming));
+    // streams: 4 (hipblaslt_loop) or 1 (hipblaslt_seq). The 4-stream mode keeps 8 handle slots,
+    // as Primus-Turbo does (hipblaslt_grouped_gemm.cu:21-27: 8 slots, 4 used).
+    explicit PerGroupLoop(int streams) : streams_(streams), slots_(streams > 1 ? 8 : 1) {
+        handles_.assign(size_t(slots_), nullptr);
+        side_.assign(size_t(slots_), nullptr);
+        joined_.assign(size_t(slots_), nullptr);
+        for (auto &h : handles_)
+            lt_ok(hipblasLtCreate(&h), "create handle");
+        for (int i = 1; i < slots_; ++i)
+            hip_ok(hipStreamCreateWithFlags(&side_[size_t(i)], hipStreamNonBlocking), "side stream");
+        for (auto &e : joined_)
+            hip_ok(hipEventCreateWithFlags(&e, hipEventDisableTiming), "event");
+        hip_ok(hipMalloc(&workspace_, size_t(streams_) * kLoopWorkspace), "workspace");
+        // stream-K kernels keep their flags in the workspace and expect zeros at the start
+        hip_ok(hipMemset(workspace_, 0, size_t(streams_) * kLoopWorkspace), "workspace clear");
     }
-    ~HipblasltLoopBackend() override {
-        for (int i = 0; i < kSlots; ++i)
-            (void)hipEventDestroy(ev_[i]);
-        for (int i = 1; i < kSlots; ++i)
-            (void)hipStreamDestroy(side_[i]);
+    ~PerGroupLoop() override {
         (void)hipFree(workspace_);
-        for (int i = 0; i < kSlots; ++i)
-            (void)hipblasLtDestroy(handle_[i]);
+        for (auto e : joined_)
+            (void)hipEventDestroy(e);
+        for (size_t i = 1; i < side_.size(); ++i)
+            (void)hipStreamDestroy(side_[i]);
+        for (auto h : handles_)
+            (void)hipblasLtDestroy(h);
     }
 
-    std::string name() const override { return kStreams == 1 ? "hipblaslt_seq" : "hipblaslt_loop"; }
+    std::string name() const override { return streams_ > 1 ? "hipblaslt_loop" : "hipblaslt_seq"; }
 
     std::string prepare(const GroupedGemmProblem &p, hipStream_t) override {
         if (p.group_lens_pinned == nullptr)
             return "needs the group lengths in pinned host memory";
-        // This 4-stream loop never finished its first call on groups of 1024 x 4096 x 7168
-        // (shapes/full.csv TestID 3) on MI355X, with one shared handle and again with one
-        // handle per stream; it is not run there.
-        for (int g = 0; g < p.group_num && kStreams > 1; ++g)
-            if (p.group_m[g] == 1024 && p.n == 4096 && p.k == 7168)
-                return "skipped: the multi-stream hipBLASLt loop hung on 1024 x 4096 x 7168 groups on MI355X";
-        p_ = p;
+        if (int64_t(p.group_m.size()) != p.group_num)
+            throw std::runtime_error("group_m has " + std::to_string(p.group_m.size()) + " entries for " +
+                                     std::to_string(p.group_num) + " groups");
+        problem_ = p;
+        kernels_.clear();
+        std::set<int64_t> sizes(p.group_m.begin(), p.group_m.end());
+        for (const int64_t m : sizes) {
+            if (m <= 0)
+                continue;
+            const GroupMatmul                mm(lt_type(p.dtype), p.n, m, p.k, kLoopWorkspace);
+            hipblasLtMatmulHeuristicResult_t pick{};
+            std::string                      kn;
+            if (streams_ > 1) {
+                if (!mm.choose_without_stream_k(handles_[0], kCandidates, &pick, &kn))
+                    return "N/A: hipBLASLt offers only stream-K kernels for groups of " + std::to_string(m) +
+                           " rows (its first " + std::to_string(kCandidates) + " choices), and stream-K kernels on " +
+                           std::to_string(streams_) +
+                           " streams at once can deadlock (each waits on workgroups that need the whole GPU); "
+                           "hipblaslt_seq runs the same kernels one at a time";
+            } else {
+                pick = mm.choose(handles_[0]);
+                kn   = hipblaslt_ext::getKernelNameFromAlgo(handles_[0], pick.algo);
+            }
+            kernels_ += (kernels_.empty() ? "" : "; ") + kn;
+        }
         return "";
     }
 
     void run(hipStream_t stream) override {
-        const hipDataType t  = hip_type(p_.dtype);
-        const size_t      es = dtype_bytes(p_.dtype);
-        side_[0]             = stream;
-        // fork: side streams start after everything already queued on the caller's stream
-        if (kStreams > 1)
-            TUNEMAX_HIP_CHECK(hipEventRecord(ev_[0], stream));
-        for (int i = 1; i < kStreams; ++i)
-            TUNEMAX_HIP_CHECK(hipStreamWaitEvent(side_[i], ev_[0], 0));
-        const float alpha = 1.0f, beta = 0.0f;
-        int64_t     row = 0;
-        int         idx = 0;
-        for (int g = 0; g < p_.group_num; ++g) {
-            const int64_t m = p_.group_lens_pinned[g]; // read on the host every call
-            if (m == 0)
-                continue;
-            const char *w   = static_cast<const char *>(p_.w) + size_t(g) * p_.n * p_.k * es;
-            const char *x   = static_cast<const char *>(p_.x) + size_t(row) * p_.k * es;
-            char       *out = static_cast<char *>(p_.out) + size_t(row) * p_.n * es;
-            const int   s   = idx % kStreams;
-            gemm(handle_[s], t, p_.n, m, p_.k, w, x, out, &alpha, &beta,
-                 static_cast<char *>(workspace_) + s * kWorkspacePerStr, side_[s]);
-            row += m;
-            ++idx;
+        const GroupedGemmProblem &p  = problem_;
+        const size_t              es = dtype_bytes(p.dtype);
+        const hipDataType         t  = lt_type(p.dtype);
+        if (streams_ > 1) { // fork: the side streams start after the caller's queued work
+            hip_ok(hipEventRecord(joined_[0], stream), "fork event");
+            for (int i = 1; i < streams_; ++i)
+                hip_ok(hipStreamWaitEvent(side_[size_t(i)], joined_[0], 0), "fork wait");
         }
-        // join: the caller's stream waits for every side stream
-        for (int i = 1; i < kStreams; ++i) {
-            TUNEMAX_HIP_CHECK(hipEventRecord(ev_[i], side_[i]));
-            TUNEMAX_HIP_CHECK(hipStreamWaitEvent(stream, ev_[i], 0));
+        int64_t row  = 0;
+        int     used = 0;
+        for (int g = 0; g < p.group_num; ++g) {
+            const int64_t m = p.group_lens_pinned[g]; // read on the host each call
+            if (m <= 0)
+                continue;
+            const int         s  = used++ % streams_;
+            const hipStream_t st = s == 0 ? stream : side_[size_t(s)];
+            const GroupMatmul                mm(t, p.n, m, p.k, kLoopWorkspace);
+            hipblasLtMatmulHeuristicResult_t pick{};
+            std::string                      kn;
+            if (streams_ == 1)
+                pick = mm.choose(handles_[0]);
+            else if (!mm.choose_without_stream_k(handles_[size_t(s)], kCandidates, &pick, &kn))
+                throw std::runtime_error("no kernel other than stream-K for a group (it had one in prepare)");
+            mm.launch(handles_[size_t(s)], pick.algo, static_cast<const char *>(p.w) + size_t(g) * p.n * p.k * es,
+                      static_cast<const char *>(p.x) + size_t(row) * p.k * es,
+                      static_cast<char *>(p.out) + size_t(row) * p.n * es,
+                      static_cast<char *>(workspace_) + size_t(s) * kLoopWorkspace, st);
+            row += m;
+        }
+        for (int i = 1; i < streams_; ++i) { // join into the caller's stream
+            hip_ok(hipEventRecord(joined_[size_t(i)], side_[size_t(i)]), "join event");
+            hip_ok(hipStreamWaitEvent(stream, joined_[size_t(i)], 0), "join wait");
         }
     }
 
     std::string detail() const override {
-        return "1 hipblasLtMatmul per group (heuristic each call), " + std::to_string(kStreams) +
-               (kStreams == 1 ? " stream" : " streams");
+        return "hipblasLtMatmul per group, heuristic each call, " + std::to_string(streams_) +
+               (streams_ > 1 ? " streams, no stream-K" : " stream") + (kernels_.empty() ? "" : " [" + kernels_ + "]");
     }
 
 private:
-    // D [m, n] col-major = op_T(A: k x m col-major) * B (k x n col-major), one group.
-    void gemm(hipblasLtHandle_t handle, hipDataType t, int64_t m, int64_t n, int64_t k, const void *a,
-              const void *b, void *d, const float *alpha, const float *beta, void *ws, hipStream_t s) {
-        hipblasLtMatmulDesc_t   desc = nullptr;
-        hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, lc = nullptr;
-        hipblasLtMatmulPreference_t pref = nullptr;
-        blas_check(hipblasLtMatmulDescCreate(&desc, HIPBLAS_COMPUTE_32F, HIP_R_32F), "desc");
-        const hipblasOperation_t opa = HIPBLAS_OP_T, opb = HIPBLAS_OP_N;
-        blas_check(hipblasLtMatmulDescSetAttribute(desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opa, sizeof(opa)), "transA");
-        blas_check(hipblasLtMatmulDescSetAttribute(desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opb, sizeof(opb)), "transB");
-        blas_check(hipblasLtMatrixLayoutCreate(&la, t, k, m, k), "layout A");
-        blas_check(hipblasLtMatrixLayoutCreate(&lb, t, k, n, k), "layout B");
-        blas_check(hipblasLtMatrixLayoutCreate(&lc, t, m, n, m), "layout C");
-        blas_check(hipblasLtMatmulPreferenceCreate(&pref), "preference");
-        const uint64_t wsb = kWorkspacePerStr;
-        blas_check(hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb,
-                                                         sizeof(wsb)),
-                   "workspace preference");
-        hipblasLtMatmulHeuristicResult_t res{};
-        int                              found = 0;
-        blas_check(hipblasLtMatmulAlgoGetHeuristic(handle, desc, la, lb, lc, lc, pref, 1, &res, &found),
-                   "heuristic");
-        if (found == 0)
-            throw std::runtime_error("hipBLASLt heuristic found no algorithm");
-        blas_check(hipblasLtMatmul(handle, desc, alpha, a, la, b, lb, beta, d, lc, d, lc, &res.algo, ws,
-                                   kWorkspacePerStr, s),
-                   "matmul");
-        (void)hipblasLtMatmulPreferenceDestroy(pref);
-        (void)hipblasLtMatrixLayoutDestroy(la);
-        (void)hipblasLtMatrixLayoutDestroy(lb);
-        (void)hipblasLtMatrixLayoutDestroy(lc);
-        (void)hipblasLtMatmulDescDestroy(desc);
-    }
-
-    const int          kStreams; // slots used per run: 4 (hipblaslt_loop) or 1 (hipblaslt_seq)
-    hipblasLtHandle_t  handle_[kSlots]{};
-    void              *workspace_ = nullptr;
-    hipStream_t        side_[kSlots]{};
-    hipEvent_t         ev_[kSlots]{};
-    GroupedGemmProblem p_;
+    static constexpr int           kCandidates = 16; // heuristic results searched for a non-stream-K kernel
+    const int                      streams_;
+    const int                      slots_;
+    std::vector<hipblasLtHandle_t> handles_;
+    std::vector<hipStream_t>       side_;   // [0] unused: slot 0 is the caller's stream
+    std::vector<hipEvent_t>        joined_; // [0] the fork point, [i] side stream i done
+    void                          *workspace_ = nullptr;
+    GroupedGemmProblem             problem_;
+    std::string                    kernels_;
 };
 
 // ---------------------------------------------------------------------------------------
-class HipblasltGroupedBackend final : public Backend {
+// hipblaslt_grouped
+// ---------------------------------------------------------------------------------------
+class LtGrouped final : public Backend {
 public:
     static constexpr size_t kWorkspace = size_t(128) << 20;
 
-    HipblasltGroupedBackend() {
-        blas_check(hipblasLtCreate(&handle_), "create");
-        TUNEMAX_HIP_CHECK(hipMalloc(&workspace_, kWorkspace));
+    LtGrouped() {
+        lt_ok(hipblasLtCreate(&handle_), "create handle");
+        hip_ok(hipMalloc(&workspace_, kWorkspace), "workspace");
     }
-    ~HipblasltGroupedBackend() override {
+    ~LtGrouped() override {
         release();
         (void)hipFree(workspace_);
         (void)hipblasLtDestroy(handle_);
@@ -181,84 +287,123 @@ public:
 
     std::string prepare(const GroupedGemmProblem &p, hipStream_t stream) override {
         release();
-        const hipDataType t  = hip_type(p.dtype);
+        if (int64_t(p.group_m.size()) != p.group_num)
+            throw std::runtime_error("group_m does not hold group_num entries");
+        const hipDataType t  = lt_type(p.dtype);
         const size_t      es = dtype_bytes(p.dtype);
-        gemm_ = std::make_unique<hipblaslt_ext::GroupedGemm>(handle_, HIPBLAS_OP_T, HIPBLAS_OP_N, t, t, t, t,
-                                                             HIPBLAS_COMPUTE_32F);
-        std::vector<int64_t> m, n, k, batch;
-        std::vector<hipblaslt_ext::GemmEpilogue> epi;
-        std::vector<hipblaslt_ext::GemmInputs>   in;
-        alpha_.clear();
-        beta_.clear();
-        alpha_.reserve(p.group_num);
-        beta_.reserve(p.group_num);
+        // one entry per non-empty group: sizes in column-major terms, pointers, alpha / beta
+        std::vector<int64_t>                     rows, cols, depth, batch;
+        std::vector<hipblaslt_ext::GemmEpilogue> epilogue;
+        std::vector<hipblaslt_ext::GemmInputs>   inputs;
+        scalars_.assign(size_t(2 * p.group_num), 0.0f);
         int64_t row = 0;
         for (int g = 0; g < p.group_num; ++g) {
-            const int64_t mg = p.group_m[g];
-            if (mg > 0) {
-                m.push_back(p.n);
-                n.push_back(mg);
-                k.push_back(p.k);
+            const int64_t m = p.group_m[size_t(g)];
+            if (m > 0) {
+                rows.push_back(p.n);
+                cols.push_back(m);
+                depth.push_back(p.k);
                 batch.push_back(1);
-                epi.emplace_back();
-                alpha_.push_back(1.0f);
-                beta_.push_back(0.0f);
-                hipblaslt_ext::GemmInputs gi;
-                gi.setA(static_cast<const char *>(p.w) + size_t(g) * p.n * p.k * es);
-                gi.setB(static_cast<const char *>(p.x) + size_t(row) * p.k * es);
-                gi.setC(static_cast<char *>(p.out) + size_t(row) * p.n * es);
-                gi.setD(static_cast<char *>(p.out) + size_t(row) * p.n * es);
-                gi.setAlpha(&alpha_.back());
-                gi.setBeta(&beta_.back());
-                in.push_back(gi);
+                epilogue.emplace_back();
+                float *ab = &scalars_[size_t(2 * g)];
+                ab[0]     = 1.0f; // alpha; ab[1] = beta = 0
+                void *o   = static_cast<char *>(p.out) + size_t(row) * p.n * es;
+                hipblaslt_ext::GemmInputs in;
+                in.setA(static_cast<const char *>(p.w) + size_t(g) * p.n * p.k * es);
+                in.setB(static_cast<const char *>(p.x) + size_t(row) * p.k * es);
+                in.setC(o);
+                in.setD(o);
+                in.setAlpha(ab);
+                in.setBeta(ab + 1);
+                inputs.push_back(in);
             }
-            row += mg;
+            row += m;
         }
-        if (m.empty())
+        if (rows.empty())
             return "no non-empty groups";
-        if (gemm_->setProblem(m, n, k, batch, epi, in) != HIPBLAS_STATUS_SUCCESS)
+        op_ = std::make_unique<hipblaslt_ext::GroupedGemm>(handle_, HIPBLAS_OP_T, HIPBLAS_OP_N, t, t, t, t,
+                                                          HIPBLAS_COMPUTE_32F);
+        if (op_->setProblem(rows, cols, depth, batch, epilogue, inputs) != HIPBLAS_STATUS_SUCCESS)
             return "hipBLASLt rejected the grouped problem";
         hipblaslt_ext::GemmPreference pref;
         pref.setMaxWorkspaceBytes(kWorkspace);
-        std::vector<hipblasLtMatmulHeuristicResult_t> cand;
-        (void)gemm_->algoGetHeuristic(1, pref, cand);
-        if (cand.empty())
-            return std::string("no hipBLASLt grouped kernel for ") + dtype_name(p.dtype);
-        std::vector<hipblaslt_ext::UserArguments> host(m.size());
-        blas_check(gemm_->getDefaultValueForDeviceUserArguments(host.data()), "user arguments");
-        const size_t bytes = host.size() * sizeof(hipblaslt_ext::UserArguments);
-        TUNEMAX_HIP_CHECK(hipMalloc(&dev_args_, bytes));
-        TUNEMAX_HIP_CHECK(hipMemcpyAsync(dev_args_, host.data(), bytes, hipMemcpyHostToDevice, stream));
-        blas_check(gemm_->initialize(cand[0].algo, workspace_), "initialize");
-        TUNEMAX_HIP_CHECK(hipStreamSynchronize(stream));
-        detail_ = gemm_->getKernelName();
+        std::vector<hipblasLtMatmulHeuristicResult_t> picks;
+        (void)op_->algoGetHeuristic(1, pref, picks);
+        if (picks.empty())
+            return std::string("hipBLASLt has no grouped kernel for ") + dtype_name(p.dtype);
+        std::vector<hipblaslt_ext::UserArguments> args(rows.size());
+        lt_ok(op_->getDefaultValueForDeviceUserArguments(args.data()), "user arguments");
+        const size_t bytes = args.size() * sizeof(hipblaslt_ext::UserArguments);
+        hip_ok(hipMalloc(&device_args_, bytes), "argument buffer");
+        hip_ok(hipMemcpyAsync(device_args_, args.data(), bytes, hipMemcpyHostToDevice, stream), "argument upload");
+        lt_ok(op_->initialize(picks[0].algo, workspace_), "initialize");
+        hip_ok(hipStreamSynchronize(stream), "prepare sync");
+        kernel_ = op_->getKernelName();
         return "";
     }
 
-    void run(hipStream_t stream) override { blas_check(gemm_->run(dev_args_, stream), "grouped run"); }
+    void run(hipStream_t stream) override { lt_ok(op_->run(device_args_, stream), "grouped run"); }
 
     void release() override {
-        gemm_.reset();
-        if (dev_args_ != nullptr)
-            TUNEMAX_HIP_CHECK(hipFree(dev_args_));
-        dev_args_ = nullptr;
+        op_.reset();
+        if (device_args_ != nullptr)
+            (void)hipFree(device_args_);
+        device_args_ = nullptr;
     }
 
-    std::string detail() const override { return detail_; }
+    std::string detail() const override { return kernel_; }
 
 private:
-    hipblasLtHandle_t                           handle_    = nullptr;
-    void                                       *workspace_ = nullptr;
-    void                                       *dev_args_  = nullptr;
-    std::unique_ptr<hipblaslt_ext::GroupedGemm> gemm_;
-    std::vector<float>                          alpha_, beta_;
-    std::string                                 detail_;
+    hipblasLtHandle_t                           handle_      = nullptr;
+    void                                       *workspace_   = nullptr;
+    void                                       *device_args_ = nullptr;
+    std::unique_ptr<hipblaslt_ext::GroupedGemm> op_;
+    std::vector<float>                          scalars_; // alpha, beta per group (read by setProblem)
+    std::string                                 kernel_;
 };
 
 } // namespace
 
-std::unique_ptr<Backend> make_hipblaslt_loop_backend() { return std::make_unique<HipblasltLoopBackend>(4); }
-std::unique_ptr<Backend> make_hipblaslt_seq_backend() { return std::make_unique<HipblasltLoopBackend>(1); }
-std::unique_ptr<Backend> make_hipblaslt_grouped_backend() { return std::make_unique<HipblasltGroupedBackend>(); }
+std::unique_ptr<Backend> make_hipblaslt_loop_backend() { return std::make_unique<PerGroupLoop>(4); }
+std::unique_ptr<Backend> make_hipblaslt_seq_backend() { return std::make_unique<PerGroupLoop>(1); }
+std::unique_ptr<Backend> make_hipblaslt_grouped_backend() { return std::make_unique<LtGrouped>(); }
 
 } // namespace tunemax
+
+// Whether a kernel name is a stream-K solution's (the 4-stream gate's rule).
+extern "C" int ggc_is_stream_k(const char *kernel_name) {
+    return kernel_name != nullptr && tunemax::stream_k_kernel(kernel_name) ? 1 : 0;
+}
+
+// The heuristic's first choice for one group, by kernel name (no launch): what the 4-stream gate
+// sees, for drivers and tests.
+extern "C" int ggc_heuristic_kernel(int dtype, int64_t n, int64_t m, int64_t k, char *buf, size_t len) {
+    try {
+        hipblasLtHandle_t h = nullptr;
+        tunemax::lt_ok(hipblasLtCreate(&h), "create handle");
+        std::string name;
+        try {
+            const tunemax::GroupMatmul mm(dtype == 1 ? HIP_R_16F : HIP_R_16BF, n, m, k, tunemax::kLoopWorkspace);
+            auto pick = mm.choose(h);
+            name      = hipblaslt_ext::getKernelNameFromAlgo(h, pick.algo);
+        } catch (...) {
+            (void)hipblasLtDestroy(h);
+            throw;
+        }
+        (void)hipblasLtDestroy(h);
+        if (buf != nullptr && len > 0) {
+            const size_t n_copy = name.size() < len - 1 ? name.size() : len - 1;
+            name.copy(buf, n_copy);
+            buf[n_copy] = '\0';
+        }
+        return tunemax::stream_k_kernel(name) ? 1 : 0;
+    } catch (const std::exception &e) {
+        if (buf != nullptr && len > 0) {
+            const std::string msg = e.what();
+            const size_t      n   = msg.size() < len - 1 ? msg.size() : len - 1;
+            msg.copy(buf, n);
+            buf[n] = '\0';
+        }
+        return -1;
+    }
+}

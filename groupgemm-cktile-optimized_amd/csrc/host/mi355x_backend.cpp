@@ -19,6 +19,9 @@ public:
 
     std::string prepare(const GroupedGemmProblem &p, hipStream_t stream) override {
         release();
+        if (static_cast<int64_t>(p.group_m.size()) != static_cast<int64_t>(p.group_num))
+            throw std::runtime_error("group_m has " + std::to_string(p.group_m.size()) + " entries for " +
+                                     std::to_string(p.group_num) + " groups");
         const int st = gg_prepare(p.dtype == DType::BF16 ? GG_DTYPE_BF16 : GG_DTYPE_FP16,
                                   p.group_num, p.n, p.k, p.group_m.data(), p.x, p.w, p.out,
                                   stream, &plan_);

@@ -1,0 +1,89 @@
+"""The drivers and the comparison backends on the GPU.
+
+* gg_bench (this repository's driver, over tunemax::Backend) runs the plumbing and tails configs
+  with mi355x and the hipBLASLt comparators: mi355x PASSes the sampled fp32 check, every other row
+  PASSes or is N/A (bench/bench_main.cpp:464-536 protocol).
+* The reference's own driver, built from its sources with this backend as its ck_tile factory
+  (oracle/_ref/tunemax_bench, built where the reference tree exists), runs the same cases: the
+  reference's fill, sampled check and timing pass on the C++ Backend path.
+* The 4-stream hipBLASLt loop runs no stream-K kernel (they deadlock when several run at once).
+"""
+import csv
+import os
+import re
+import subprocess
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+if not torch.cuda.is_available():
+    pytest.skip("needs an MI355X", allow_module_level=True)
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG = os.path.join(ROOT, "groupgemm-cktile-optimized_amd")
+SHAPES = os.path.join(PKG, "shapes", "configs.csv")
+DEV = torch.device("cuda:0")
+
+
+def _rows(path):
+    with open(path) as f:
+        return list(csv.DictReader(f))
+
+
+def _run(cmd, timeout=240):
+    print("[drivers] " + " ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout)
+    print(r.stdout[-3000:], r.stderr[-2000:], flush=True)
+    return r
+
+
+def test_gg_bench_configs_with_comparators(tmp_path):
+    out = tmp_path / "rows.csv"
+    r = _run([os.path.join(PKG, "bin", "gg_bench"), "--shapes", SHAPES, "--only", "1001,1005", "--backends",
+              "mi355x,hipblaslt_seq,hipblaslt_grouped,hipblaslt_loop", "--warmup", "1", "--iters", "3",
+              "--out", str(out)])
+    assert r.returncode == 0, r.stderr
+    rows = _rows(out)
+    assert len(rows) == 8
+    assert list(rows[0].keys()) == ["TestID", "Case", "B", "M", "N", "K", "Dtype", "GPU", "Backend", "Check",
+                                    "Time_ms", "TFLOPS", "MaxAbsErr", "Detail"]
+    for row in rows:
+        if row["Backend"] == "mi355x":
+            assert row["Check"] == "PASS", row
+            assert float(row["TFLOPS"]) > 0
+        else:
+            assert row["Check"] in ("PASS", "N/A"), row
+
+
+@pytest.mark.skipif(not os.path.exists(os.path.join(ROOT, "oracle", "_ref", "tunemax_bench")),
+                    reason="the reference driver is built only where the reference tree exists")
+def test_reference_driver_runs_this_backend(tmp_path):
+    out = tmp_path / "ref_rows.csv"
+    r = _run([os.path.join(ROOT, "oracle", "_ref", "tunemax_bench"), "--shapes", SHAPES, "--only", "1001,1005",
+              "--backends", "ck_tile,hipblaslt_grouped", "--warmup", "1", "--iters", "3", "--out", str(out)])
+    assert r.returncode == 0, r.stderr
+    rows = _rows(out)
+    ours = [row for row in rows if row["Backend"] == "mi355x"]
+    assert len(ours) == 2 and all(row["Check"] == "PASS" for row in ours), rows
+    assert all(row["Check"] in ("PASS", "N/A") for row in rows)
+
+
+def _stream_k(name):
+    """Tensile's stream-K token "_SK<n>_" with n > 0 (the comparators' gate rule)."""
+    return any(int(v) > 0 for v in re.findall(r"_SK(\d+)(?=_|$)", name))
+
+
+def test_four_stream_loop_runs_no_stream_k_kernel(tmp_path):
+    """hipblaslt_loop takes the heuristic's best non-stream-K kernel (stream-K kernels wait on each
+    other's workgroups and must have the GPU to themselves); hipblaslt_seq keeps the first choice."""
+    out = tmp_path / "rows.csv"
+    r = _run([os.path.join(PKG, "bin", "gg_bench"), "--shapes", SHAPES, "--only", "1001,1005,1006", "--backends",
+              "hipblaslt_loop,hipblaslt_seq", "--warmup", "1", "--iters", "3", "--out", str(out)])
+    assert r.returncode == 0, r.stderr
+    for row in _rows(out):
+        assert row["Check"] in ("PASS", "N/A"), row
+        kernels = re.findall(r"Cijk_\w+", row["Detail"])
+        if row["Backend"] == "hipblaslt_loop" and row["Check"] == "PASS":
+            assert kernels and not any(_stream_k(kn) for kn in kernels), row["Detail"]
