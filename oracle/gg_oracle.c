@@ -451,6 +451,8 @@ static inline uint64_t splitmix64(uint64_t z) {
     return z ^ (z >> 31);
 }
 
+uint64_t gg_oracle_splitmix64(uint64_t z) { return splitmix64(z); }
+
 void gg_oracle_fill_randn(int dtype, uint16_t *p, size_t count, uint64_t seed) {
 #pragma omp parallel for schedule(static) if (count > 65536)
     for (size_t i = 0; i < count; ++i) {

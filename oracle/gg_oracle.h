@@ -119,6 +119,9 @@ int64_t gg_oracle_check(const float *got, const float *ref, int64_t count, doubl
 
 /* Seeded N(0,1) generator of the reference driver, restated on the host. */
 void gg_oracle_fill_randn(int dtype, uint16_t *p, size_t count, uint64_t seed);
+/* The generator's splitmix64 stage alone: mix(z + 0x9E3779B97F4A7C15), i.e. the next output of a
+ * splitmix64 whose state is z (bench/bench_main.cpp:160-165). */
+uint64_t gg_oracle_splitmix64(uint64_t z);
 
 /* std::mt19937_64: `count` outputs of an engine seeded with `seed`. */
 void gg_mt19937_64_seq(uint64_t seed, uint64_t *out, size_t count);

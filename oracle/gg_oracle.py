@@ -63,6 +63,7 @@ def lib() -> ctypes.CDLL:
             "gg_oracle_check": (ctypes.c_int64, [_PF, _PF, ctypes.c_int64, ctypes.c_double, ctypes.c_double,
                                                  ctypes.POINTER(ctypes.c_double)]),
             "gg_oracle_fill_randn": (None, [ctypes.c_int, _P16, ctypes.c_size_t, ctypes.c_uint64]),
+            "gg_oracle_splitmix64": (ctypes.c_uint64, [ctypes.c_uint64]),
             "gg_mt19937_64_seq": (None, [ctypes.c_uint64, _PU64, ctypes.c_size_t]),
             "gg_mt19937_64_nth": (ctypes.c_uint64, [ctypes.c_uint64, ctypes.c_uint64]),
             "gg_oracle_threads": (ctypes.c_int, []),
@@ -224,6 +225,11 @@ def fill_randn(dtype: int, count: int, seed: int) -> np.ndarray:
     out = np.empty(count, dtype=np.uint16)
     lib().gg_oracle_fill_randn(dtype, _ptr(out, ctypes.c_uint16), count, seed)
     return out
+
+
+def splitmix64(z: int) -> int:
+    """The input generator's splitmix64 stage: the next output of a splitmix64 in state z."""
+    return int(lib().gg_oracle_splitmix64(z))
 
 
 def mt19937_64(seed: int, count: int) -> np.ndarray:

@@ -340,6 +340,30 @@ def test_check_rule(oracle):
 # --------------------------------------------------------------------------------------
 # input generator (bench/bench_main.cpp:160-176); exact bits unpinned (device math library)
 # --------------------------------------------------------------------------------------
+# splitmix64 (Steele, Lea and Flood 2014; Vigna's splitmix64.c): the published first outputs of
+# the generator seeded with 0, which are also java.util.SplittableRandom(0)'s first nextLong()
+# values. The stage is stateless in the fill (state = seed ^ index * 0x2545F4914F6CDD1D), so the
+# n-th output is splitmix64(n * 0x9E3779B97F4A7C15). A wrong constant, shift or order fails this.
+SPLITMIX64_SEED0 = [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F, 0xF88BB8A8724C81EC,
+                    0x1B39896A51A8749B]
+
+
+def test_splitmix64_known_answers(oracle):
+    gamma = 0x9E3779B97F4A7C15
+    for i, want in enumerate(SPLITMIX64_SEED0):
+        assert oracle.splitmix64((i * gamma) % (1 << 64)) == want, i
+
+
+def test_fill_uses_splitmix_of_seed_xor_scaled_index(oracle):
+    """Element i of the fill is a function of splitmix64(seed ^ i * 0x2545F4914F6CDD1D) alone: two
+    (seed, index) pairs with the same splitmix input give the same element (bench_main.cpp:170)."""
+    c = 0x2545F4914F6CDD1D
+    mask = (1 << 64) - 1
+    i, j, seed_i = 3, 17, 1
+    seed_j = seed_i ^ ((i * c) & mask) ^ ((j * c) & mask)
+    a = oracle.fill_randn(0, i + 1, seed_i)[i]
+    b = oracle.fill_randn(0, j + 1, seed_j)[j]
+    assert a == b
 @pytest.mark.parametrize("dt", [0, 1])
 def test_fill_randn_is_standard_normal(oracle, dt):
     from scipy import stats
