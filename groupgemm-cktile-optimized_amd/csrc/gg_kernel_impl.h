@@ -65,6 +65,13 @@
 namespace gg {
 namespace {
 
+// Pointer to const T in the constant address space (scalar loads; the data is invariant for
+// the kernel's lifetime).
+template <typename T> using const_space = const __attribute__((address_space(4))) T *;
+template <typename T> __device__ __forceinline__ const_space<T> to_const_space(const T *p) {
+    return (const_space<T>)(p);
+}
+
 typedef int      i32x2 __attribute__((ext_vector_type(2)));
 typedef int      i32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
@@ -155,40 +162,78 @@ constexpr bool mode_b_mn(int m) { return mode_layout(m) == kDgrad || mode_layout
 constexpr int reads_per_frag(bool mn) { return mn ? 4 : 2; }
 
 // ---------------------------------------------------------------------------------------
-// Slot plan of one K step. Row mi (0..7) issues 16 MFMAs, idx = kh * 8 + ni; each function
+// Slot plan of one K step. Row mi (0..R-1) issues 16 MFMAs, idx = kh * 8 + ni; each function
 // says which memory operation follows MFMA idx of row mi (-1: none). LDS reads sit after odd
 // MFMAs, DMAs after even ones, so no MFMA gap holds more than one memory operation.
 // NA / NB: LDS reads per fragment of A / B (2 K-major, 4 MN-major); a read op index r is the
 // k-half (K-major) or k-half * 2 + half (MN-major).
+// R: rows with MFMAs, 8 (256-row tiles) or 6 (short tiles). The barrier, and the next step's
+// row-0 x reads behind it, sit in the last row, so MFMAs cover both whatever R is; a plan laid
+// out for 8 rows would leave a short tile's last two rows of memory operations with no MFMAs
+// between them, ending every step with an exposed barrier and LDS read latency.
 // ---------------------------------------------------------------------------------------
-constexpr int kBarRow = 7; // the step's barrier follows MFMA Plan::bar of this row
 static_assert(GG_BAR_IDX >= 5 && GG_BAR_IDX <= 11 && GG_BAR_IDX % 2 == 1, "barrier slot");
 
-constexpr int plan_epi(int mi, int idx);
-template <int NA, int NB> struct Plan {
-    static constexpr int slots = 16, early = kEarlyA;
+// First step of a cross tile: store s (0-3, see store_line) of the previous tile's row block
+// mi+1 is issued after MFMA 2 + 4s of row mi (row block 0 before the step).
+constexpr int plan_epi(int mi, int idx) {
+    return (mi < 7 && idx % 4 == 2) ? (idx - 2) / 4 : -1;
+}
+template <int NA, int NB, int R = 8> struct Plan {
+    static_assert(R == 8 || R == 6, "plans for 8 or 6 rows of MFMAs");
+    static constexpr int rows = R, slots = 16, early = kEarlyA;
+    static constexpr int last = R - 1; // the row that holds the step's barrier
     static constexpr int epi(int mi, int idx) { return plan_epi(mi, idx); }
-    // The w fragments of row 7 are read before the barrier, at MFMAs 1 .. 2 NB - 1.
-    static constexpr int bar = GG_BAR_IDX > 2 * NB + 1 ? GG_BAR_IDX : 2 * NB + 1;
+    // R = 8: the w fragments of row 7 are read before the barrier, at MFMAs 1 .. 2 NB - 1.
+    static constexpr int bar = R < 8 || GG_BAR_IDX > 2 * NB + 1 ? GG_BAR_IDX : 2 * NB + 1;
     static constexpr int row0_first = GG_ROW0_AT_BAR ? bar : bar + 2;
-    static_assert(row0_first + 2 * (NA - 1) <= 15, "row-0 reads fit in row 7");
+    static_assert(row0_first + 2 * (NA - 1) <= 15, "row-0 reads fit in the last row");
 
-    // x fragments of row mi+1 into the register ring: the first NA odd slots of rows 0-6.
+    // x fragments of row mi+1 into the register ring: the first NA odd slots of rows 0 .. R-2.
     static constexpr int read_a_next(int mi, int idx) {
-        return (mi < 7 && idx % 2 == 1 && idx < 2 * NA) ? idx / 2 : -1;
+        return (mi < last && idx % 2 == 1 && idx < 2 * NA) ? idx / 2 : -1;
     }
-    // w fragments of step kt+1, column block ni = mi: the next NB odd slots of rows 0-6; in
-    // row 7 the first NB odd slots, so they are complete before the barrier.
-    static constexpr int read_b_next(int mi, int idx) {
+    // R < 8: the w reads of step kt+1 (q = block * NB + read, in order) fill the odd slots after
+    // the x reads of rows 0 .. R-2, spread evenly (row mi takes q in [q_first(mi), q_first(mi+1)));
+    // what does not fit there takes the first odd slots of the last row, before the barrier.
+    static constexpr int cap     = 8 - NA; // w-read slots of each of rows 0 .. R-2
+    static constexpr int n_first = 8 * NB < (R - 1) * cap ? 8 * NB : (R - 1) * cap;
+    static constexpr int q_first(int mi) { return (mi * n_first + (R - 2)) / (R - 1); }
+    static constexpr int read_b_q(int mi, int idx) {
         if (idx % 2 == 0)
             return -1;
-        if (mi < 7)
-            return (idx >= 2 * NA && idx < 2 * (NA + NB)) ? (idx - 2 * NA) / 2 : -1;
-        return idx < 2 * NB ? idx / 2 : -1;
+        if (mi == last) {
+            const int q = n_first + idx / 2;
+            return (q < 8 * NB && idx < bar) ? q : -1;
+        }
+        if (idx < 2 * NA)
+            return -1;
+        const int q = q_first(mi) + (idx - 2 * NA) / 2;
+        return q < q_first(mi + 1) ? q : -1;
+    }
+    // w fragments of step kt+1: read op index of column block read_b_blk(mi, idx).
+    // R = 8: block ni = mi, the next NB odd slots of rows 0-6; in row 7 the first NB odd slots,
+    // so they are complete before the barrier.
+    static constexpr int read_b_next(int mi, int idx) {
+        if constexpr (R < 8) {
+            return read_b_q(mi, idx) >= 0 ? read_b_q(mi, idx) % NB : -1;
+        } else {
+            if (idx % 2 == 0)
+                return -1;
+            if (mi < 7)
+                return (idx >= 2 * NA && idx < 2 * (NA + NB)) ? (idx - 2 * NA) / 2 : -1;
+            return idx < 2 * NB ? idx / 2 : -1;
+        }
+    }
+    static constexpr int read_b_blk(int mi, int idx) {
+        if constexpr (R < 8)
+            return read_b_q(mi, idx) >= 0 ? read_b_q(mi, idx) / NB : -1;
+        else
+            return read_b_next(mi, idx) >= 0 ? mi : -1;
     }
     // x fragments of row 0 of step kt+1, right after the barrier.
     static constexpr int read_a_row0(int mi, int idx) {
-        return (mi == 7 && idx % 2 == 1 && idx >= row0_first && idx < row0_first + 2 * NA)
+        return (mi == last && idx % 2 == 1 && idx >= row0_first && idx < row0_first + 2 * NA)
                    ? (idx - row0_first) / 2
                    : -1;
     }
@@ -200,17 +245,21 @@ template <int NA, int NB> struct Plan {
         const int j = kEarlyA + mi * per + idx / step;
         return j < kLoads ? j : -1;
     }
-    // DMA j of B(kt+3): two per row in rows GG_B_ROW0 .. +3.
+    // DMA j of B(kt+3). R = 8: two per row in rows GG_B_ROW0 .. +3. R < 8: four per row (after
+    // MFMAs 0, 4, 8, 12) in rows 3 and 4.
     static constexpr int load_b(int mi, int idx) {
-        return (mi >= GG_B_ROW0 && mi < GG_B_ROW0 + 4 && (idx == GG_B_SLOT0 || idx == GG_B_SLOT0 + 8))
-                   ? (mi - GG_B_ROW0) * 2 + (idx - GG_B_SLOT0) / 8
-                   : -1;
+        if constexpr (R < 8)
+            return (mi >= 3 && mi < 5 && idx % 4 == 0) ? (mi - 3) * 4 + idx / 4 : -1;
+        else
+            return (mi >= GG_B_ROW0 && mi < GG_B_ROW0 + 4 && (idx == GG_B_SLOT0 || idx == GG_B_SLOT0 + 8))
+                       ? (mi - GG_B_ROW0) * 2 + (idx - GG_B_SLOT0) / 8
+                       : -1;
     }
-    // DMA j < kEarlyA of A(kt+2): the first even slots of row 7 after the barrier (A(kt)'s
+    // DMA j < kEarlyA of A(kt+2): the first even slots of the last row after the barrier (A(kt)'s
     // stage is free once every wave passed it).
     static constexpr int load_a_early(int mi, int idx) {
         const int j = (idx - (bar + 1)) / 2;
-        return (mi == 7 && idx > bar && idx % 2 == 0 && j < kEarlyA) ? j : -1;
+        return (mi == last && idx > bar && idx % 2 == 0 && j < kEarlyA) ? j : -1;
     }
     // The DMA that follows MFMA idx of row mi: 0 none, 1 A(kt+1), 2 B(kt+3), 3 A(kt+2).
     static constexpr int dma_kind(int mi, int idx) {
@@ -227,35 +276,57 @@ template <int NA, int NB> struct Plan {
     // longer.
     static constexpr int vm_at_barrier() {
         int last_a = -1;
-        for (int p = 0; p < 8 * 16; ++p)
+        for (int p = 0; p < R * 16; ++p)
             if (load_a(p / 16, p % 16) >= 0)
                 last_a = p;
         int n = 0;
-        for (int p = last_a + 1; p < kBarRow * 16 + bar; ++p)
+        for (int p = last_a + 1; p < last * 16 + bar; ++p)
             n += (load_b(p / 16, p % 16) >= 0) + (load_a_early(p / 16, p % 16) >= 0);
         return n;
     }
     template <typename F> static constexpr int count(F f) {
         int n = 0;
-        for (int p = 0; p < 8 * 16; ++p)
+        for (int p = 0; p < R * 16; ++p)
             n += f(p / 16, p % 16) >= 0;
         return n;
     }
     static constexpr bool check() {
-        for (int p = 0; p < 8 * 16; ++p) {
+        int per_block[8] = {};
+        for (int p = 0; p < R * 16; ++p) {
             const int mi = p / 16, idx = p % 16;
             const int dmas  = (load_a(mi, idx) >= 0) + (load_b(mi, idx) >= 0) + (load_a_early(mi, idx) >= 0);
             const int reads = (read_a_next(mi, idx) >= 0) + (read_b_next(mi, idx) >= 0) +
                               (read_a_row0(mi, idx) >= 0);
             if (dmas > 1 || reads > 1 || (dmas && reads))
                 return false;
+            // every read of step kt+1's w precedes the barrier; the row-0 x reads follow it;
+            // the fused stores of a cross tile's first step (rows 0 .. R-2) meet no DMA
+            if (mi == last && ((read_b_next(mi, idx) >= 0 && idx >= bar) || (read_a_row0(mi, idx) >= 0 && idx < bar)))
+                return false;
+            if (mi < last && epi(mi, idx) >= 0 && dmas)
+                return false;
+            if (read_b_next(mi, idx) >= 0) {
+                const int b = read_b_blk(mi, idx);
+                if (b < 0 || b > 7 || read_b_next(mi, idx) != per_block[b])
+                    return false;
+                ++per_block[b];
+            }
         }
+        for (int b = 0; b < 8; ++b)
+            if (per_block[b] != NB)
+                return false;
+        // A(kt+1)'s DMAs all precede the barrier
+        for (int p = last * 16 + bar; p < R * 16; ++p)
+            if (load_a(p / 16, p % 16) >= 0)
+                return false;
         return count(load_a) == kLoads - kEarlyA && count(load_b) == kLoads &&
                count(load_a_early) == kEarlyA && count(read_b_next) == 8 * NB &&
-               count(read_a_next) == 7 * NA && count(read_a_row0) == NA;
+               count(read_a_next) == (R - 1) * NA && count(read_a_row0) == NA;
     }
 };
 static_assert(Plan<2, 2>::check() && Plan<2, 4>::check() && Plan<4, 4>::check(), "slot plans");
+static_assert(Plan<2, 2, 6>::check() && Plan<2, 4, 6>::check(), "short-tile slot plans");
+static_assert(Plan<2, 2, 6>::vm_at_barrier() == 8 && Plan<2, 2>::vm_at_barrier() == 8, "barrier waits");
 
 // fp8 K step: 128 fp8 values per 128-byte row; v_mfma_f32_16x16x128_f8f6f4 takes 32 bytes of a
 // row per lane, so a row mi of the step is 8 MFMAs of twice the length, and a fragment is two
@@ -268,7 +339,7 @@ static_assert(Plan<2, 2>::check() && Plan<2, 4>::check() && Plan<4, 4>::check(),
 // beside a read in one gap.
 template <int NA, int NB> struct Plan8 {
     static_assert((NA == 2 || NA == 4) && (NB == 2 || NB == 4), "reads per fragment");
-    static constexpr int slots = 8, early = 1, bar = NA == 4 ? 4 : 5;
+    static constexpr int rows = 8, last = 7, slots = 8, early = 1, bar = NA == 4 ? 4 : 5;
     static constexpr int read_a_next(int mi, int idx) {
         return (mi < 7 && idx % 2 == 1 && idx < 2 * NA) ? idx / 2 : -1;
     }
@@ -283,6 +354,7 @@ template <int NA, int NB> struct Plan8 {
             return (idx == 2 || idx == 6) ? idx / 4 : -1;
         return idx % 2 == 0 ? idx / 2 : -1;
     }
+    static constexpr int read_b_blk(int mi, int idx) { return read_b_next(mi, idx) >= 0 ? mi : -1; }
     static constexpr int read_a_row0(int mi, int idx) {
         if (mi != 7)
             return -1;
@@ -316,7 +388,7 @@ template <int NA, int NB> struct Plan8 {
             if (load_a(p / slots, p % slots) >= 0)
                 last_a = p;
         int n = 0;
-        for (int p = last_a + 1; p < kBarRow * slots + bar; ++p)
+        for (int p = last_a + 1; p < last * slots + bar; ++p)
             n += (load_b(p / slots, p % slots) >= 0) + (load_a_early(p / slots, p % slots) >= 0);
         return n;
     }
@@ -492,11 +564,6 @@ constexpr int  kStoreCpol     = GG_STORE_CPOL;
 #endif
 constexpr bool kPartialNt = GG_PARTIAL_NT; // split-K partial sums stored non-temporal (2-5 % slower)
 
-// First step of a cross tile: store s (0-3, see store_line) of the previous tile's row block
-// mi+1 is issued after MFMA 2 + 4s of row mi (row block 0 before the step).
-constexpr int plan_epi(int mi, int idx) {
-    return (mi < 7 && idx % 4 == 2) ? (idx - 2) / 4 : -1;
-}
 
 // Inclusive prefix sum over the 64 lanes of a wave.
 __device__ __forceinline__ int64_t wave_inclusive_sum(int64_t v, int lane) {
@@ -600,7 +667,7 @@ grouped_gemm_kernel(const KernelArgs args) {
     // the launch time whatever the partial ones save, and the per-tile instances stay smaller.
     constexpr bool kThin  = kTailSkip && CROSS;
     using P = std::conditional_t<F8, Plan8<reads_per_frag(A_MN), reads_per_frag(B_MN)>,
-                                 Plan<reads_per_frag(A_MN), reads_per_frag(B_MN)>>;
+                                 Plan<reads_per_frag(A_MN), reads_per_frag(B_MN), RB>>;
     static_assert(!(F8 && F16), "fp8 writes bf16");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kLdsBytes];
     typedef __attribute__((address_space(3))) uint8_t lds_u8;
@@ -789,6 +856,11 @@ grouped_gemm_kernel(const KernelArgs args) {
     };
     const int bad_off = static_cast<int>(0x80000000u);
     int       g       = 0; // group hint of locate_tile (logical tiles only grow)
+    // The group table and the fp8 scales do not change while the kernel runs: read through the
+    // constant address space they take scalar loads (lgkmcnt). Through a global pointer the
+    // compiler issues vector loads and waits for them with vmcnt(0), which also drains every
+    // operand DMA in flight, once per table entry the tile walk reads.
+    const const_space<GroupEntry> const_table = to_const_space(args.groups);
     auto      make_tile = [&](int t) -> Tile {
         // split-K: one unit per workgroup, no L2 sharing across rounds to arrange
         const int split = splits > 1 ? t / total_tiles : 0;
@@ -806,9 +878,11 @@ grouped_gemm_kernel(const KernelArgs args) {
             const int m_tiles = ((LAYOUT == kWgrad ? args.m_out : ge.m) + kTileM - 1) / kTileM;
             band_coords(L - ge.tile0, m_tiles, args.n_tiles, args.band, &tm, &tn);
         } else {
-            locate_tile(L, args.groups, args.group_num, args.n_tiles, args.band, &g, &tm, &tn,
+            locate_tile(L, const_table, args.group_num, args.n_tiles, args.band, &g, &tm, &tn,
                         LAYOUT == kWgrad ? args.m_out : 0, SHORT ? args.tile_m : kTileM);
-            ge = args.groups[g];
+            ge.row0  = const_table[g].row0;
+            ge.m     = const_table[g].m;
+            ge.tile0 = const_table[g].tile0;
         }
         const uint8_t   *xa = static_cast<const uint8_t *>(args.x); // A storage (bytes)
         const uint8_t   *wb = static_cast<const uint8_t *>(args.w); // B storage (bytes)
@@ -854,7 +928,7 @@ grouped_gemm_kernel(const KernelArgs args) {
             tl.c_ptr = static_cast<uint16_t *>(args.out) + row0 * N + col0;
         }
         if constexpr (F8)
-            tl.scale = args.x_scale[0] * args.w_scale[g];
+            tl.scale = to_const_space(args.x_scale)[0] * to_const_space(args.w_scale)[g];
         tl.rows = __builtin_amdgcn_readfirstlane(active_rows(ILV, tl.m_valid, tl.n_valid, wm, wn));
         return tl;
     };
@@ -1123,7 +1197,7 @@ grouped_gemm_kernel(const KernelArgs args) {
         const DmaSrc src_a1 = dma_src(A_OP{}, kt + 1, chk{}); // A(kt+1)
         const DmaSrc src_b3 = dma_src(B_OP{}, kt + 3, chk{}); // B(kt+3)
         const DmaSrc src_a2 = dma_src(A_OP{}, kt + 2, chk{}); // A(kt+2)
-        sfor<0, 8>([&](auto mi_) {
+        sfor<0, P::rows>([&](auto mi_) {
             constexpr int mi = decltype(mi_)::value;
             sfor<0, P::slots>([&](auto idx_) {
                 constexpr int idx = decltype(idx_)::value;
@@ -1137,7 +1211,7 @@ grouped_gemm_kernel(const KernelArgs args) {
                 sched_fence();
                 row_mfma.template operator()<SA, FIRST>(mi_, idx_);
                 sched_fence();
-                if constexpr (mi == kBarRow && idx == P::bar) {
+                if constexpr (mi == P::last && idx == P::bar) {
                     wait_vm_lds_barrier<P::vm_at_barrier()>();
                     sched_fence();
                 }
@@ -1147,8 +1221,9 @@ grouped_gemm_kernel(const KernelArgs args) {
                     sched_fence();
                 }
                 if constexpr (P::read_b_next(mi, idx) >= 0) {
-                    read_frag.template operator()<B_MN, P::read_b_next(mi, idx)>(fb[NX][mi], b_rd[SB_NEXT],
-                                                                                 ic<mi>{});
+                    constexpr int bb = P::read_b_blk(mi, idx);
+                    read_frag.template operator()<B_MN, P::read_b_next(mi, idx)>(fb[NX][bb], b_rd[SB_NEXT],
+                                                                                 ic<bb>{});
                     sched_fence();
                 }
                 if constexpr (P::read_a_row0(mi, idx) >= 0) {
@@ -1192,12 +1267,12 @@ grouped_gemm_kernel(const KernelArgs args) {
             dma16(dst + j * 4096, dma_voff(b_op, j, d, chk{}), d.rs, d.so);
             sched_fence();
         };
-        sfor<0, 8>([&](auto mi_) {
+        sfor<0, P::rows>([&](auto mi_) {
             constexpr int mi = decltype(mi_)::value;
             sfor<0, P::slots>([&](auto idx_) {
                 constexpr int idx = decltype(idx_)::value;
                 constexpr int dk = P::dma_kind(mi, idx), dj = P::dma_j(mi, idx);
-                if constexpr (mi == kBarRow && idx == P::bar) {
+                if constexpr (mi == P::last && idx == P::bar) {
                     sched_fence();
                     wait_vm_lds_barrier<P::vm_at_barrier()>();
                     sched_fence();
@@ -1208,8 +1283,9 @@ grouped_gemm_kernel(const KernelArgs args) {
                     sched_fence();
                 }
                 if constexpr (P::read_b_next(mi, idx) >= 0) {
-                    read_frag.template operator()<B_MN, P::read_b_next(mi, idx)>(fb[NX][mi], b_rd[SB_NEXT],
-                                                                                 ic<mi>{});
+                    constexpr int bb = P::read_b_blk(mi, idx);
+                    read_frag.template operator()<B_MN, P::read_b_next(mi, idx)>(fb[NX][bb], b_rd[SB_NEXT],
+                                                                                 ic<bb>{});
                     sched_fence();
                 }
                 if constexpr (P::read_a_row0(mi, idx) >= 0) {

@@ -132,8 +132,10 @@ inline int64_t build_group_table(const int64_t *group_m, int group_num, int64_t 
 // Group and (M-tile, N-tile) of logical tile L. *g is a hint: the group of a smaller L seen
 // before (0 at the start); logical tiles only grow for one workgroup, so the scan only moves
 // forward. Empty groups own no tiles and are stepped over. out_rows and tile_m as in
-// build_group_table.
-GG_HD void locate_tile(int L, const GroupEntry *groups, int group_num, int n_tiles, int band,
+// build_group_table. GP is a pointer to const GroupEntry in any address space (the kernel
+// passes the constant address space, so the table is read with scalar loads).
+template <typename GP>
+GG_HD void locate_tile(int L, GP groups, int group_num, int n_tiles, int band,
                        int *g, int *tm, int *tn, int out_rows = 0, int tile_m = kTileM) {
     int gi = *g;
     while (gi + 1 < group_num && groups[gi + 1].tile0 <= L)

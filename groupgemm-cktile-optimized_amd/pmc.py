@@ -229,6 +229,9 @@ def main():
     ap.add_argument("--commit", default="unknown")
     ap.add_argument("--limit", type=int, default=90, help="seconds per rocprofv3 run")
     args = ap.parse_args()
+    # rocprofv3 runs with /tmp as its working directory: every path it is given is absolute
+    args.raw = os.path.abspath(args.raw)
+    args.profiles = os.path.abspath(args.profiles)
     names = sorted(bench.WORKLOADS) if args.workloads == "all" else args.workloads.split(",")
     sha = entry.load_package().kernel_source_sha()
     os.makedirs(args.profiles, exist_ok=True)
