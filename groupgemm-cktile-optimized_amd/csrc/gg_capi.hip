@@ -39,7 +39,7 @@ struct gg_plan {
     const int64_t      *d_offs      = nullptr;
     gg::TableHeader    *d_header    = nullptr; // follows the table in the d_groups allocation
     bool                in_kernel_table = false; // the GEMM builds the table (no table launch)
-    float              *d_ws        = nullptr; // split-K partial sums (args.ws)
+    float              *d_ws        = nullptr; // split-K / tail-split partial sums (args.ws)
     int64_t             in_rows     = 0;       // device-size plans: rows of the inputs
 };
 
@@ -120,6 +120,7 @@ void fill_args(gg_plan *plan, int n_xcd) {
     a.ws        = nullptr;
     a.tile_n    = gg::kTileN;
     a.tile_m    = gg::kTileM;
+    a.tail_splits = 1;
 }
 
 // Split-K for problems whose tiles cannot fill the GPU (fewer than half as many tiles as CUs):
@@ -274,6 +275,54 @@ int setup_split_k(gg_plan *plan, const hipDeviceProp_t &prop) {
     a.splits    = sp;
     a.ws        = plan->d_ws;
     plan->grid  = static_cast<int>(std::min<int64_t>(prop.multiProcessorCount, int64_t(sp) * plan->total_tiles));
+    return GG_OK;
+}
+
+// Tail split for cross-tile 16-bit forward plans (host-size tables): when the last round holds
+// rem tiles, at most half the grid, each of them is cut into two K ranges run by two workgroups,
+// so the busiest workgroup does R + 1/2 tiles instead of R + 1 (R full rounds). The ranges store
+// fp32 partial sums (2 * rem slabs of 256 KB) and tail_reduce_kernel, launched right after the
+// GEMM on the same stream, adds and stores them. Taken when a launch-time model (microseconds,
+// fitted to MI355X end-to-end timings) predicts a gain: the busiest workgroup saves T / 2 K steps
+// (kStepUs each), and pays its 256 KB of partial sums through the store path (kTailStoreUs), the
+// second launch (kTailLaunchUs) and the reduction's traffic, 1.5 MB per last-round tile
+// (kTailTileUs). Measured: 3 x 4096 x 1536 x 2048 (32 tiles in the last round, 32 K steps) 935 ->
+// 980 TFLOPS; config 5a (128 tiles, 45 steps) 1022 -> 948 and 1 x 4096 x 5376 x 2048 (80 tiles)
+// 1097 -> 1030, both left unsplit by the model. At least kMinTailSteps K steps per range.
+// GG_TAIL_SPLIT=0 in the environment turns it off; GG_TAIL_SPLIT=2 takes it wherever the plan
+// allows a split.
+constexpr int    kMinTailSteps = 8;
+constexpr double kTailStoreUs  = 6.0;
+constexpr double kTailLaunchUs = 5.0;
+constexpr double kTailTileUs   = 0.15;
+
+int setup_tail_split(gg_plan *plan) {
+    gg::KernelArgs &a = plan->args;
+    a.tail_splits     = 1;
+    if (plan->mode != gg::make_mode(gg::kFwd, gg::kIn16) || a.splits > 1 || a.d_total != nullptr ||
+        a.d_lens != nullptr || !gg::uses_cross_tile(a, plan->grid, plan->mode))
+        return GG_OK;
+    const int grid = plan->grid, tiles = plan->total_tiles;
+    const int full = tiles / grid * grid, rem = tiles - full;
+    if (full == 0 || rem == 0 || 2 * rem > grid)
+        return GG_OK;
+    int forced = -1;
+    if (const char *env = std::getenv("GG_TAIL_SPLIT"); env != nullptr && *env != '\0')
+        forced = std::atoi(env);
+    if (forced == 0 || forced == 1)
+        return GG_OK;
+    constexpr int sp = 2;
+    if (a.k_tiles / sp < (forced > 1 ? gg::kCrossMinStepsHost : kMinTailSteps))
+        return GG_OK;
+    const double saved_us = (a.k_tiles - gg::cdiv(a.k_tiles, sp)) * kStepUs;
+    const double cost_us  = kTailStoreUs + kTailLaunchUs + rem * kTailTileUs;
+    if (forced < 0 && saved_us < 1.1 * cost_us)
+        return GG_OK;
+    const hipError_t e = hipMalloc(&plan->d_ws, size_t(rem) * size_t(sp) * 262144);
+    if (e != hipSuccess)
+        return hip_fail(e, "tail-split workspace");
+    a.tail_splits = sp;
+    a.ws          = plan->d_ws;
     return GG_OK;
 }
 
@@ -553,6 +602,11 @@ int run_plan(const gg_plan *plan, void *stream, bool zero_kernel) {
         if (e != hipSuccess)
             return hip_fail(e, "split-K reduction launch");
     }
+    if (plan->args.tail_splits > 1) {
+        e = gg::launch_tail_reduce(plan->args, plan->dtype == GG_DTYPE_FP16, plan->grid, s);
+        if (e != hipSuccess)
+            return hip_fail(e, "tail-split reduction launch");
+    }
     return GG_OK;
 }
 
@@ -640,13 +694,18 @@ int gg_prepare(int dtype, int group_num, int64_t n, int64_t k, const int64_t *gr
             free_plan(plan);
             return GG_ERR_HIP;
         }
+        if (setup_tail_split(plan) != GG_OK) {
+            free_plan(plan);
+            return GG_ERR_HIP;
+        }
         plan->detail      = "mi355x persistent " + std::to_string(a.tile_m) + "x" + std::to_string(a.tile_n) + "x64 " +
                        std::string(dtype == GG_DTYPE_BF16 ? "bf16" : "fp16") +
                        " grid=" + std::to_string(plan->grid) +
                        " tiles=" + std::to_string(plan->total_tiles) +
                        " xcd=" + std::to_string(a.n_xcd) +
                        (gg::uses_cross_tile(a, plan->grid) ? " cross-tile" : " per-tile") +
-                       (a.splits > 1 ? " split-k=" + std::to_string(a.splits) : "");
+                       (a.splits > 1 ? " split-k=" + std::to_string(a.splits) : "") +
+                       (a.tail_splits > 1 ? " tail-split=" + std::to_string(a.tail_splits) : "");
     } else {
         plan->detail = "mi355x: no launch (" +
                        std::string(has_output ? "K = 0, zero fill" : "empty output") + ")";
@@ -799,13 +858,15 @@ static int prepare_backward(int layout, int dtype_a, int dtype_b, int group_num,
                 return st2;
             }
         }
+
         plan->detail = "mi355x " + what + " persistent " + std::to_string(ka.tile_m) + "x256x" +
                        std::to_string(f8 ? 128 : 64) + " " +
                        (f8 ? "bf16-out" : dtype_a == GG_DTYPE_BF16 ? "bf16" : "fp16") +
                        " grid=" + std::to_string(plan->grid) + " tiles=" + std::to_string(plan->total_tiles) +
                        " xcd=" + std::to_string(ka.n_xcd) +
                        (gg::uses_cross_tile(ka, plan->grid, plan->mode) ? " cross-tile" : " per-tile") +
-                       (ka.splits > 1 ? " split-k=" + std::to_string(ka.splits) : "");
+                       (ka.splits > 1 ? " split-k=" + std::to_string(ka.splits) : "") +
+                       (ka.tail_splits > 1 ? " tail-split=" + std::to_string(ka.tail_splits) : "");
     } else {
         plan->detail = "mi355x " + what + ": no launch (" +
                        (has_output ? "empty contraction, zero fill" : "empty output") + ")";
@@ -903,7 +964,8 @@ int gg_prepare_fp8(int dtype, int group_num, int64_t n, int64_t k, const int64_t
                        " persistent 256x256x128 bf16-out grid=" + std::to_string(plan->grid) +
                        " tiles=" + std::to_string(plan->total_tiles) + " xcd=" + std::to_string(a.n_xcd) +
                        (gg::uses_cross_tile(a, plan->grid, plan->mode) ? " cross-tile" : " per-tile") +
-                       (a.splits > 1 ? " split-k=" + std::to_string(a.splits) : "");
+                       (a.splits > 1 ? " split-k=" + std::to_string(a.splits) : "") +
+                       (a.tail_splits > 1 ? " tail-split=" + std::to_string(a.tail_splits) : "");
     } else {
         plan->detail = std::string("mi355x fp8: no launch (") +
                        (has_output ? "K = 0, zero fill" : "empty output") + ")";

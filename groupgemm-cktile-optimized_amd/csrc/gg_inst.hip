@@ -1,5 +1,6 @@
 // One instance unit of the persistent grouped GEMM: the (input type, mode) pair GG_PART selects,
-// both variants (cross-tile and per-tile), or (parts 14-17) the short-tile instances.
+// both variants (cross-tile and per-tile), or (parts 14-17) the short-tile instances. 16-bit
+// forward units also hold the cross-tile instances with the tail split (TAIL).
 // The Makefile compiles this file once per part, in parallel; gg_kernel.hip's dispatch calls
 // launch_mode of every part.
 #include "gg_kernel_impl.h"
@@ -19,6 +20,12 @@ void launch_mode(const KernelArgs &args, bool cross, dim3 g, dim3 b, hipStream_t
         }
     }
     if (cross) {
+        if constexpr (MODE == make_mode(kFwd, kIn16)) {
+            if (args.tail_splits > 1) {
+                hipLaunchKernelGGL((grouped_gemm_kernel<F16, true, MODE, kShapeWide, true>), g, b, 0, stream, args);
+                return;
+            }
+        }
         hipLaunchKernelGGL((grouped_gemm_kernel<F16, true, MODE>), g, b, 0, stream, args);
         return;
     }
@@ -33,9 +40,15 @@ void launch_mode(const KernelArgs &args, bool cross, dim3 g, dim3 b, hipStream_t
 
 template <bool F16, int MODE>
 void launch_short(const KernelArgs &args, bool cross, dim3 g, dim3 b, hipStream_t stream) {
-    if (cross)
+    if (cross) {
+        if constexpr (MODE == make_mode(kFwd, kIn16)) {
+            if (args.tail_splits > 1) {
+                hipLaunchKernelGGL((grouped_gemm_kernel<F16, true, MODE, kShapeShort, true>), g, b, 0, stream, args);
+                return;
+            }
+        }
         hipLaunchKernelGGL((grouped_gemm_kernel<F16, true, MODE, kShapeShort>), g, b, 0, stream, args);
-    else
+    } else
         hipLaunchKernelGGL((grouped_gemm_kernel<F16, false, MODE, kShapeShort>), g, b, 0, stream, args);
 }
 

@@ -72,11 +72,20 @@ struct KernelArgs {
     int               tile_m;      // output rows per tile: kTileM, or at most kShortTileM
                                    // (16-bit forward and dgrad plans whose groups keep their
                                    // M-tile counts; the group table counts these)
+    // Tail split (cross-tile variant, host-size 16-bit forward plans with a partial last round
+    // of at most half the grid): K ranges per last-round tile, 2 (1 = none). ws then holds
+    // 2 * rem partial-sum slabs of 256 KB (range k of last-round tile j at slab k * rem + j), which
+    // tail_reduce_kernel adds and stores after the GEMM.
+    int               tail_splits;
 };
 
 // Tile shapes of the forward kernel: 256 x 256; narrow 256 x 224 (per-tile, one-round plans);
 // short tile_m x 256 with tile_m <= kShortTileM (6 row blocks per wave).
 enum TileShape { kShapeWide = 0, kShapeNarrow = 1, kShapeShort = 2 };
+
+// Fewest K steps of a tile (or tail-split K range) in the cross-tile pipeline: its first step
+// plus the three whose DMAs prefetch the next tile.
+constexpr int kCrossMinStepsHost = 4;
 
 // Whether a launch takes the cross-tile pipeline variant (several tiles per workgroup, enough
 // K steps) rather than a prologue and an LDS-staged epilogue per tile.
@@ -105,6 +114,11 @@ hipError_t launch_grouped_gemm(const KernelArgs &args, bool fp16, int grid, hipS
 // order), times the fp8 scales for fp8 formats, converted to 16 bits and stored within the
 // tile's valid rows and columns. Forward and dgrad layouts (out row stride N).
 hipError_t launch_split_reduce(const KernelArgs &args, bool fp16, hipStream_t stream, int mode = 0);
+
+// Tail split, second pass: every last-round tile of a tail-split plan (launched on `grid`
+// workgroups) = the sum of its two K ranges' partial sums in args.ws, converted to 16 bits and
+// stored within the tile's valid rows and columns.
+hipError_t launch_tail_reduce(const KernelArgs &args, bool fp16, int grid, hipStream_t stream);
 
 // Build the group table on the device from device-resident group sizes: lens[group_num]
 // (int64 rows) and offs[group_num + 1] (int64 first rows) or null for back-to-back groups.

@@ -50,6 +50,36 @@ __global__ void __launch_bounds__(256) split_reduce_kernel(const KernelArgs args
 }
 
 // ---------------------------------------------------------------------------------------
+// Tail split, second pass: block b takes 256 16-byte positions (b % 64) of last-round tile
+// b / 64 (the tile of physical slot full + b / 64, as the GEMM's xcd_remap placed it), in the
+// slab layout of split_reduce_kernel; the two K ranges are added (fp32, commutative) and stored.
+// Short tiles store row blocks 0-5 only: positions of rows past tile_m are never valid rows.
+// ---------------------------------------------------------------------------------------
+template <bool F16>
+__global__ void __launch_bounds__(256) tail_reduce_kernel(const KernelArgs args, int grid) {
+    const int j    = blockIdx.x >> 6;
+    const int full = (args.total_tiles / grid) * grid;
+    const int rem  = args.total_tiles - full;
+    const int L    = xcd_remap(full + j, args.total_tiles, grid, args.n_xcd);
+    int       g    = 0, tm, tn;
+    locate_tile(L, args.groups, args.group_num, args.n_tiles, args.band, &g, &tm, &tn, 0, args.tile_m);
+    const GroupEntry ge  = args.groups[g];
+    const int        p   = (blockIdx.x & 63) * 256 + static_cast<int>(threadIdx.x);
+    const int        wv  = p >> 12, blk = (p >> 6) & 63, l = p & 63;
+    const int        row = (wv >> 1) * 16 + (blk >> 3) * 32 + (l & 15);
+    const int        col = (wv & 1) * 128 + (blk & 7) * 16 + (l >> 4) * 4;
+    const int        N   = args.n;
+    const float     *src = args.ws + static_cast<int64_t>(j) * 65536 + p * 4;
+    const f32x4      v0  = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(src));
+    const f32x4      v1  = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(src + static_cast<int64_t>(rem) * 65536));
+    if (row < min(args.tile_m, ge.m - tm * args.tile_m) && col < N - tn * kTileN) {
+        uint16_t *o = static_cast<uint16_t *>(args.out) +
+                      (ge.row0 + static_cast<int64_t>(tm) * args.tile_m + row) * N + static_cast<int64_t>(tn) * kTileN + col;
+        *reinterpret_cast<u32x2 *>(o) = pack4<F16>(v0 + v1);
+    }
+}
+
+// ---------------------------------------------------------------------------------------
 // Group table from device-resident group sizes (one wave, groups in chunks of 64).
 // The same facts as the host's build_group_table: first row, rows and first tile per group.
 // ---------------------------------------------------------------------------------------
@@ -211,6 +241,17 @@ hipError_t launch_grouped_gemm(const KernelArgs &args, bool fp16, int grid, hipS
         }
     }
 #undef GG_CASE
+    return hipGetLastError();
+}
+
+hipError_t launch_tail_reduce(const KernelArgs &args, bool fp16, int grid, hipStream_t stream) {
+    const int rem = args.total_tiles - (args.total_tiles / grid) * grid;
+    if (rem <= 0)
+        return hipSuccess;
+    if (fp16)
+        hipLaunchKernelGGL(tail_reduce_kernel<true>, dim3(rem * 64), dim3(256), 0, stream, args, grid);
+    else
+        hipLaunchKernelGGL(tail_reduce_kernel<false>, dim3(rem * 64), dim3(256), 0, stream, args, grid);
     return hipGetLastError();
 }
 

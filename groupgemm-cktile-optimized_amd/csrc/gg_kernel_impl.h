@@ -557,7 +557,7 @@ template <bool F16> __device__ __forceinline__ u32x2 pack4(const f32x4 &v) {
 #define GG_STORE_CPOL 2 // cache policy of the register-direct C stores: bit 0 sc0, bit 1 nt, bit 4 sc1
 #endif
 constexpr bool kCrossAllowed  = GG_CROSS_TILE;
-constexpr int  kCrossMinSteps = 4; // the three prefetching steps follow the first
+constexpr int  kCrossMinSteps = kCrossMinStepsHost; // the three prefetching steps follow the first
 constexpr int  kStoreCpol     = GG_STORE_CPOL;
 #ifndef GG_PARTIAL_NT
 #define GG_PARTIAL_NT 0
@@ -639,7 +639,10 @@ constexpr bool kTailSkip = GG_TAIL_SKIP;
 // first 6 interleaved row blocks (tile rows up to 191); the MFMAs, x fragment reads and stores
 // of blocks 6 and 7 are compiled out and the memory schedule is unchanged: the A DMAs of rows
 // past tile_m fall outside the bounded resource (zeros, no traffic).
-template <bool F16, bool CROSS, int MODE, int SHAPE = kShapeWide>
+// TAIL (cross-tile 16-bit forward only): the plan cuts its last-round tiles into K ranges (tail
+// split: K ranges of last-round tiles store partial sums from epilogue_lds); instances without it
+// carry none of its state.
+template <bool F16, bool CROSS, int MODE, int SHAPE = kShapeWide, bool TAIL = false>
 __global__ void __launch_bounds__(kThreads, 1) __attribute__((amdgpu_waves_per_eu(1, 1)))
 grouped_gemm_kernel(const KernelArgs args) {
     constexpr bool A_MN   = mode_a_mn(MODE), B_MN = mode_b_mn(MODE);
@@ -701,7 +704,17 @@ grouped_gemm_kernel(const KernelArgs args) {
     // Work units: a tile, or with split-K (per-tile variant only) one K range of a tile; unit
     // u = split * total_tiles + tile.
     const int splits      = CROSS ? 1 : args.splits;
-    const int total_units = total_tiles * splits;
+    // Tail split (cross-tile variant, host-size plans): the tiles of the last, partial round
+    // (rem < half the grid) are cut into tail_s K ranges, one per workgroup, so every workgroup
+    // ends the launch after its full rounds plus 1/tail_s of a tile instead of half the grid
+    // idling through one more tile. Unit u < full is tile u; u >= full is K range
+    // (u - full) / rem of last-round tile (u - full) % rem.
+    static_assert(!TAIL || (CROSS && MODE == make_mode(kFwd, kIn16)), "tail split: cross-tile 16-bit forward");
+    const int tail_s      = TAIL ? args.tail_splits : 1;
+    const int full        = tail_s > 1 ? (total_tiles / static_cast<int>(gridDim.x)) * static_cast<int>(gridDim.x)
+                                       : total_tiles;
+    const int rem         = total_tiles - full;
+    const int total_units = tail_s > 1 ? full + rem * tail_s : total_tiles * splits;
 
     // DMA lane offsets within a tile's K step (the tile origin is in the buffer resource).
     // K-major operand, row stride ld: DMA j covers tile rows j*32 + wave*8 .. +8; lane -> row
@@ -851,6 +864,8 @@ grouped_gemm_kernel(const KernelArgs args) {
         int       T;              // K steps (wgrad: of the tile's group, at least 1)
         int       k0;             // first K step (split-K: the split's range), 0 otherwise
         int       klast;          // the range ends with the problem's last (maybe partial) K step
+        int       tail;           // tail split: index of the last-round tile (-1: a whole tile)
+        int       tail_k;         // tail split: the unit's K range (0 .. tail_s - 1)
         float     scale;          // fp8: x scale * w[g] scale (1 otherwise)
         uint32_t  rows;           // this wave's row blocks (bit mi) that hold a valid output
     };
@@ -863,8 +878,19 @@ grouped_gemm_kernel(const KernelArgs args) {
     const const_space<GroupEntry> const_table = to_const_space(args.groups);
     auto      make_tile = [&](int t) -> Tile {
         // split-K: one unit per workgroup, no L2 sharing across rounds to arrange
-        const int split = splits > 1 ? t / total_tiles : 0;
-        const int L     = splits > 1 ? t - split * total_tiles : xcd_remap(t, total_tiles, gridDim.x, args.n_xcd);
+        int split = 0, nsplit = splits, L, tail = -1;
+        if (splits > 1) {
+            split = t / total_tiles;
+            L     = t - split * total_tiles;
+        } else if (TAIL && t >= full) {
+            // a K range of a last-round tile: that tile's place in the round decides the XCD order
+            tail   = (t - full) % rem;
+            split  = (t - full) / rem;
+            nsplit = tail_s;
+            L      = xcd_remap(full + tail, total_tiles, gridDim.x, args.n_xcd);
+        } else {
+            L = xcd_remap(t, total_tiles, gridDim.x, args.n_xcd);
+        }
         int        tm, tn;
         GroupEntry ge;
         if (in_kernel_table) {
@@ -891,11 +917,13 @@ grouped_gemm_kernel(const KernelArgs args) {
         const int64_t col0 = static_cast<int64_t>(tn) * TN;
         tl.o0a = tl.o0b = 0;
         // K range of the unit: steps [k0, k1) of k_tiles, balanced over the splits
-        const int k0 = split * args.k_tiles / splits, k1 = (split + 1) * args.k_tiles / splits;
-        tl.T     = k1 - k0;
-        tl.k0    = k0;
-        tl.klast = k1 == args.k_tiles;
-        tl.scale = 1.0f;
+        const int k0 = split * args.k_tiles / nsplit, k1 = (split + 1) * args.k_tiles / nsplit;
+        tl.T      = k1 - k0;
+        tl.k0     = k0;
+        tl.klast  = k1 == args.k_tiles;
+        tl.tail   = tail;
+        tl.tail_k = split;
+        tl.scale  = 1.0f;
         if constexpr (LAYOUT == kWgrad) {
             // A^T = grad_out rows of the group, columns tm*256..; B^T = x rows, columns tn*256..
             const int64_t o0a = static_cast<int64_t>(tm) * kTileM;
@@ -943,7 +971,7 @@ grouped_gemm_kernel(const KernelArgs args) {
     if (t >= total_units)
         return;
     Tile cur = make_tile(t), nxt = cur;
-    if constexpr (!CROSS || LAYOUT == kWgrad)
+    if (!CROSS || LAYOUT == kWgrad || TAIL)
         T = __builtin_amdgcn_readfirstlane(cur.T);
     bool cross_next = false; // the DMAs past this tile's last K step fetch `nxt`
 
@@ -975,8 +1003,13 @@ grouped_gemm_kernel(const KernelArgs args) {
         if constexpr (decltype(checked)::value) {
             const bool in_cur = kidx < T;
             const int  koff   = in_cur ? kidx : kidx - T;
-            // step of the operand: the unit's first step plus koff (the next tile starts at 0)
-            const int kabs = in_cur ? koff + cur.k0 : koff;
+            // step of the operand: the unit's first step plus koff (the next unit starts at 0 but for
+            // a tail split's later K ranges)
+            int kabs;
+            if constexpr (TAIL)
+                kabs = koff + (in_cur ? cur.k0 : nxt.k0);
+            else
+                kabs = in_cur ? koff + cur.k0 : koff;
             d.rs           = in_cur ? rc : (cross_next ? rn : rsrc_0);
             if constexpr (MN) {
                 d.so   = 0;
@@ -986,6 +1019,8 @@ grouped_gemm_kernel(const KernelArgs args) {
             } else {
                 d.so   = kabs * kRowBytes;
                 d.vadd = 0;
+                // the unit's partial last K step (a next unit has at least kCrossMinSteps steps, so
+                // the three prefetched never include its last, and koff < 3 < T - 1 for them)
                 d.mask = (koff == T - 1 && cur.klast) ? ktail_bad : 0;
             }
         } else {
@@ -1064,7 +1099,14 @@ grouped_gemm_kernel(const KernelArgs args) {
     //   Z_B: lanes l%16 >= 8 keep X_2h+1 (row l%16), lanes l%16 < 8 take X_2h of lane l+8.
     // Z_A holds rows 0-7 and Z_B rows 8-15 of the block, columns 64h..64h+63.
     float prev_scale = 1.0f; // fp8: scale of the tile whose accumulators the fused stores take
-    auto  pack_chunk = [&](auto r, auto j) -> u32x4 {
+    auto  pack_vals = [&](f32x4 v0, f32x4 v1) -> u32x4 { // blocks 2j and 2j+1 -> chunk X_j
+        const u32x2 p0 = pack4<F16>(v0);
+        const u32x2 p1 = pack4<F16>(v1);
+        const auto  s0 = __builtin_amdgcn_permlane16_swap(p0[0], p1[0], false, false);
+        const auto  s1 = __builtin_amdgcn_permlane16_swap(p0[1], p1[1], false, false);
+        return u32x4{s0[0], s1[0], s0[1], s1[1]};
+    };
+    auto pack_chunk = [&](auto r, auto j) -> u32x4 {
         // reads of these accumulators may not move above this point
         asm volatile("" : "+a"(acc[r][2 * j]), "+a"(acc[r][2 * j + 1]));
         f32x4 v0 = acc[r][2 * j], v1 = acc[r][2 * j + 1];
@@ -1072,20 +1114,17 @@ grouped_gemm_kernel(const KernelArgs args) {
             v0 *= prev_scale;
             v1 *= prev_scale;
         }
-        const u32x2 p0 = pack4<F16>(v0);
-        const u32x2 p1 = pack4<F16>(v1);
-        const auto  s0 = __builtin_amdgcn_permlane16_swap(p0[0], p1[0], false, false);
-        const auto  s1 = __builtin_amdgcn_permlane16_swap(p0[1], p1[1], false, false);
-        return u32x4{s0[0], s1[0], s0[1], s1[1]};
+        return pack_vals(v0, v1);
     };
-    auto pack_pair = [&](auto r, auto h, u32x4 &za, u32x4 &zb) {
-        const u32x4 x0 = pack_chunk(r, ic<2 * h>{});
-        const u32x4 x1 = pack_chunk(r, ic<2 * h + 1>{});
+    auto dpp_pair = [&](const u32x4 &x0, const u32x4 &x1, u32x4 &za, u32x4 &zb) {
         sfor<0, 4>([&](auto i) {
             // row_shr:8 into banks 2-3, row_shl:8 into banks 0-1
             za[int(i)] = __builtin_amdgcn_update_dpp(x0[int(i)], x1[int(i)], 0x118, 0xf, 0xc, false);
             zb[int(i)] = __builtin_amdgcn_update_dpp(x1[int(i)], x0[int(i)], 0x108, 0xf, 0x3, false);
         });
+    };
+    auto pack_pair = [&](auto r, auto h, u32x4 &za, u32x4 &zb) {
+        dpp_pair(pack_chunk(r, ic<2 * h>{}), pack_chunk(r, ic<2 * h + 1>{}), za, zb);
     };
     // Store s = 2h + half of row block r. Chunks past n_valid get an out-of-range offset
     // (N % 8 == 0, so a 16-byte chunk is either all valid or all past N).
@@ -1099,24 +1138,23 @@ grouped_gemm_kernel(const KernelArgs args) {
     };
     // ---- epilogue through LDS: accumulators -> 16-bit -> LDS (528-byte row stride) -> every wave
     // streams 64 whole rows, two 512-byte rows per 16-byte-per-lane store. Needs all of LDS.
-    auto epilogue_lds = [&](const Tile &tl) {
-        wait_vm_lds_barrier<0>(); // trailing DMAs landed, every wave is done reading LDS
-        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" ::: "memory"); // MFMA -> VALU read distance
-        {
-            int row = wm * (ILV ? 16 : 128) + (lane & 15);
-            fresh_v(row);
-            const int col = wn * WCOLS + (lane >> 4) * 4;
-            const int off = row * kCStride + col * 2;
-            sfor<0, RB>([&](auto mi) { // short tiles: blocks 6 and 7 are past the tile
-                sfor<0, NBLK>([&](auto ni) { // narrow tiles: the 8th block is another wave's columns
-                    asm volatile("" : "+a"(acc[mi][ni]));
-                    f32x4 v = acc[mi][ni];
-                    if constexpr (F8)
-                        v *= tl.scale;
-                    *reinterpret_cast<u32x2 *>(smem + off + mi * A_BLK * kCStride + ni * 16 * 2) = pack4<F16>(v);
-                });
-            });
-        }
+    // Accumulators are only ever written by the MFMAs (inline asm, "+a"): code that assigns them
+    // from VGPR values lets the register allocator keep an accumulator in VGPRs across the K loop
+    // and copy it around the MFMAs, reading an MFMA's result one wait state after issue.
+    // Staging offset of a lane's 4 outputs of block (mi, ni) in the 528-byte-stride C tile.
+    auto stage_off = [&]() {
+        int row = wm * (ILV ? 16 : 128) + (lane & 15);
+        fresh_v(row);
+        const int col = wn * WCOLS + (lane >> 4) * 4;
+        return row * kCStride + col * 2;
+    };
+    auto stage_block = [&](const Tile &tl, int off, auto mi, auto ni, f32x4 v) {
+        if constexpr (F8)
+            v *= tl.scale;
+        *reinterpret_cast<u32x2 *>(smem + off + mi * A_BLK * kCStride + ni * 16 * 2) = pack4<F16>(v);
+    };
+    // Second half of the LDS epilogue: the staged tile to global memory.
+    auto store_staged = [&](const Tile &tl) {
         wait_vm_lds_barrier<63>();
         int row = wave * 64 + (lane >> 5);
         fresh_v(row);
@@ -1134,6 +1172,35 @@ grouped_gemm_kernel(const KernelArgs args) {
             });
         });
         wait_vm_lds_barrier<63>(); // every wave is done reading the staged C
+    };
+    // TAIL: a K range of a last-round tile leaves through here too, as fp32 partial sums (slab
+    // k * rem + tail of the workspace, store_partial's register order) for tail_reduce_kernel, the
+    // next launch on the stream. One exit path reads the accumulators, branch-free: a whole tile's
+    // partial-sum stores go to a zero-length resource and a K range's C stores to a zero-row tile
+    // (both dropped). With a second exit path reading them, the register allocator homed an
+    // accumulator in VGPRs for the whole kernel and read it back one wait state after its MFMAs
+    // (csrc/check_mfma_acc_hazard.py rejects such builds).
+    auto epilogue_lds = [&](Tile tl) {
+        wait_vm_lds_barrier<0>(); // trailing DMAs landed, every wave is done reading LDS
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" ::: "memory"); // MFMA -> VALU read distance
+        const int off = stage_off();
+        const bool part = TAIL && tl.tail >= 0;
+        const __amdgpu_buffer_rsrc_t prs =
+            __builtin_amdgcn_make_buffer_rsrc(args.ws, static_cast<short>(0), part ? 0x7fffffff : 0, 0x00020000);
+        const int poff = part ? ((tl.tail_k * rem + tl.tail) * 65536 + wave * 16384 + lane * 4) * 4 : 0;
+        if constexpr (TAIL)
+            tl.m_valid = part ? 0 : tl.m_valid; // no C rows for a K range
+        sfor<0, RB>([&](auto mi) { // short tiles: blocks 6 and 7 are past the tile
+            sfor<0, NBLK>([&](auto ni) { // narrow tiles: the 8th block is another wave's columns
+                asm volatile("" : "+a"(acc[mi][ni]));
+                const f32x4 v = acc[mi][ni];
+                if constexpr (TAIL)
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), prs,
+                                                           poff + (mi * 8 + ni) * 1024, 0, 0);
+                stage_block(tl, off, mi, ni, v);
+            });
+        });
+        store_staged(tl);
     };
     // ---- split-K unit: its fp32 accumulators to the workspace slab of unit u (256 KB), in
     // register order: wave w, block (mi, ni), lane l at float 65536 u + 16384 w + 256 (8 mi + ni)
@@ -1393,7 +1460,7 @@ grouped_gemm_kernel(const KernelArgs args) {
                 set_stages();
                 if (T & 1) // the first step reads w set 0
                     sfor<0, 8>([&](auto ni) { sfor<0, 2>([&](auto h) { fb[0][ni][h] = fb[1][ni][h]; }); });
-                if constexpr (LAYOUT == kWgrad) // the next group's K-step count
+                if (LAYOUT == kWgrad || TAIL) // the next group's or K range's step count
                     T = __builtin_amdgcn_readfirstlane(cur.T);
                 continue;
             }
@@ -1413,8 +1480,9 @@ grouped_gemm_kernel(const KernelArgs args) {
             T   = __builtin_amdgcn_readfirstlane(cur.T);
         }
     }
-    if constexpr (CROSS)
-        epilogue_lds(cur);
+    if constexpr (CROSS) {
+        epilogue_lds(cur); // TAIL: a K range's partial sums instead of its C tile
+    }
 }
 
 } // namespace

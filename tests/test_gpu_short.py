@@ -41,6 +41,9 @@ def _run(pkg, x, w, gm, env, monkeypatch):
         monkeypatch.delenv("GG_SHORT", raising=False)
     else:
         monkeypatch.setenv("GG_SHORT", env)
+    # bit-identity needs the same K order per output in both plans: no tail split (it sums the
+    # K ranges of other last-round tiles in the two tilings)
+    monkeypatch.setenv("GG_TAIL_SPLIT", "0")
     b, n, k = w.shape
     out = torch.full((x.shape[0], n), float("nan"), dtype=x.dtype, device=DEV)
     s = torch.cuda.current_stream(DEV).cuda_stream
