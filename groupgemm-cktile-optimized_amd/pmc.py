@@ -12,7 +12,8 @@ Per workload, four runs of `bench.py --workload W --op OP --steps 3 --warmup 1 -
   write  rocprofv3 --pmc WRITE_SIZE
   sq     rocprofv3 --pmc SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE SQ_VALU_MFMA_BUSY_CYCLES
                          SQ_BUSY_CU_CYCLES GRBM_GUI_ACTIVE GRBM_COUNT
-  trace  rocprofv3 --kernel-trace (the kernel's time without counters, for the clock)
+  trace  rocprofv3 --kernel-trace over the driver's protocol (--warmup 5 --steps 20): every launch's
+         duration without counters, the timed 20 averaged for the clock
 and once per call two passes over a 1 GiB device copy (bench.py --calibrate-copy), which give the
 bytes one KiB of FETCH_SIZE / WRITE_SIZE stands for (the reference's counters, scripts/pmc.sh:4,
 16-17, are the SQ ones).
@@ -20,7 +21,8 @@ bytes one KiB of FETCH_SIZE / WRITE_SIZE stands for (the reference's counters, s
 Per workload it writes profiles/hbm_traffic_<workload>[_<op>].json: the per-dispatch counters of
 the grouped GEMM kernel (mean over the dispatches after the first), fetch and write bytes per
 launch scaled by the copy calibration, their ratio to the algorithmic bytes, LDS bank conflicts,
-MFMA busy and the clock, with the kernel instance, the plan and the hash of the kernel sources
+MFMA busy, issued vs useful MFMA cycles, cycles per launch (GRBM_GUI_ACTIVE per XCD), the share
+of the MFMA peak per clock and the clock, with the kernel instance, the plan and the hash of the kernel sources
 (kernel_source_sha) they were measured on; bench.py reports `traffic` only for a build with the
 same hash and plan. Prints one line per pass; stops at the first pass that fails (exit 1).
 FETCH_SIZE counts the L2's read requests to the data fabric, Infinity-Cache hits included, so
@@ -140,20 +142,29 @@ def profile_workload(w: str, op: str, raw: str, limit: int, cal, commit: str, sh
         m = re.search(r"\[bench\] \S+ \S+: (.*)", err)
         plan = m.group(1).strip() if m else plan
         log(f"{tag0} {p}: " + ", ".join(f"{c}={counters[c]:.6g}" for c in names if counters[c] is not None))
-    files, _ = run_pass(f"{tag0}_trace", ["--kernel-trace"], bench_args, raw, limit)
+    trace_args = ["--workload", w, "--op", op, "--steps", "20", "--warmup", "5", "--no-cpu-baseline",
+                  "--power-seconds", "0", "--baselines", ""]
+    files, _ = run_pass(f"{tag0}_trace", ["--kernel-trace"], trace_args, raw, limit)
     ds = dispatches(files, lambda n: "grouped_gemm_kernel" in n)
     ns = [d["ns"] for _, d in sorted(ds.items()) if d["ns"]]
-    trace_ns = sum(ns[1:]) / len(ns[1:]) if len(ns) > 1 else (ns[0] if ns else None)
-    log(f"{tag0} trace: {len(ns)} dispatches, {trace_ns} ns after the first")
+    timed = ns[-20:] if len(ns) >= 25 else ns[1:] or ns
+    trace_ns = sum(timed) / len(timed) if timed else None
+    log(f"{tag0} trace: {len(ns)} dispatches, {trace_ns} ns over the last {len(timed)}")
 
     dtype, b, m, n, k = workloads[w]
-    es = 2
-    algo = es * (b * m * k + b * n * k + b * m * n)
+    fp8 = "fp8" in op
+    es = 1 if fp8 else 2
+    algo = es * (b * m * k + b * n * k) + 2 * b * m * n
+    flops = 2.0 * b * m * n * k
+    flop_per_simd_clk = 2048.0 if fp8 else 1024.0  # dense MFMA peak per SIMD per clock
+    cycles = counters["GRBM_GUI_ACTIVE"] / XCDS if counters.get("GRBM_GUI_ACTIVE") else None
+    mfma = counters.get("SQ_VALU_MFMA_BUSY_CYCLES")
     fetch = counters["FETCH_SIZE"] * cal["bytes_per_fetch_kib"] if counters.get("FETCH_SIZE") and cal.get(
         "bytes_per_fetch_kib") else None
     write = counters["WRITE_SIZE"] * cal["bytes_per_write_kib"] if counters.get("WRITE_SIZE") and cal.get(
         "bytes_per_write_kib") else None
     busy = counters.get("SQ_BUSY_CU_CYCLES")
+    cus = 256
     res = {
         "workload": w, "op": op, "kernel": instance(name), "plan": plan, "kernel_source_sha": sha, "commit": commit,
         "counters_per_dispatch": counters,
@@ -167,12 +178,22 @@ def profile_workload(w: str, op: str, raw: str, limit: int, cal, commit: str, sh
         "lds_bank_conflict_pct": round(100.0 * counters["SQ_LDS_BANK_CONFLICT"] / counters["SQ_LDS_IDX_ACTIVE"], 3)
         if counters.get("SQ_LDS_IDX_ACTIVE") else None,
         "mfma_busy_pct": round(100.0 * counters["SQ_VALU_MFMA_BUSY_CYCLES"] / (4.0 * busy), 2) if busy else None,
+        "mfma_cycles_issued": round(mfma) if mfma else None,
+        "mfma_cycles_useful": round(flops / flop_per_simd_clk),
+        "mfma_useful_over_issued": round(flops / flop_per_simd_clk / mfma, 4) if mfma else None,
+        "cycles_per_launch": round(cycles) if cycles else None,
+        "mfma_peak_per_clock_pct": round(100.0 * flops / (cycles * cus * 4 * flop_per_simd_clk), 2)
+        if cycles else None,
+        "launch_ns_unprofiled": ns,
         "kernel_ns_unprofiled": round(trace_ns) if trace_ns else None,
-        "clock_ghz": round(counters["GRBM_GUI_ACTIVE"] / XCDS / trace_ns, 3)
-        if trace_ns and counters.get("GRBM_GUI_ACTIVE") else None,
+        "tflops_unprofiled": round(flops / trace_ns / 1e3, 1) if trace_ns else None,
+        "clock_ghz": round(cycles / trace_ns, 3) if trace_ns and cycles else None,
         "note": "FETCH_SIZE counts the L2's read requests to the data fabric (Infinity-Cache hits included), "
-                "WRITE_SIZE its writes; both scaled by a 1 GiB device copy. The clock is GRBM_GUI_ACTIVE per XCD "
-                "over the kernel's unprofiled time (counter passes run the kernel slower).",
+                "WRITE_SIZE its writes; both scaled by a 1 GiB device copy. cycles_per_launch is GRBM_GUI_ACTIVE "
+                "per XCD; launch_ns_unprofiled are the 25 launches of the driver's protocol (5 warmup + 20 timed) "
+                "without counters, kernel_ns_unprofiled their timed 20's mean, and the clock is the cycles over "
+                "that mean. mfma_cycles_useful = flops / (dense MFMA flops per SIMD per clock): the rest of the "
+                "issued MFMA cycles compute padding.",
     }
     return res
 
@@ -197,8 +218,9 @@ def write_markdown(path: str, results, cal, cmdline: str):
         "bytes per KiB counted.",
         "",
         "| Workload | Kernel instance | fetch GB | write GB | (fetch+write) / algorithmic | fetch / (x+w) | "
-        "LDS bank conflicts | MFMA busy | kernel ms (unprofiled) | clock GHz |",
-        "|---|---|---|---|---|---|---|---|---|---|",
+        "LDS bank conflicts | MFMA busy | useful / issued MFMA | Mcycles | % MFMA peak per clock | "
+        "kernel ms (timed 20) | TFLOPS | clock GHz |",
+        "|---|---|---|---|---|---|---|---|---|---|---|---|---|---|",
     ]
     for r in results:
         f = r["fetch_bytes_per_launch"]
@@ -206,10 +228,12 @@ def write_markdown(path: str, results, cal, cmdline: str):
         lines.append(
             f"| {r['workload']}{'' if r['op'] == 'fwd' else ' ' + r['op']} | `{r['kernel']}` | "
             f"{f / 1e9:.3f} | {wr / 1e9:.3f} | {r['traffic_over_algorithmic']} | {r['fetch_over_input_bytes']} | "
-            f"{r['lds_bank_conflict_pct']} % | {r['mfma_busy_pct']} % | "
-            f"{(r['kernel_ns_unprofiled'] or 0) / 1e6:.4f} | {r['clock_ghz']} |" if f and wr else
+            f"{r['lds_bank_conflict_pct']} % | {r['mfma_busy_pct']} % | {r['mfma_useful_over_issued']} | "
+            f"{(r['cycles_per_launch'] or 0) / 1e6:.3f} | {r['mfma_peak_per_clock_pct']} % | "
+            f"{(r['kernel_ns_unprofiled'] or 0) / 1e6:.4f} | {r['tflops_unprofiled']} | {r['clock_ghz']} |"
+            if f and wr else
             f"| {r['workload']} | `{r['kernel']}` | - | - | - | - | {r['lds_bank_conflict_pct']} % | "
-            f"{r['mfma_busy_pct']} % | - | - |")
+            f"{r['mfma_busy_pct']} % | - | - | - | - | - | - |")
     lines += ["", f"Kernel sources: `{results[0]['kernel_source_sha'] if results else ''}` "
                   f"(commit {results[0]['commit'] if results else ''}).", ""]
     with open(path, "w") as fh:
