@@ -40,6 +40,7 @@ struct gg_plan {
     gg::TableHeader    *d_header    = nullptr; // follows the table in the d_groups allocation
     bool                in_kernel_table = false; // the GEMM builds the table (no table launch)
     float              *d_ws        = nullptr; // split-K / tail-split partial sums (args.ws)
+    gg::TileDesc       *d_desc      = nullptr; // tile descriptors (args.desc)
     int64_t             in_rows     = 0;       // device-size plans: rows of the inputs
 };
 
@@ -121,6 +122,8 @@ void fill_args(gg_plan *plan, int n_xcd) {
     a.tile_n    = gg::kTileN;
     a.tile_m    = gg::kTileM;
     a.tail_splits = 1;
+    a.desc        = nullptr;
+    a.desc_per_wg = 0;
 }
 
 // Split-K for problems whose tiles cannot fill the GPU (fewer than half as many tiles as CUs):
@@ -331,7 +334,56 @@ void free_plan(gg_plan *plan) {
         (void)hipFree(plan->d_groups);
     if (plan->d_ws != nullptr)
         (void)hipFree(plan->d_ws);
+    if (plan->d_desc != nullptr)
+        (void)hipFree(plan->d_desc);
     delete plan;
+}
+
+// Tile descriptors of forward and dgrad plans of whole tiles (host-size tables): every
+// workgroup's tiles in the kernel's own walk (xcd_remap, then locate_tile over the plan's group
+// table with its tile rows and N-tiles), so that the kernel reads a tile's first row, group and
+// N-tile from a lane of a register instead of recomputing them between its K loops. Not built
+// (the kernel walks the table itself) with split-K, a tail split, more than kMaxDescPerWg tiles
+// per workgroup or rows past 2^31. GG_TILE_DESC=0 in the environment turns them off.
+int setup_tile_desc(gg_plan *plan, const int64_t *group_m, hipStream_t s) {
+    gg::KernelArgs &a   = plan->args;
+    const char     *env = std::getenv("GG_TILE_DESC");
+    if ((env != nullptr && env[0] == '0') || a.splits > 1 || a.tail_splits > 1 || plan->grid <= 0 ||
+        plan->mode % 4 == gg::kWgrad || plan->total_m >= INT32_MAX)
+        return GG_OK;
+    const int per_wg = static_cast<int>(gg::cdiv(plan->total_tiles, plan->grid));
+    if (per_wg > gg::kMaxDescPerWg)
+        return GG_OK;
+    std::vector<gg::GroupEntry> table(static_cast<size_t>(plan->group_num));
+    const int64_t tiles = gg::build_group_table(group_m, plan->group_num, a.n_tiles, table.data(), 0, a.tile_m);
+    if (tiles != plan->total_tiles)
+        return fail(GG_ERR_INVALID, "tile descriptors: the group table's tile count differs from the plan's");
+    std::vector<gg::TileDesc> desc(static_cast<size_t>(plan->grid) * per_wg, gg::TileDesc{0, 0, 0, 0});
+    for (int wg = 0; wg < plan->grid; ++wg) {
+        int g = 0; // locate_tile's hint: a workgroup's logical tiles only grow
+        for (int i = 0; i < per_wg; ++i) {
+            const int t = wg + i * plan->grid;
+            if (t >= plan->total_tiles)
+                break;
+            const int L = gg::xcd_remap(t, plan->total_tiles, plan->grid, a.n_xcd);
+            int       tm, tn;
+            gg::locate_tile(L, table.data(), plan->group_num, a.n_tiles, a.band, &g, &tm, &tn, 0, a.tile_m);
+            const int64_t r0 = table[g].row0 + static_cast<int64_t>(tm) * a.tile_m;
+            const int     mv = static_cast<int>(std::min<int64_t>(a.tile_m, table[g].m - static_cast<int64_t>(tm) * a.tile_m));
+            desc[static_cast<size_t>(wg) * per_wg + i] = gg::TileDesc{static_cast<int32_t>(r0), g, (tn << 9) | mv, 0};
+        }
+    }
+    const size_t bytes = desc.size() * sizeof(gg::TileDesc);
+    hipError_t   e     = hipMalloc(&plan->d_desc, bytes);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(plan->d_desc, desc.data(), bytes, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess)
+        e = hipStreamSynchronize(s);
+    if (e != hipSuccess)
+        return hip_fail(e, "tile descriptor upload");
+    a.desc        = reinterpret_cast<const int *>(plan->d_desc);
+    a.desc_per_wg = per_wg;
+    return GG_OK;
 }
 
 } // namespace
@@ -698,6 +750,10 @@ int gg_prepare(int dtype, int group_num, int64_t n, int64_t k, const int64_t *gr
             free_plan(plan);
             return GG_ERR_HIP;
         }
+        if (const int st3 = setup_tile_desc(plan, group_m, s); st3 != GG_OK) {
+            free_plan(plan);
+            return st3;
+        }
         plan->detail      = "mi355x persistent " + std::to_string(a.tile_m) + "x" + std::to_string(a.tile_n) + "x64 " +
                        std::string(dtype == GG_DTYPE_BF16 ? "bf16" : "fp16") +
                        " grid=" + std::to_string(plan->grid) +
@@ -858,6 +914,12 @@ static int prepare_backward(int layout, int dtype_a, int dtype_b, int group_num,
                 return st2;
             }
         }
+        if (dgrad) {
+            if (const int st3 = setup_tile_desc(plan, group_m, s); st3 != GG_OK) {
+                free_plan(plan);
+                return st3;
+            }
+        }
 
         plan->detail = "mi355x " + what + " persistent " + std::to_string(ka.tile_m) + "x256x" +
                        std::to_string(f8 ? 128 : 64) + " " +
@@ -959,6 +1021,10 @@ int gg_prepare_fp8(int dtype, int group_num, int64_t n, int64_t k, const int64_t
         if (setup_split_k(plan, prop) != GG_OK) {
             free_plan(plan);
             return GG_ERR_HIP;
+        }
+        if (const int st3 = setup_tile_desc(plan, group_m, s); st3 != GG_OK) {
+            free_plan(plan);
+            return st3;
         }
         plan->detail = std::string("mi355x fp8 ") + (dtype == GG_DTYPE_FP8_E4M3 ? "e4m3" : "e5m2") +
                        " persistent 256x256x128 bf16-out grid=" + std::to_string(plan->grid) +

@@ -77,7 +77,22 @@ struct KernelArgs {
     // 2 * rem partial-sum slabs of 256 KB (range k of last-round tile j at slab k * rem + j), which
     // tail_reduce_kernel adds and stores after the GEMM.
     int               tail_splits;
+    // Tile descriptors (null: the kernel locates its tiles itself): desc_per_wg (<= 64) entries
+    // of 4 ints per workgroup, entry i of workgroup w for its tile t = w + i * grid: first row
+    // of the tile in A and out, group, (N-tile << 9) | valid rows, 0. Host-size forward and
+    // dgrad plans without split-K or tail split (TileDesc, built by the plan).
+    const int        *desc;
+    int               desc_per_wg;
 };
+
+// One tile descriptor (see KernelArgs::desc).
+struct TileDesc {
+    int32_t row0;  // first row of the tile in A (x or grad_out) and out
+    int32_t g;     // group
+    int32_t tn_mv; // (N-tile << 9) | valid rows (at most 256)
+    int32_t pad;
+};
+constexpr int kMaxDescPerWg = 64; // one per lane of a wave
 
 // Tile shapes of the forward kernel: 256 x 256; narrow 256 x 224 (per-tile, one-round plans);
 // short tile_m x 256 with tile_m <= kShortTileM (6 row blocks per wave).

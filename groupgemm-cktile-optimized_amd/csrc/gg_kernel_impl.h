@@ -819,6 +819,13 @@ grouped_gemm_kernel(const KernelArgs args) {
         });
         fresh_v(ktail_bad);
         fresh_v(voffc);
+        {
+            // the step count, opaque: the checked steps' comparisons with it are made in the loop,
+            // not hoisted out of it as lane masks kept in (spilled) SGPRs
+            uint32_t t_ = static_cast<uint32_t>(T);
+            fresh_s(t_);
+            T = static_cast<int>(t_);
+        }
         sfor<0, 2>([&](auto L) {
             fresh_s(a_dst[L]);
             sfor<0, 2>([&](auto h) { fresh_v(a_rd[L][h]); });
@@ -876,10 +883,25 @@ grouped_gemm_kernel(const KernelArgs args) {
     // compiler issues vector loads and waits for them with vmcnt(0), which also drains every
     // operand DMA in flight, once per table entry the tile walk reads.
     const const_space<GroupEntry> const_table = to_const_space(args.groups);
-    auto      make_tile = [&](int t) -> Tile {
+    // Tile descriptors (host-size forward and dgrad plans of whole tiles, at most 64 per
+    // workgroup): lane i holds this workgroup's i-th tile, its first row in x / out, its group and
+    // (N-tile << 9 | valid rows). make_tile reads them with three v_readlane instead of walking
+    // the XCD remap, the group table and the band order (divisions and dependent scalar loads
+    // between the K loops, where no MFMA issues).
+    const bool use_desc = LAYOUT != kWgrad && !TAIL && splits == 1 && args.desc != nullptr;
+    int        d_row0 = 0, d_g = 0, d_tnm = 0;
+    if (use_desc && lane < args.desc_per_wg) {
+        const i32x4 dv = reinterpret_cast<const i32x4 *>(args.desc)[static_cast<int>(blockIdx.x) * args.desc_per_wg + lane];
+        d_row0         = dv[0];
+        d_g            = dv[1];
+        d_tnm          = dv[2];
+    }
+    auto      make_tile = [&](int t, int ti) -> Tile {
         // split-K: one unit per workgroup, no L2 sharing across rounds to arrange
-        int split = 0, nsplit = splits, L, tail = -1;
-        if (splits > 1) {
+        int split = 0, nsplit = splits, L = 0, tail = -1;
+        if (use_desc) {
+            // the descriptor holds the tile
+        } else if (splits > 1) {
             split = t / total_tiles;
             L     = t - split * total_tiles;
         } else if (TAIL && t >= full) {
@@ -891,9 +913,17 @@ grouped_gemm_kernel(const KernelArgs args) {
         } else {
             L = xcd_remap(t, total_tiles, gridDim.x, args.n_xcd);
         }
-        int        tm, tn;
-        GroupEntry ge;
-        if (in_kernel_table) {
+        int        tm = 0, tn;
+        GroupEntry ge{0, 0, 0};
+        int        desc_row0 = 0, desc_mv = 0; // use_desc: the tile's first row and valid rows
+        if (use_desc) {
+            ti        = __builtin_amdgcn_readfirstlane(ti);
+            desc_row0 = __builtin_amdgcn_readlane(d_row0, ti);
+            g         = __builtin_amdgcn_readlane(d_g, ti);
+            const int tnm = __builtin_amdgcn_readlane(d_tnm, ti);
+            tn        = tnm >> 9;
+            desc_mv   = tnm & 511;
+        } else if (in_kernel_table) {
             // the one lane whose group owns logical tile L
             const uint64_t hit = __ballot(lane < args.group_num && lgrp.tile0 <= L && L - lgrp.tile0 < lgrp.tiles);
             g                  = __builtin_amdgcn_readfirstlane(static_cast<int>(__builtin_ctzll(hit)));
@@ -941,8 +971,8 @@ grouped_gemm_kernel(const KernelArgs args) {
             tl.klast = 1;
         } else {
             const int TM       = SHORT ? args.tile_m : kTileM; // rows per tile
-            tl.m_valid         = min(TM, ge.m - tm * TM);
-            const int64_t row0 = ge.row0 + static_cast<int64_t>(tm) * TM;
+            tl.m_valid         = use_desc ? desc_mv : min(TM, ge.m - tm * TM);
+            const int64_t row0 = use_desc ? static_cast<int64_t>(desc_row0) : ge.row0 + static_cast<int64_t>(tm) * TM;
             tl.rsrc_a = dma_rsrc(xa + row0 * args.lda * ES, static_cast<uint32_t>(tl.m_valid) * args.lda * ES);
             if constexpr (LAYOUT == kFwd) {
                 tl.rsrc_b = dma_rsrc(wb + (static_cast<int64_t>(g) * N + col0) * args.ldb * ES,
@@ -965,12 +995,14 @@ grouped_gemm_kernel(const KernelArgs args) {
         return __builtin_amdgcn_make_buffer_rsrc(tl.c_ptr, static_cast<short>(0),
                                                  static_cast<int>(tl.m_valid * N * 2), 0x00020000);
     };
-    const i32x4 rsrc_0 = dma_rsrc(args.x, 0); // zero length: no traffic, the DMA writes zeros
+    // zero length: no traffic, the DMA writes zeros (all-constant, so no SGPRs held for it)
+    const i32x4 rsrc_0 = dma_rsrc(nullptr, 0);
 
     int t = blockIdx.x;
     if (t >= total_units)
         return;
-    Tile cur = make_tile(t), nxt = cur;
+    int  tile_i = 0; // this workgroup's tile count so far (unit t = blockIdx.x + tile_i * grid)
+    Tile cur = make_tile(t, 0), nxt = cur;
     if (!CROSS || LAYOUT == kWgrad || TAIL)
         T = __builtin_amdgcn_readfirstlane(cur.T);
     bool cross_next = false; // the DMAs past this tile's last K step fetch `nxt`
@@ -1131,8 +1163,12 @@ grouped_gemm_kernel(const KernelArgs args) {
     auto store_line = [&](const u32x4 &d, int r, int s_, const __amdgpu_buffer_rsrc_t &crs,
                           int n_valid) {
         const int h  = s_ >> 1, half = s_ & 1;
+        // The row block's byte offset from an opaque copy of the stride: computed here (two SALU)
+        // instead of 32 loop-invariant offsets that the compiler would keep in (spilled) SGPRs.
+        uint32_t bs = static_cast<uint32_t>(blk_stride);
+        fresh_s(bs);
         const int vo = ecol + 64 * h < n_valid
-                           ? voffc + r * blk_stride + half * (8 * N * 2) + h * 128
+                           ? voffc + r * static_cast<int>(bs) + half * (8 * N * 2) + h * 128
                            : static_cast<int>(0x80000000u);
         __builtin_amdgcn_raw_buffer_store_b128(d, crs, vo, 0, kStoreCpol);
     };
@@ -1227,7 +1263,7 @@ grouped_gemm_kernel(const KernelArgs args) {
     // blocks 1-7 here; block 0 before the step), to prev_crs / prev_n. Nothing to store before
     // the first tile: zero-length resource, the stores are dropped.
     const __amdgpu_buffer_rsrc_t null_crs =
-        __builtin_amdgcn_make_buffer_rsrc(cur.c_ptr, static_cast<short>(0), 0, 0x00020000);
+        __builtin_amdgcn_make_buffer_rsrc(nullptr, static_cast<short>(0), 0, 0x00020000);
     __amdgpu_buffer_rsrc_t prev_crs = null_crs;
     int                    prev_n   = 0;
     u32x4                  pair[2];
@@ -1422,7 +1458,7 @@ grouped_gemm_kernel(const KernelArgs args) {
         }
         cross_next = CROSS && more;
         if (cross_next)
-            nxt = make_tile(t_next);
+            nxt = make_tile(t_next, tile_i + 1);
         for (; !thin && kt < T; kt += 6) { // with CROSS the last three steps prefetch `nxt`
             refresh();
             step.template operator()<1, 1, false, true, false>(kt);
@@ -1454,6 +1490,7 @@ grouped_gemm_kernel(const KernelArgs args) {
                 prev_scale = cur.scale;
                 cur      = nxt;
                 t        = t_next;
+                ++tile_i;
                 rot_a    = (rot_a + T) & 1;
                 rot_b    = rot_b + T % 3;
                 rot_b    = rot_b >= 3 ? rot_b - 3 : rot_b;
@@ -1476,7 +1513,8 @@ grouped_gemm_kernel(const KernelArgs args) {
             if (!more)
                 return;
             t   = t_next;
-            cur = make_tile(t);
+            ++tile_i;
+            cur = make_tile(t, tile_i);
             T   = __builtin_amdgcn_readfirstlane(cur.T);
         }
     }

@@ -1,0 +1,162 @@
+"""Tile descriptors: the plan lists every workgroup's tiles (first row, group, N-tile, valid rows)
+and the kernel reads them from a register lane instead of walking the XCD remap, the group table
+and the band order itself.
+
+The descriptors describe the same tiles in the same order as the kernel's own walk, so a plan
+with them must give the bits of the same plan without them (GG_TILE_DESC=0), and every output
+must be within rtol = atol = 1e-2 of float32 (bench/bench_main.cpp:264-268). Outputs are
+NaN-prefilled, so an unwritten tile fails.
+
+Cases (forward through the backend, fp8 forward and dgrad through their plans):
+- 256 x 256 cross-tile bf16 with ragged and empty groups and a column tail;
+- config 5a's short tiles (176 rows) in fp16;
+- a one-round per-tile plan with narrow tiles (256 x 224);
+- exactly 64 tiles per workgroup (the last descriptor lane), and 68 (no descriptors: the kernel
+  walks the table itself), checked on sampled rows against float32;
+- fp8 e4m3 forward and bf16 dgrad with empty groups.
+"""
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+if not torch.cuda.is_available():
+    pytest.skip("needs an MI355X", allow_module_level=True)
+
+DEV = torch.device("cuda:0")
+ATOL = RTOL = 1e-2
+
+# dtype, group_m, N, K, tile shape expected in the plan
+FWD = [
+    (torch.bfloat16, [700, 0, 1300, 256, 0, 2049, 513, 900] * 4, 2000, 576, "256x256x64"),
+    (torch.float16, [520] * 32, 2880, 2880, "176x256x64"),
+    (torch.bfloat16, [2048], 7168, 2048, "256x224x64"),
+]
+
+
+def _fwd(pkg, x, w, gm, desc, monkeypatch):
+    if desc:
+        monkeypatch.delenv("GG_TILE_DESC", raising=False)
+    else:
+        monkeypatch.setenv("GG_TILE_DESC", "0")
+    b, n, k = w.shape
+    out = torch.full((x.shape[0], n), float("nan"), dtype=x.dtype, device=DEV)
+    s = torch.cuda.current_stream(DEV).cuda_stream
+    be = pkg.make_mi355x_backend()
+    dt = pkg.DType.BF16 if x.dtype == torch.bfloat16 else pkg.DType.FP16
+    why = be.prepare(pkg.GroupedGemmProblem(dt, b, n, k, gm, x.data_ptr(), w.data_ptr(), out.data_ptr()), s)
+    assert why == "", why
+    be.run(s)
+    torch.cuda.synchronize(DEV)
+    detail = be.detail()
+    be.release()
+    return out, detail
+
+
+def _check_rows(x, w, gm, out, rows_per_group=None):
+    row = 0
+    for gi, m in enumerate(gm):
+        sel = torch.arange(row, row + m, device=DEV)
+        if rows_per_group is not None and m > rows_per_group:
+            sel = sel[torch.linspace(0, m - 1, rows_per_group, device=DEV).long()]
+        if m:
+            ref = x[sel].float() @ w[gi].float().t().contiguous()
+            got = out[sel].float()
+            assert not torch.isnan(got).any(), f"group {gi}: unwritten outputs"
+            bad = int(((got - ref).abs() > ATOL + RTOL * ref.abs()).sum())
+            assert bad == 0, f"group {gi}: {bad} outputs off"
+        row += m
+
+
+@pytest.mark.parametrize("case", range(len(FWD)))
+def test_forward_descriptors_match_walk(pkg, monkeypatch, case):
+    dt, gm, n, k, shape = FWD[case]
+    print(f"[desc] forward case {case}: dtype={dt} groups={len(gm)} N={n} K={k}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(90 + case)
+    x = torch.randn((sum(gm), k), generator=g, device=DEV).to(dt)
+    w = torch.randn((len(gm), n, k), generator=g, device=DEV).to(dt)
+    with_desc, d1 = _fwd(pkg, x, w, gm, True, monkeypatch)
+    walk, d2 = _fwd(pkg, x, w, gm, False, monkeypatch)
+    assert shape in d1 and d1 == d2, (d1, d2)
+    assert torch.equal(with_desc.view(torch.int16), walk.view(torch.int16)), d1
+    _check_rows(x, w, gm, with_desc)
+
+
+@pytest.mark.parametrize("groups,expect_desc", [(16, True), (17, False)])
+def test_descriptor_capacity(pkg, monkeypatch, groups, expect_desc):
+    """16 groups of 4096 x 16384: 16384 tiles, 64 per workgroup of 256 (lane 63 is the last);
+    17 groups: 68 per workgroup, more than a wave has lanes, so the kernel walks the table."""
+    gm, n, k = [4096] * groups, 16384, 256
+    print(f"[desc] capacity: {groups} groups N={n} K={k}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(95 + groups)
+    x = torch.randn((sum(gm), k), generator=g, device=DEV).to(torch.bfloat16)
+    w = torch.randn((len(gm), n, k), generator=g, device=DEV).to(torch.bfloat16)
+    a, d1 = _fwd(pkg, x, w, gm, True, monkeypatch)
+    b, d2 = _fwd(pkg, x, w, gm, False, monkeypatch)
+    assert "grid=256" in d1 and "cross-tile" in d1, d1
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16)), d1
+    del b
+    _check_rows(x, w, gm, a, rows_per_group=24)
+    # tiles per workgroup: descriptors exactly when they fit in one lane per tile
+    s = torch.cuda.current_stream(DEV).cuda_stream
+    be = pkg.make_mi355x_backend()
+    monkeypatch.delenv("GG_TILE_DESC", raising=False)
+    assert be.prepare(pkg.GroupedGemmProblem(pkg.DType.BF16, len(gm), n, k, gm, x.data_ptr(), w.data_ptr(),
+                                             a.data_ptr()), s) == ""
+    assert (be.tiles() + be.grid() - 1) // be.grid() == (64 if expect_desc else 68)
+    be.release()
+
+
+def test_fp8_descriptors_match_walk(pkg, monkeypatch):
+    gm, n, k = [300, 0, 1000, 2100, 64, 0, 777] * 3, 1536, 1024
+    g = torch.Generator(device=DEV).manual_seed(97)
+    x = (torch.randn((sum(gm), k), generator=g, device=DEV) * 0.5).to(torch.float8_e4m3fn)
+    w = (torch.randn((len(gm), n, k), generator=g, device=DEV) * 0.5).to(torch.float8_e4m3fn)
+    xs = torch.tensor([0.5], device=DEV)
+    ws = torch.linspace(0.5, 2.0, len(gm), device=DEV)
+    outs = []
+    for desc in (True, False):
+        if desc:
+            monkeypatch.delenv("GG_TILE_DESC", raising=False)
+        else:
+            monkeypatch.setenv("GG_TILE_DESC", "0")
+        out = torch.full((sum(gm), n), float("nan"), dtype=torch.bfloat16, device=DEV)
+        outs.append(pkg.grouped_gemm_fp8(x, w, gm, xs, ws, out=out))
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    row = 0
+    for gi, m in enumerate(gm):
+        ref = (x[row:row + m].float() @ w[gi].float().t().contiguous()) * xs[0] * ws[gi]
+        got = outs[0][row:row + m].float()
+        assert not torch.isnan(got).any(), f"group {gi}: unwritten outputs"
+        bad = int(((got - ref).abs() > ATOL + RTOL * ref.abs()).sum())
+        assert bad == 0, f"group {gi}: {bad} outputs off"
+        row += m
+
+
+def test_dgrad_descriptors_match_walk(pkg, monkeypatch):
+    gm, n, k = [1000, 0, 2500, 300, 4096, 0, 17], 2048, 1536
+    g = torch.Generator(device=DEV).manual_seed(98)
+    go = torch.randn((sum(gm), n), generator=g, device=DEV).to(torch.bfloat16)
+    w = torch.randn((len(gm), n, k), generator=g, device=DEV).to(torch.bfloat16)
+    s = torch.cuda.current_stream(DEV).cuda_stream
+    outs = []
+    for desc in (True, False):
+        if desc:
+            monkeypatch.delenv("GG_TILE_DESC", raising=False)
+        else:
+            monkeypatch.setenv("GG_TILE_DESC", "0")
+        out = torch.full((sum(gm), k), float("nan"), dtype=torch.bfloat16, device=DEV)
+        plan = pkg.BackwardPlan("dgrad", pkg.DType.BF16, n, k, gm, go.data_ptr(), w.data_ptr(), out.data_ptr(), s)
+        plan.run(s)
+        torch.cuda.synchronize(DEV)
+        plan.release()
+        outs.append(out)
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    row = 0
+    for gi, m in enumerate(gm):
+        ref = go[row:row + m].float() @ w[gi].float()
+        got = outs[0][row:row + m].float()
+        assert not torch.isnan(got).any(), f"group {gi}: unwritten outputs"
+        bad = int(((got - ref).abs() > ATOL + RTOL * ref.abs()).sum())
+        assert bad == 0, f"group {gi}: {bad} outputs off"
+        row += m
