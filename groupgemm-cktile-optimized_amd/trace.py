@@ -70,7 +70,13 @@ def resource_line(name: str) -> str:
     return ", ".join(f"{k} {v}" for k, v in vals.items())
 
 
-def trace_workload(w: str, op: str, raw: str, profiles: str, limit: int, workloads) -> dict:
+def kernel_label(name: str) -> str:
+    """A kernel's demangled name without its namespace qualifiers and argument list."""
+    name = name.replace("(anonymous namespace)::", "")
+    return re.sub(r"\([^()]*\)$", "", name).replace("void ", "", 1)
+
+
+def trace_workload(w: str, op: str, raw: str, profiles: str, limit: int, workloads, rerun: bool = True) -> dict:
     tag = w if op == "fwd" else f"{w}_{op}"
     out_dir = os.path.join(raw, tag)
     os.makedirs(out_dir, exist_ok=True)
@@ -78,9 +84,14 @@ def trace_workload(w: str, op: str, raw: str, profiles: str, limit: int, workloa
                   "--power-seconds", "0", "--baselines", ""]
     cmd = (["timeout", "-s", "KILL", str(limit), "rocprofv3", "--kernel-trace", "--stats", "-d", out_dir, "-o", tag,
             "--output-format", "csv", "--", sys.executable, os.path.join(ROOT, "bench.py")] + bench_args)
-    p = subprocess.run(cmd, cwd="/tmp", capture_output=True, text=True)
-    with open(os.path.join(out_dir, "run.log"), "w") as f:
-        f.write(" ".join(cmd) + "\n---- stdout ----\n" + p.stdout + "\n---- stderr ----\n" + p.stderr)
+    if rerun:
+        p = subprocess.run(cmd, cwd="/tmp", capture_output=True, text=True)
+        with open(os.path.join(out_dir, "run.log"), "w") as f:
+            f.write(" ".join(cmd) + "\n---- stdout ----\n" + p.stdout + "\n---- stderr ----\n" + p.stderr)
+    else:  # summarise an earlier run from its log and CSV files
+        text = open(os.path.join(out_dir, "run.log")).read()
+        out, err = text.split("\n---- stdout ----\n", 1)[1].split("\n---- stderr ----\n", 1)
+        p = subprocess.CompletedProcess(cmd, 0, out, err)
     line = next((x for x in p.stdout.splitlines() if x.startswith("{") and '"metric"' in x), None)
     files = glob.glob(os.path.join(out_dir, "**", "*.csv"), recursive=True)
     # rocprofv3 may end with a segmentation fault after the program finished and wrote its line
@@ -129,9 +140,8 @@ def trace_workload(w: str, op: str, raw: str, profiles: str, limit: int, workloa
         "|---|---|---|---|---|",
     ]
     for r in stats:
-        nm = r.get("Name", r.get("KernelName", ""))
-        nm = re.sub(r"\(.*$", "", nm)
-        lines.append(f"| `{nm[:90]}` | {r.get('Calls')} | {float(r.get('AverageNs', 0)):,.0f} | "
+        nm = kernel_label(r.get("Name", r.get("KernelName", "")))
+        lines.append(f"| `{nm[:100]}` | {r.get('Calls')} | {float(r.get('AverageNs', 0)):,.0f} | "
                      f"{float(r.get('MinNs', 0)):,.0f} | {float(r.get('MaxNs', 0)):,.0f} |")
     lines += [
         "",
@@ -168,6 +178,8 @@ def main():
     ap.add_argument("--raw", default=os.path.join(ROOT, "gpurun_out", "trace"))
     ap.add_argument("--profiles", default=os.path.join(ROOT, "profiles"))
     ap.add_argument("--limit", type=int, default=120, help="seconds per rocprofv3 run")
+    ap.add_argument("--summarise-only", action="store_true",
+                    help="write the summaries from the runs already under --raw (no rocprofv3)")
     ap.add_argument("--fill-resources", action="store_true",
                     help="only rewrite the compiler-report line of the existing summaries (where the build's "
                          "lib/resource_usage.txt is, which GPU runs need not carry)")
@@ -188,7 +200,8 @@ def main():
     names = sorted(bench.WORKLOADS) if args.workloads == "all" else args.workloads.split(",")
     for w in names:
         try:
-            r = trace_workload(w, args.op, args.raw, args.profiles, args.limit, bench.WORKLOADS)
+            r = trace_workload(w, args.op, args.raw, args.profiles, args.limit, bench.WORKLOADS,
+                               rerun=not args.summarise_only)
         except RuntimeError as e:
             log(f"stopped: {e}")
             sys.exit(1)
