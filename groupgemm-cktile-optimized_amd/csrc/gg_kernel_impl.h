@@ -877,7 +877,8 @@ grouped_gemm_kernel(const KernelArgs args) {
         uint32_t  rows;           // this wave's row blocks (bit mi) that hold a valid output
     };
     const int bad_off = static_cast<int>(0x80000000u);
-    int       g       = 0; // group hint of locate_tile (logical tiles only grow)
+    int       g       = 0; // group hint of locate_tile (a workgroup's logical tiles grow, but
+                           // for split-K units, which make_tile restarts the scan for)
     // The group table and the fp8 scales do not change while the kernel runs: read through the
     // constant address space they take scalar loads (lgkmcnt). Through a global pointer the
     // compiler issues vector loads and waits for them with vmcnt(0), which also drains every
@@ -904,6 +905,12 @@ grouped_gemm_kernel(const KernelArgs args) {
         } else if (splits > 1) {
             split = t / total_tiles;
             L     = t - split * total_tiles;
+            // A workgroup's units wrap around the tile list when units outnumber the grid (the
+            // grid is not a multiple of the tile count), so its logical tiles are not monotone:
+            // restart the group scan, whose hint only moves forward, when the tile lies before
+            // the hinted group.
+            if (!in_kernel_table && L < const_table[g].tile0)
+                g = 0;
         } else if (TAIL && t >= full) {
             // a K range of a last-round tile: that tile's place in the round decides the XCD order
             tail   = (t - full) % rem;

@@ -71,6 +71,9 @@ FORCED = [
     (1, [129], 136, 264, 5),             # 5 K steps, one per range, partial last
     (0, [2048] * 4, 1024, 512, 8),       # 128 tiles x 8 ranges: several units per workgroup
     (0, [300, 40], 512, 512, 64),        # asked for more ranges than K steps: one step each
+    # 48 tiles x 8 ranges = 384 units on 256 workgroups: a workgroup's second unit wraps to an
+    # earlier tile of an earlier group (the kernel's group scan has to restart)
+    (0, [512, 512], 2880, 1024, 8),
 ]
 
 
