@@ -54,8 +54,9 @@ typedef struct gg_plan gg_plan;
 
 /*
  * Validate the problem and build its plan. Replaces CkTileBackend::prepare_typed + finish
- * (ck_kernel/ck_grouped_gemm.cpp:153-218): per-group row offsets and tile ranges, one
- * hipMalloc + H2D copy of the argument table on `stream`, then a stream sync.
+ * (ck_kernel/ck_grouped_gemm.cpp:153-218): per-group row offsets and tile ranges, a hipMalloc
+ * + H2D copy of the argument table on `stream` (and of the per-workgroup tile descriptors, and
+ * the fp32 workspace of a split-K or tail-split plan), then a stream sync.
  *   group_m: host array of group_num row counts (>= 0; zero-row groups are skipped).
  *   x, w, out: device buffers laid out as above; they must stay valid while the plan is used.
  * Requirements (else GG_ERR_UNSUPPORTED): n % 8 == 0 and k % 8 == 0 (16-byte rows for the
@@ -67,7 +68,8 @@ int gg_prepare(int dtype, int group_num, int64_t n, int64_t k, const int64_t *gr
                const void *x, const void *w, void *out, void *stream, gg_plan **plan_out);
 
 /*
- * Enqueue the grouped GEMM of `plan` on `stream`: one kernel launch, no host sync, no
+ * Enqueue the grouped GEMM of `plan` on `stream`: one kernel launch (two for a split-K or
+ * tail-split plan: the GEMM, then the reduction of its partial sums), no host sync, no
  * allocation. Replaces CkTileBackend::run / CkGroupedGemm::launch
  * (ck_kernel/ck_grouped_gemm.cpp:140, 114-121). Problems with no output rows are a no-op;
  * k == 0 writes zeros.
