@@ -11,6 +11,21 @@
 
 namespace gg {
 
+// Cross-tile launch of one tile shape: the instance without the K-tail mask (KT = false) when K
+// is a multiple of the mode's K step and an operand is K-major (forward, dgrad; wgrad's
+// operands are both MN-major and mask no K tail).
+template <bool F16, int MODE, int SHAPE>
+void launch_cross(const KernelArgs &args, dim3 g, dim3 b, hipStream_t stream) {
+    constexpr int ks = MODE / 4 == kIn16 ? kTileK : 2 * kTileK; // fp8: 128 K values per step
+    if constexpr (MODE % 4 != kWgrad) {
+        if (args.k % ks == 0) {
+            hipLaunchKernelGGL((grouped_gemm_kernel<F16, true, MODE, SHAPE, false, false>), g, b, 0, stream, args);
+            return;
+        }
+    }
+    hipLaunchKernelGGL((grouped_gemm_kernel<F16, true, MODE, SHAPE>), g, b, 0, stream, args);
+}
+
 template <bool F16, int MODE>
 void launch_mode(const KernelArgs &args, bool cross, dim3 g, dim3 b, hipStream_t stream) {
     if constexpr (has_short_tiles(MODE)) {
@@ -26,7 +41,7 @@ void launch_mode(const KernelArgs &args, bool cross, dim3 g, dim3 b, hipStream_t
                 return;
             }
         }
-        hipLaunchKernelGGL((grouped_gemm_kernel<F16, true, MODE>), g, b, 0, stream, args);
+        launch_cross<F16, MODE, kShapeWide>(args, g, b, stream);
         return;
     }
     if constexpr (MODE == make_mode(kFwd, kIn16)) {
@@ -47,7 +62,7 @@ void launch_short(const KernelArgs &args, bool cross, dim3 g, dim3 b, hipStream_
                 return;
             }
         }
-        hipLaunchKernelGGL((grouped_gemm_kernel<F16, true, MODE, kShapeShort>), g, b, 0, stream, args);
+        launch_cross<F16, MODE, kShapeShort>(args, g, b, stream);
     } else
         hipLaunchKernelGGL((grouped_gemm_kernel<F16, false, MODE, kShapeShort>), g, b, 0, stream, args);
 }

@@ -642,7 +642,11 @@ constexpr bool kTailSkip = GG_TAIL_SKIP;
 // TAIL (cross-tile 16-bit forward only): the plan cuts its last-round tiles into K ranges (tail
 // split: K ranges of last-round tiles store partial sums from epilogue_lds); instances without it
 // carry none of its state.
-template <bool F16, bool CROSS, int MODE, int SHAPE = kShapeWide, bool TAIL = false>
+// KT: the problem may have a partial last K step (K % K-step != 0), whose DMAs of K-major
+// operands mask the chunks past K. Instances with KT = false (K a multiple of the K step) leave
+// the mask out of the checked steps: its per-DMA VALU OR sits between the offset and the DMA and
+// cost 2.4 % on config 3.
+template <bool F16, bool CROSS, int MODE, int SHAPE = kShapeWide, bool TAIL = false, bool KT = true>
 __global__ void __launch_bounds__(kThreads, 1) __attribute__((amdgpu_waves_per_eu(1, 1)))
 grouped_gemm_kernel(const KernelArgs args) {
     constexpr bool A_MN   = mode_a_mn(MODE), B_MN = mode_b_mn(MODE);
@@ -1060,7 +1064,7 @@ grouped_gemm_kernel(const KernelArgs args) {
                 d.vadd = 0;
                 // the unit's partial last K step (a next unit has at least kCrossMinSteps steps, so
                 // the three prefetched never include its last, and koff < 3 < T - 1 for them)
-                d.mask = (koff == T - 1 && cur.klast) ? ktail_bad : 0;
+                d.mask = (KT && koff == T - 1 && cur.klast) ? ktail_bad : 0;
             }
         } else {
             d.rs = rc;
