@@ -759,6 +759,11 @@ grouped_gemm_kernel(const KernelArgs args) {
         if constexpr (!kSameOff)
             voff[1][j] = dma_off(B_MN, j, args.ldb);
     });
+    // MN-major operands in unchecked steps: the lane offsets with the current tile's column mask
+    // already applied (set once per tile by set_mn_offsets), and the K step in soffset. Every
+    // row of an unchecked step lies inside the contraction, so nothing there relies on the
+    // lane offset's range check for rows, and the DMAs need no VALU add and OR per step.
+    int voffm[2][kLoads] = {};
     // Last K step when K % 64 != 0: chunks at k >= K get an offset past every bound.
     const int k_last    = K - (T - 1) * KS; // valid K of the last step
     int       ktail_bad = (ld_chunk * (16 / ES) >= k_last) ? static_cast<int>(0x80000000u) : 0;
@@ -820,6 +825,10 @@ grouped_gemm_kernel(const KernelArgs args) {
             fresh_v(voff[0][j]);
             if constexpr (!kSameOff)
                 fresh_v(voff[1][j]);
+            if constexpr (A_MN)
+                fresh_v(voffm[0][j]);
+            if constexpr (B_MN)
+                fresh_v(voffm[1][j]);
         });
         fresh_v(ktail_bad);
         fresh_v(voffc);
@@ -1069,10 +1078,11 @@ grouped_gemm_kernel(const KernelArgs args) {
         } else {
             d.rs = rc;
             if constexpr (MN) {
-                d.so   = 0;
-                d.vadd = (kidx + cur.k0) * kTileK * ld * 2;
-                d.mask  = oc + mn_col(0) >= ld ? bad_off : 0;
-                d.mask1 = oc + mn_col(1) >= ld ? bad_off : 0;
+                // the column masks are in voffm (set_mn_offsets)
+                d.so    = (kidx + cur.k0) * kTileK * ld * 2;
+                d.vadd  = 0;
+                d.mask  = 0;
+                d.mask1 = 0;
             } else {
                 d.so   = (kidx + cur.k0) * kRowBytes;
                 d.vadd = 0;
@@ -1086,12 +1096,24 @@ grouped_gemm_kernel(const KernelArgs args) {
         constexpr bool B  = decltype(b_op)::value;
         constexpr bool MN = B ? B_MN : A_MN;
         const int      vo = voff[(B && !kSameOff) ? 1 : 0][j];
-        if constexpr (MN)
+        if constexpr (MN && !decltype(checked)::value)
+            return voffm[B ? 1 : 0][j];
+        else if constexpr (MN)
             return (vo + d.vadd) | (mn_swz(j) ? d.mask1 : d.mask);
         else if constexpr (decltype(checked)::value)
             return vo | d.mask;
         else
             return vo;
+    };
+    // The current tile's column masks folded into the MN-major lane offsets (voffm), once per
+    // tile before its unchecked steps: the mask of DMA j is that of its column-block swap.
+    auto set_mn_offsets = [&](const Tile &tl) {
+        sfor<0, kLoads>([&](auto j) {
+            if constexpr (A_MN)
+                voffm[0][j] = voff[0][j] | (tl.o0a + mn_col(mn_swz(j)) >= args.lda ? bad_off : 0);
+            if constexpr (B_MN)
+                voffm[1][j] = voff[kSameOff ? 0 : 1][j] | (tl.o0b + mn_col(mn_swz(j)) >= args.ldb ? bad_off : 0);
+        });
     };
     // DMA with its own M0 write (prologue).
     auto dma_now = [&](uint32_t dst, auto b_op, auto j, int kidx) {
@@ -1457,6 +1479,8 @@ grouped_gemm_kernel(const KernelArgs args) {
             step.template operator()<0, 0, true, true, false>(0);
         }
         int kt = 1; // kt % 6 == 1 at the top of each block of six steps
+        if constexpr (A_MN || B_MN)
+            set_mn_offsets(cur);
         // Unchecked: every prefetch of the block (up to kt + 8) is a full step before T-1.
         for (; !thin && kt + 9 < T; kt += 6) {
             refresh();
