@@ -124,6 +124,7 @@ void fill_args(gg_plan *plan, int n_xcd) {
     a.tail_splits = 1;
     a.desc        = nullptr;
     a.desc_per_wg = 0;
+    a.tails       = 1; // set by the plan builders that know the sizes
 }
 
 // Split-K for problems whose tiles cannot fill the GPU (fewer than half as many tiles as CUs):
@@ -573,6 +574,11 @@ int plan_device_lens(gg_plan *plan, bool noalloc, int op, int a_dtype, int b_dty
     fill_args(plan, 1);
     gg::KernelArgs &ka = plan->args;
     ka.k_tiles         = op == GG_OP_WGRAD ? 1 : static_cast<int>(gg::cdiv(k_c, steps));
+    // tails (see KernelArgs): forward has K-major operands only; dgrad's w columns are the k of
+    // its output; wgrad's K steps depend on the device-resident sizes, so it keeps the masks
+    ka.tails = op == GG_OP_FORWARD ? (k_c % steps != 0)
+               : op == GG_OP_DGRAD ? (k_c % steps != 0 || k % gg::kTileN != 0)
+                                   : 1;
     ka.x_scale         = f8 ? a_scale : nullptr;
     ka.w_scale         = f8 ? b_scale : nullptr;
     if (op != GG_OP_FORWARD) {
@@ -734,6 +740,7 @@ int gg_prepare(int dtype, int group_num, int64_t n, int64_t k, const int64_t *gr
         gg::KernelArgs &a = plan->args;
         a.total_tiles     = plan->total_tiles;
         a.d_total         = nullptr;
+        a.tails           = k % gg::kTileK != 0; // K-major operands: only a partial K step
         if (setup_split_k(plan, prop) != GG_OK) {
             free_plan(plan);
             return GG_ERR_HIP;
@@ -903,6 +910,16 @@ static int prepare_backward(int layout, int dtype_a, int dtype_b, int group_num,
         }
         ka.x_scale         = f8 ? a_scale : nullptr;
         ka.w_scale         = f8 ? b_scale : nullptr;
+        // tails (see KernelArgs). dgrad: the contraction n and w's columns k. wgrad: every group's
+        // rows (its contraction) and the columns of grad_out (n) and x (k).
+        if (dgrad) {
+            ka.tails = n % steps != 0 || k % gg::kTileN != 0;
+        } else {
+            bool t = n % gg::kTileN != 0 || k % gg::kTileN != 0;
+            for (int g = 0; g < group_num; ++g)
+                t = t || group_m[g] % steps != 0;
+            ka.tails = t;
+        }
         // wgrad's K steps differ per group: no split
         if (dgrad && setup_split_k(plan, prop) != GG_OK) {
             free_plan(plan);
@@ -1016,6 +1033,7 @@ int gg_prepare_fp8(int dtype, int group_num, int64_t n, int64_t k, const int64_t
         a.total_tiles     = plan->total_tiles;
         a.d_total         = nullptr;
         a.k_tiles         = static_cast<int>(gg::cdiv(k, 128)); // 128 fp8 values per K step
+        a.tails           = k % 128 != 0;
         a.x_scale         = x_scale;
         a.w_scale         = w_scale;
         if (setup_split_k(plan, prop) != GG_OK) {

@@ -11,17 +11,13 @@
 
 namespace gg {
 
-// Cross-tile launch of one tile shape: the instance without the K-tail mask (KT = false) when K
-// is a multiple of the mode's K step and an operand is K-major (forward, dgrad; wgrad's
-// operands are both MN-major and mask no K tail).
+// Cross-tile launch of one tile shape: the instance without tail masks (KT = false) when the
+// plan has no partial K step and no column tail of an MN-major operand (args.tails == 0).
 template <bool F16, int MODE, int SHAPE>
 void launch_cross(const KernelArgs &args, dim3 g, dim3 b, hipStream_t stream) {
-    constexpr int ks = MODE / 4 == kIn16 ? kTileK : 2 * kTileK; // fp8: 128 K values per step
-    if constexpr (MODE % 4 != kWgrad) {
-        if (args.k % ks == 0) {
-            hipLaunchKernelGGL((grouped_gemm_kernel<F16, true, MODE, SHAPE, false, false>), g, b, 0, stream, args);
-            return;
-        }
+    if (args.tails == 0) {
+        hipLaunchKernelGGL((grouped_gemm_kernel<F16, true, MODE, SHAPE, false, false>), g, b, 0, stream, args);
+        return;
     }
     hipLaunchKernelGGL((grouped_gemm_kernel<F16, true, MODE, SHAPE>), g, b, 0, stream, args);
 }

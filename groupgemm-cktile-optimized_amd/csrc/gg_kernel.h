@@ -83,6 +83,8 @@ struct KernelArgs {
     // dgrad plans without split-K or tail split (TileDesc, built by the plan).
     const int        *desc;
     int               desc_per_wg;
+    int               tails;       // 0: no partial K step and no column tail of an MN-major
+                                   // operand anywhere in the plan (instances without the masks)
 };
 
 // One tile descriptor (see KernelArgs::desc).

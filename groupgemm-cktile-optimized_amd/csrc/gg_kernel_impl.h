@@ -642,10 +642,12 @@ constexpr bool kTailSkip = GG_TAIL_SKIP;
 // TAIL (cross-tile 16-bit forward only): the plan cuts its last-round tiles into K ranges (tail
 // split: K ranges of last-round tiles store partial sums from epilogue_lds); instances without it
 // carry none of its state.
-// KT: the problem may have a partial last K step (K % K-step != 0), whose DMAs of K-major
-// operands mask the chunks past K. Instances with KT = false (K a multiple of the K step) leave
-// the mask out of the checked steps: its per-DMA VALU OR sits between the offset and the DMA and
-// cost 2.4 % on config 3.
+// KT: the problem may have a partial K step (K-major operands mask the chunks past K; MN-major
+// ones put the K step in the lane offset, whose range check drops rows past K) or a column tail
+// of an MN-major operand (lanes past the stored row masked). Instances with KT = false (the plan
+// says there is neither: KernelArgs::tails == 0) give their checked steps the unchecked steps'
+// DMA offsets, with no per-DMA VALU OR or add between the offset and the DMA (that cost 2.4 %
+// on config 3).
 template <bool F16, bool CROSS, int MODE, int SHAPE = kShapeWide, bool TAIL = false, bool KT = true>
 __global__ void __launch_bounds__(kThreads, 1) __attribute__((amdgpu_waves_per_eu(1, 1)))
 grouped_gemm_kernel(const KernelArgs args) {
@@ -1063,7 +1065,12 @@ grouped_gemm_kernel(const KernelArgs args) {
             else
                 kabs = in_cur ? koff + cur.k0 : koff;
             d.rs           = in_cur ? rc : (cross_next ? rn : rsrc_0);
-            if constexpr (MN) {
+            if constexpr (MN && !KT) { // no partial K step, no column tail
+                d.so    = kabs * kTileK * ld * 2;
+                d.vadd  = 0;
+                d.mask  = 0;
+                d.mask1 = 0;
+            } else if constexpr (MN) {
                 d.so   = 0;
                 d.vadd = kabs * kTileK * ld * 2;
                 d.mask  = (in_cur ? oc : on) + mn_col(0) >= ld ? bad_off : 0;
@@ -1098,6 +1105,8 @@ grouped_gemm_kernel(const KernelArgs args) {
         const int      vo = voff[(B && !kSameOff) ? 1 : 0][j];
         if constexpr (MN && !decltype(checked)::value)
             return voffm[B ? 1 : 0][j];
+        else if constexpr (MN && !KT)
+            return vo;
         else if constexpr (MN)
             return (vo + d.vadd) | (mn_swz(j) ? d.mask1 : d.mask);
         else if constexpr (decltype(checked)::value)
