@@ -49,6 +49,9 @@ void launch_mode(const KernelArgs &args, bool cross, dim3 g, dim3 b, hipStream_t
     hipLaunchKernelGGL((grouped_gemm_kernel<F16, false, MODE>), g, b, 0, stream, args);
 }
 
+// Defined only in the short-tile parts (14-17); launch_mode's calls in parts 0-3 link to their
+// explicit instantiations, so the short-tile kernels compile once.
+#if GG_PART >= 14
 template <bool F16, int MODE>
 void launch_short(const KernelArgs &args, bool cross, dim3 g, dim3 b, hipStream_t stream) {
     if (cross) {
@@ -62,6 +65,7 @@ void launch_short(const KernelArgs &args, bool cross, dim3 g, dim3 b, hipStream_
     } else
         hipLaunchKernelGGL((grouped_gemm_kernel<F16, false, MODE, kShapeShort>), g, b, 0, stream, args);
 }
+#endif
 
 // part -> (fp16 MFMA, mode); the dispatch's switch in gg_kernel.hip covers the same 14 pairs
 #if GG_PART == 0
