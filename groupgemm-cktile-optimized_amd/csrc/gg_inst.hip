@@ -41,8 +41,17 @@ void launch_mode(const KernelArgs &args, bool cross, dim3 g, dim3 b, hipStream_t
         return;
     }
     if constexpr (MODE == make_mode(kFwd, kIn16)) {
+        // 16-bit forward per-tile plans (one round: config 5b's narrow tiles) also have instances
+        // without tail masks
         if (args.tile_n == kNarrowTileN) {
-            hipLaunchKernelGGL((grouped_gemm_kernel<F16, false, MODE, kShapeNarrow>), g, b, 0, stream, args);
+            if (args.tails == 0)
+                hipLaunchKernelGGL((grouped_gemm_kernel<F16, false, MODE, kShapeNarrow, false, false>), g, b, 0, stream, args);
+            else
+                hipLaunchKernelGGL((grouped_gemm_kernel<F16, false, MODE, kShapeNarrow>), g, b, 0, stream, args);
+            return;
+        }
+        if (args.tails == 0) {
+            hipLaunchKernelGGL((grouped_gemm_kernel<F16, false, MODE, kShapeWide, false, false>), g, b, 0, stream, args);
             return;
         }
     }
