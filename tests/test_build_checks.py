@@ -1,6 +1,11 @@
-"""The build's assembly check for VALU SGPR -> VMEM hazards (csrc/check_vmem_sgpr_hazard.py),
-on hand-written gfx9 snippets: the hazard is caught straight-line and across a branch, and 5
-wait states (instructions or s_nop) clear it."""
+"""The build's assembly checks, on hand-written gfx9 snippets.
+
+- VALU SGPR -> VMEM hazards (csrc/check_vmem_sgpr_hazard.py): caught straight-line and across a
+  branch; 5 wait states (instructions or s_nop) clear them.
+- Accumulator reads after an inline-asm MFMA (csrc/check_mfma_acc_hazard.py): caught within 19
+  wait states, across a fall-through and a loop's back edge; reads of other AGPRs pass; SGPR
+  spill traffic in a K-loop block (many MFMAs) fails, in a single step's block it does not.
+"""
 import importlib.util
 import os
 
@@ -78,3 +83,72 @@ k:
     v_readlane_b32 s4, v197, 28
     s_cbranch_scc1 .LBB0_1
     s_endpgm""")) == 1
+
+
+# ---- accumulator reads after an inline-asm MFMA (csrc/check_mfma_acc_hazard.py) ----
+spec2 = importlib.util.spec_from_file_location(
+    "acc", os.path.join(ROOT, "groupgemm-cktile-optimized_amd", "csrc", "check_mfma_acc_hazard.py"))
+acc = importlib.util.module_from_spec(spec2)
+spec2.loader.exec_module(acc)
+
+
+def _acc(body):
+    return acc.scan_text("\n_Zk:\n" + body.strip() + "\n.Lfunc_end0:\n")
+
+
+def test_accumulator_read_right_after_mfma_is_flagged():
+    bad, _ = _acc("""
+    v_mfma_f32_16x16x32_bf16 a[4:7], v[0:3], v[8:11], a[4:7]
+    v_accvgpr_read_b32 v20, a5""")
+    assert len(bad) == 1 and "after 0 wait states" in bad[0]
+
+
+def test_nineteen_wait_states_or_other_registers_clear_it():
+    bad, _ = _acc("""
+    v_mfma_f32_16x16x32_bf16 a[4:7], v[0:3], v[8:11], a[4:7]
+    s_nop 7
+    s_nop 7
+    s_nop 2
+    v_accvgpr_read_b32 v20, a5""")
+    assert not bad
+    bad, _ = _acc("""
+    v_mfma_f32_16x16x32_bf16 a[4:7], v[0:3], v[8:11], a[4:7]
+    s_nop 7
+    s_nop 7
+    s_nop 1
+    v_accvgpr_read_b32 v20, a5""")
+    assert len(bad) == 1  # 18 wait states
+    bad, _ = _acc("""
+    v_mfma_f32_16x16x32_bf16 a[4:7], v[0:3], v[8:11], a[4:7]
+    v_accvgpr_read_b32 v20, a8
+    global_store_dwordx4 v[0:1], a[0:3], off""")
+    assert not bad
+
+
+def test_store_of_an_mfma_result_and_a_read_across_a_branch_are_flagged():
+    bad, _ = _acc("""
+    v_mfma_f32_16x16x32_bf16 a[0:3], v[0:3], v[8:11], a[0:3]
+    global_store_dwordx4 v[4:5], a[0:3], off""")
+    assert len(bad) == 1
+    # through a back edge: the MFMA ends the loop block, the read starts it
+    bad, _ = _acc("""
+.LBB0_1:
+    v_accvgpr_read_b32 v20, a2
+    v_mfma_f32_16x16x32_bf16 a[0:3], v[0:3], v[8:11], a[0:3]
+    s_cbranch_scc1 .LBB0_1
+    s_endpgm""")
+    assert len(bad) == 1
+    # through a fall-through into the next block
+    bad, _ = _acc("""
+    v_mfma_f32_16x16x32_bf16 a[0:3], v[0:3], v[8:11], a[0:3]
+.LBB0_2:
+    v_accvgpr_read_b32 v20, a1""")
+    assert len(bad) == 1
+
+
+def test_spill_traffic_in_the_k_loop_is_flagged():
+    mfma = "    v_mfma_f32_16x16x32_bf16 a[0:3], v[0:3], v[8:11], a[0:3]"
+    _, spills = _acc(".LBB0_3:\n    v_readlane_b32 s4, v185, 12\n" + "\n".join([mfma] * acc.LOOP_MFMAS))
+    assert len(spills) == 1
+    _, spills = _acc(".LBB0_3:\n    v_readlane_b32 s4, v185, 12\n" + "\n".join([mfma] * 16))
+    assert not spills  # a single step's block (first or checked steps) may reload
