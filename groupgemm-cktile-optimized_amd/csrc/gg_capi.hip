@@ -266,6 +266,58 @@ int use_short_tiles(gg_plan *plan, const int64_t *group_m, hipStream_t s) {
     return GG_OK;
 }
 
+// Short-wide tiles (at most 192 x 288) for a cross-tile 16-bit forward plan of short tiles: nine
+// column blocks per wave instead of eight, so the same loads per K step feed 9/8 of the MFMAs and
+// fewer tiles make fewer rounds (32 groups of 520 rows, N = K = 2880: 1152 short tiles, 4.5
+// rounds on 256 CUs; 960 short-wide tiles, 3.75 rounds, and no 64-column tail tile). A
+// short-wide tile is modelled at kWideTileCost short tiles (its K step moves 7 % more bytes for
+// 12.5 % more MFMAs); taken when the modelled busiest workgroup gains at least 5 % and the plan
+// stays cross-tile. The group table is rebuilt for the 288-column tiles.
+// GG_WIDE=0 in the environment turns this off, GG_WIDE=1 takes short-wide tiles wherever the
+// plan allows them.
+constexpr double kWideTileCost = 1.10;
+
+int use_short_wide_tiles(gg_plan *plan, const int64_t *group_m, const hipDeviceProp_t &prop, hipStream_t s) {
+    gg::KernelArgs &a   = plan->args;
+    const char     *env = std::getenv("GG_WIDE");
+    const int       opt = env != nullptr && *env != '\0' ? std::atoi(env) : -1;
+    if (opt == 0 || plan->mode != gg::make_mode(gg::kFwd, gg::kIn16) || a.tile_m == gg::kTileM ||
+        a.tile_n != gg::kTileN || a.splits > 1 || a.d_total != nullptr || a.d_lens != nullptr)
+        return GG_OK;
+    const int64_t n_tiles = gg::cdiv(plan->n, gg::kShortWideTileN);
+    std::vector<gg::GroupEntry> table(static_cast<size_t>(plan->group_num));
+    const int64_t tiles = gg::build_group_table(group_m, plan->group_num, n_tiles, table.data(), 0, a.tile_m);
+    if (tiles <= 0 || tiles > INT32_MAX)
+        return GG_OK;
+    const int grid  = static_cast<int>(std::min<int64_t>(prop.multiProcessorCount, tiles));
+    const int n_xcd = grid % xcd_count(prop) == 0 ? xcd_count(prop) : 1;
+    gg::KernelArgs w = a;
+    w.total_tiles    = static_cast<int>(tiles);
+    w.n_tiles        = static_cast<int>(n_tiles);
+    w.tile_n         = gg::kShortWideTileN;
+    w.n_xcd          = n_xcd;
+    if (!gg::uses_cross_tile(w, grid, plan->mode))
+        return GG_OK;
+    if (opt != 1) {
+        const double short_ = busiest_workgroup(group_m, plan->group_num, a.n_tiles, a.tile_m, plan->total_tiles,
+                                                plan->grid, a.n_xcd);
+        const double wide   = kWideTileCost * busiest_workgroup(group_m, plan->group_num, n_tiles, a.tile_m,
+                                                                w.total_tiles, grid, n_xcd);
+        if (wide > 0.95 * short_)
+            return GG_OK;
+    }
+    hipError_t e = hipMemcpyAsync(plan->d_groups, table.data(), table.size() * sizeof(gg::GroupEntry),
+                                  hipMemcpyHostToDevice, s);
+    if (e == hipSuccess)
+        e = hipStreamSynchronize(s);
+    if (e != hipSuccess)
+        return hip_fail(e, "short-wide group table upload");
+    plan->total_tiles = w.total_tiles;
+    plan->grid        = grid;
+    a                 = w;
+    return GG_OK;
+}
+
 // Picks the plan's split count (plan->args filled, k_tiles set) and allocates the partial sums.
 int setup_split_k(gg_plan *plan, const hipDeviceProp_t &prop) {
     gg::KernelArgs &a  = plan->args;
@@ -304,7 +356,7 @@ int setup_tail_split(gg_plan *plan) {
     gg::KernelArgs &a = plan->args;
     a.tail_splits     = 1;
     if (plan->mode != gg::make_mode(gg::kFwd, gg::kIn16) || a.splits > 1 || a.d_total != nullptr ||
-        a.d_lens != nullptr || !gg::uses_cross_tile(a, plan->grid, plan->mode))
+        a.d_lens != nullptr || a.tile_n != gg::kTileN || !gg::uses_cross_tile(a, plan->grid, plan->mode))
         return GG_OK;
     const int grid = plan->grid, tiles = plan->total_tiles;
     const int full = tiles / grid * grid, rem = tiles - full;
@@ -748,6 +800,10 @@ int gg_prepare(int dtype, int group_num, int64_t n, int64_t k, const int64_t *gr
         if (const int st2 = use_short_tiles(plan, group_m, s); st2 != GG_OK) {
             free_plan(plan);
             return st2;
+        }
+        if (use_short_wide_tiles(plan, group_m, prop, s) != GG_OK) {
+            free_plan(plan);
+            return GG_ERR_HIP;
         }
         if (use_narrow_tiles(plan, group_m, prop, s) != GG_OK) {
             free_plan(plan);

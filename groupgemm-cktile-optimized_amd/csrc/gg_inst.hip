@@ -1,12 +1,13 @@
 // One instance unit of the persistent grouped GEMM: the (input type, mode) pair GG_PART selects,
-// both variants (cross-tile and per-tile), or (parts 14-17) the short-tile instances. 16-bit
-// forward units also hold the cross-tile instances with the tail split (TAIL).
+// both variants (cross-tile and per-tile), (parts 14-17) the short-tile instances or (parts 18-19)
+// the short-wide forward instances. 16-bit forward units also hold the cross-tile instances with
+// the tail split (TAIL).
 // The Makefile compiles this file once per part, in parallel; gg_kernel.hip's dispatch calls
 // launch_mode of every part.
 #include "gg_kernel_impl.h"
 
 #ifndef GG_PART
-#error "GG_PART selects the instance (0-17)"
+#error "GG_PART selects the instance (0-19)"
 #endif
 
 namespace gg {
@@ -60,11 +61,15 @@ void launch_mode(const KernelArgs &args, bool cross, dim3 g, dim3 b, hipStream_t
 
 // Defined only in the short-tile parts (14-17); launch_mode's calls in parts 0-3 link to their
 // explicit instantiations, so the short-tile kernels compile once.
-#if GG_PART >= 14
+#if GG_PART >= 14 && GG_PART <= 17
 template <bool F16, int MODE>
 void launch_short(const KernelArgs &args, bool cross, dim3 g, dim3 b, hipStream_t stream) {
     if (cross) {
         if constexpr (MODE == make_mode(kFwd, kIn16)) {
+            if (args.tile_n == kShortWideTileN) { // cross-tile only (launch_grouped_gemm checks)
+                launch_short_wide<F16>(args, g, b, stream);
+                return;
+            }
             if (args.tail_splits > 1) {
                 hipLaunchKernelGGL((grouped_gemm_kernel<F16, true, MODE, kShapeShort, true>), g, b, 0, stream, args);
                 return;
@@ -73,6 +78,12 @@ void launch_short(const KernelArgs &args, bool cross, dim3 g, dim3 b, hipStream_
         launch_cross<F16, MODE, kShapeShort>(args, g, b, stream);
     } else
         hipLaunchKernelGGL((grouped_gemm_kernel<F16, false, MODE, kShapeShort>), g, b, 0, stream, args);
+}
+#endif
+
+#if GG_PART >= 18
+template <bool F16> void launch_short_wide(const KernelArgs &args, dim3 g, dim3 b, hipStream_t stream) {
+    launch_cross<F16, make_mode(kFwd, kIn16), kShapeShortWide>(args, g, b, stream);
 }
 #endif
 
@@ -113,6 +124,10 @@ template void launch_short<true, make_mode(kFwd, kIn16)>(const KernelArgs &, boo
 template void launch_short<false, make_mode(kDgrad, kIn16)>(const KernelArgs &, bool, dim3, dim3, hipStream_t);
 #elif GG_PART == 17
 template void launch_short<true, make_mode(kDgrad, kIn16)>(const KernelArgs &, bool, dim3, dim3, hipStream_t);
+#elif GG_PART == 18
+template void launch_short_wide<false>(const KernelArgs &, dim3, dim3, hipStream_t);
+#elif GG_PART == 19
+template void launch_short_wide<true>(const KernelArgs &, dim3, dim3, hipStream_t);
 #else
 #error "GG_PART out of range"
 #endif

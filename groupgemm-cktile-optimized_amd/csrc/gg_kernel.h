@@ -67,8 +67,10 @@ struct KernelArgs {
     const int64_t    *d_offs;      // [group_num + 1] first rows, or null for back-to-back groups
     int64_t           lens_rows;   // rows of the inputs: groups outside [0, lens_rows) are invalid
     TableHeader      *d_header;    // written by workgroup 0: tile count and the first bad group
-    int               tile_n;      // output columns per tile: kTileN, or kNarrowTileN (per-tile
-                                   // 16-bit forward plans of one round; n_tiles counts these)
+    int               tile_n;      // output columns per tile: kTileN, kNarrowTileN (per-tile
+                                   // 16-bit forward plans of one round) or kShortWideTileN
+                                   // (cross-tile 16-bit forward plans of short tiles); n_tiles
+                                   // counts these
     int               tile_m;      // output rows per tile: kTileM, or at most kShortTileM
                                    // (16-bit forward and dgrad plans whose groups keep their
                                    // M-tile counts; the group table counts these)
@@ -97,8 +99,9 @@ struct TileDesc {
 constexpr int kMaxDescPerWg = 64; // one per lane of a wave
 
 // Tile shapes of the forward kernel: 256 x 256; narrow 256 x 224 (per-tile, one-round plans);
-// short tile_m x 256 with tile_m <= kShortTileM (6 row blocks per wave).
-enum TileShape { kShapeWide = 0, kShapeNarrow = 1, kShapeShort = 2 };
+// short tile_m x 256 with tile_m <= kShortTileM (6 row blocks per wave); short-wide tile_m x 288
+// (6 row blocks and 9 column blocks per wave; cross-tile 16-bit forward plans).
+enum TileShape { kShapeWide = 0, kShapeNarrow = 1, kShapeShort = 2, kShapeShortWide = 3 };
 
 // Fewest K steps of a tile (or tail-split K range) in the cross-tile pipeline: its first step
 // plus the three whose DMAs prefetch the next tile.
@@ -115,6 +118,8 @@ void launch_mode(const KernelArgs &args, bool cross, dim3 g, dim3 b, hipStream_t
 // Short-tile instances (16-bit forward and dgrad; instance units of their own).
 template <bool F16, int MODE>
 void launch_short(const KernelArgs &args, bool cross, dim3 g, dim3 b, hipStream_t stream);
+// Short-wide instances (cross-tile 16-bit forward; instance units of their own).
+template <bool F16> void launch_short_wide(const KernelArgs &args, dim3 g, dim3 b, hipStream_t stream);
 // Modes with short-tile instances. (fp8 forward ran 6 % slower with them on config 5a's shapes.)
 constexpr bool has_short_tiles(int mode) {
     return mode == make_mode(kFwd, kIn16) || mode == make_mode(kDgrad, kIn16);

@@ -208,12 +208,17 @@ bool mode_supported(int mode, bool fp16) {
 hipError_t launch_grouped_gemm(const KernelArgs &args, bool fp16, int grid, hipStream_t stream, int mode) {
     if (!mode_supported(mode, fp16))
         return hipErrorInvalidValue;
-    // short tiles: forward and 16-bit dgrad plans with a host-built group table, never split
+    // short tiles: forward and 16-bit dgrad plans with a host-built group table, never split;
+    // short-wide tiles (288 columns): short cross-tile 16-bit forward plans without a tail split
+    const bool wide_n = args.tile_n == kShortWideTileN;
     if (args.tile_m != kTileM &&
         (args.tile_m <= 0 || args.tile_m > kShortTileM || args.tile_m % 16 != 0 || !has_short_tiles(mode) ||
-         args.d_lens != nullptr || args.d_total != nullptr || args.splits > 1 || args.tile_n != kTileN))
+         args.d_lens != nullptr || args.d_total != nullptr || args.splits > 1 ||
+         (args.tile_n != kTileN && !wide_n)))
         return hipErrorInvalidValue;
     const bool cross = uses_cross_tile(args, grid, mode);
+    if (wide_n && (args.tile_m == kTileM || mode != make_mode(kFwd, kIn16) || !cross || args.tail_splits > 1))
+        return hipErrorInvalidValue;
     const dim3 g(grid), b(kThreads);
 #define GG_CASE(L, F)                                                                          \
     case make_mode(L, F):                                                                      \

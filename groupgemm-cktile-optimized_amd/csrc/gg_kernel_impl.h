@@ -33,8 +33,12 @@
 //   * Short tiles (kShapeShort; 16-bit forward and dgrad): at most 192 x 256 (tile_m rows), each wave 6
 //     row blocks; the host picks them when every group keeps its M-tile count (520 rows: three
 //     tiles of 176 instead of 256 + 256 + 8).
+//   * Short-wide tiles (kShapeShortWide; cross-tile 16-bit forward): at most 192 x 288, each wave
+//     6 row blocks and 9 column blocks, on a slot plan of their own (PlanSW); the host picks them
+//     when they make fewer rounds (config 5a: 960 tiles instead of 1152).
 //
-// LDS (160 KB, all of it): A (x rows) 2 stages + B (w rows) 3 stages of 256 rows x 128 B.
+// LDS (160 KB, all of it): A (x rows) 2 stages + B (w rows) 3 stages of 256 rows x 128 B
+// (short-wide tiles: A stages of 192 rows, B stages of 288 rows, 156 KB).
 // Row r keeps its 16-byte chunk c at chunk position c ^ (r % 8): the eight lanes that a
 // ds_read_b128 serves together (8 consecutive rows, same chunk) hit eight different 16-byte
 // slots of a 128-byte window, which is conflict-free on gfx950.
@@ -182,6 +186,7 @@ constexpr int plan_epi(int mi, int idx) {
 template <int NA, int NB, int R = 8> struct Plan {
     static_assert(R == 8 || R == 6, "plans for 8 or 6 rows of MFMAs");
     static constexpr int rows = R, slots = 16, early = kEarlyA;
+    static constexpr int nc = 8, la = kLoads, lb = kLoads; // column blocks; A / B DMAs per wave
     static constexpr int last = R - 1; // the row that holds the step's barrier
     static constexpr int epi(int mi, int idx) { return plan_epi(mi, idx); }
     // R = 8: the w fragments of row 7 are read before the barrier, at MFMAs 1 .. 2 NB - 1.
@@ -340,6 +345,7 @@ static_assert(Plan<2, 2, 6>::vm_at_barrier() == 8 && Plan<2, 2>::vm_at_barrier()
 template <int NA, int NB> struct Plan8 {
     static_assert((NA == 2 || NA == 4) && (NB == 2 || NB == 4), "reads per fragment");
     static constexpr int rows = 8, last = 7, slots = 8, early = 1, bar = NA == 4 ? 4 : 5;
+    static constexpr int nc = 8, la = kLoads, lb = kLoads;
     static constexpr int read_a_next(int mi, int idx) {
         return (mi < 7 && idx % 2 == 1 && idx < 2 * NA) ? idx / 2 : -1;
     }
@@ -416,6 +422,122 @@ template <int NA, int NB> struct Plan8 {
 static_assert(Plan8<2, 2>::check() && Plan8<2, 4>::check() && Plan8<4, 4>::check(), "fp8 slot plans");
 static_assert(Plan8<2, 2>::vm_at_barrier() == 7, "fp8 forward plan unchanged");
 static_assert(Plan<2, 2>::bar == GG_BAR_IDX, "forward plan keeps the tuned barrier slot");
+
+// Slot plan of a short-wide tile (at most 192 rows x 288 columns, 16-bit forward, K-major
+// operands): 6 rows of 18 MFMAs per wave (9 column blocks, idx = kh * 9 + ni), A stages of 192
+// rows (6 DMAs per wave) and B stages of 288 rows (9 DMAs per wave).
+// - A(kt+1) DMAs 2-5 after MFMAs 0 and 10 of rows 0-1; B(kt+3) DMAs after MFMAs 0, 6 and 12 of
+//   rows 2-4; the barrier after MFMA 9 of row 5, then the early A(kt+2) DMAs 0-1 (after MFMAs 10
+//   and 12) and row 0 of the next step's x (after MFMAs 9 and 11).
+// - The x reads of row mi+1 follow MFMAs 1 and 3 of row mi; the 18 w reads of step kt+1 the odd
+//   MFMAs from 5 on of rows 0-4, spread evenly (4, 4, 3, 4, 3).
+// - First step of a cross tile: store s of the previous tile's row block mi+1 after MFMA 2, 4, 8,
+//   14, 16 of row mi (s = 0-3: the 8-row lines of the first 128 columns, 4: the ninth column
+//   block), none next to a DMA.
+struct PlanSW {
+    static constexpr int NA = 2, NB = 2; // K-major reads per fragment
+    static constexpr int rows = 6, last = 5, nc = 9, slots = 2 * nc, early = kEarlyA, bar = 9;
+    static constexpr int la = kShortTileM * kRowBytes / 1024 / kWaves;     // 6
+    static constexpr int lb = kShortWideTileN * kRowBytes / 1024 / kWaves; // 9
+    static constexpr int row0_first = bar;
+    static constexpr int epi(int mi, int idx) {
+        if (mi >= last)
+            return -1;
+        return idx == 2 ? 0 : idx == 4 ? 1 : idx == 8 ? 2 : idx == 14 ? 3 : idx == 16 ? 4 : -1;
+    }
+    static constexpr int read_a_next(int mi, int idx) {
+        return (mi < last && idx % 2 == 1 && idx < 2 * NA) ? idx / 2 : -1;
+    }
+    static constexpr int q_first(int mi) { return (mi * nc * NB + (rows - 2)) / (rows - 1); }
+    static constexpr int read_b_q(int mi, int idx) {
+        if (mi >= last || idx % 2 == 0 || idx < 2 * NA)
+            return -1;
+        const int q = q_first(mi) + (idx - 2 * NA) / 2;
+        return q < q_first(mi + 1) ? q : -1;
+    }
+    static constexpr int read_b_next(int mi, int idx) { return read_b_q(mi, idx) >= 0 ? read_b_q(mi, idx) % NB : -1; }
+    static constexpr int read_b_blk(int mi, int idx) { return read_b_q(mi, idx) >= 0 ? read_b_q(mi, idx) / NB : -1; }
+    static constexpr int read_a_row0(int mi, int idx) {
+        return (mi == last && idx % 2 == 1 && idx >= row0_first && idx < row0_first + 2 * NA)
+                   ? (idx - row0_first) / 2
+                   : -1;
+    }
+    static constexpr int load_a(int mi, int idx) {
+        const int j = early + 2 * mi + idx / 10;
+        return (mi < 2 && (idx == 0 || idx == 10) && j < la) ? j : -1;
+    }
+    static constexpr int load_b(int mi, int idx) {
+        return (mi >= 2 && mi < 5 && idx % 6 == 0) ? 3 * (mi - 2) + idx / 6 : -1;
+    }
+    static constexpr int load_a_early(int mi, int idx) {
+        const int j = (idx - (bar + 1)) / 2;
+        return (mi == last && idx > bar && idx % 2 == 0 && j < early) ? j : -1;
+    }
+    static constexpr int dma_kind(int mi, int idx) {
+        return load_a(mi, idx) >= 0 ? 1 : load_b(mi, idx) >= 0 ? 2 : load_a_early(mi, idx) >= 0 ? 3 : 0;
+    }
+    static constexpr int dma_j(int mi, int idx) {
+        return load_a(mi, idx) >= 0 ? load_a(mi, idx) : load_b(mi, idx) >= 0 ? load_b(mi, idx) : load_a_early(mi, idx);
+    }
+    static constexpr int vm_at_barrier() { // loads issued after A(kt+1)'s last DMA, as in Plan
+        int last_a = -1;
+        for (int p = 0; p < rows * slots; ++p)
+            if (load_a(p / slots, p % slots) >= 0)
+                last_a = p;
+        int n = 0;
+        for (int p = last_a + 1; p < last * slots + bar; ++p)
+            n += (load_b(p / slots, p % slots) >= 0) + (load_a_early(p / slots, p % slots) >= 0);
+        return n;
+    }
+    template <typename F> static constexpr int count(F f) {
+        int n = 0;
+        for (int p = 0; p < rows * slots; ++p)
+            n += f(p / slots, p % slots) >= 0;
+        return n;
+    }
+    static constexpr bool check() {
+        int per_block[nc] = {};
+        int per_row_epi[rows] = {};
+        for (int p = 0; p < rows * slots; ++p) {
+            const int mi = p / slots, idx = p % slots;
+            const int dmas  = (load_a(mi, idx) >= 0) + (load_b(mi, idx) >= 0) + (load_a_early(mi, idx) >= 0);
+            const int reads = (read_a_next(mi, idx) >= 0) + (read_b_next(mi, idx) >= 0) +
+                              (read_a_row0(mi, idx) >= 0);
+            const int stores = epi(mi, idx) >= 0;
+            if (dmas + reads + stores > 1)
+                return false;
+            if (mi == last && ((read_b_next(mi, idx) >= 0 && idx >= bar) || (read_a_row0(mi, idx) >= 0 && idx < bar)))
+                return false;
+            if (read_b_next(mi, idx) >= 0) {
+                const int b = read_b_blk(mi, idx);
+                if (b < 0 || b >= nc || read_b_next(mi, idx) != per_block[b])
+                    return false;
+                ++per_block[b];
+            }
+            if (stores) {
+                if (epi(mi, idx) != per_row_epi[mi])
+                    return false;
+                ++per_row_epi[mi];
+            }
+        }
+        for (int b = 0; b < nc; ++b)
+            if (per_block[b] != NB)
+                return false;
+        for (int r = 0; r < last; ++r)
+            if (per_row_epi[r] != 5)
+                return false;
+        for (int p = last * slots + bar; p < rows * slots; ++p)
+            if (load_a(p / slots, p % slots) >= 0)
+                return false;
+        return count(load_a) == la - early && count(load_b) == lb && count(load_a_early) == early &&
+               count(read_b_next) == nc * NB && count(read_a_next) == last * NA && count(read_a_row0) == NA &&
+               early + 2 * 2 == la;
+    }
+};
+static_assert(PlanSW::check() && PlanSW::vm_at_barrier() == 9 && PlanSW::la == 6 && PlanSW::lb == 9,
+              "short-wide slot plan");
+static_assert(2 * PlanSW::la * kWaves * 1024 + 3 * PlanSW::lb * kWaves * 1024 <= kLdsBytes,
+              "short-wide operand stages fit in LDS");
 
 // ---------------------------------------------------------------------------------------
 // Device primitives
@@ -639,6 +761,10 @@ constexpr bool kTailSkip = GG_TAIL_SKIP;
 // first 6 interleaved row blocks (tile rows up to 191); the MFMAs, x fragment reads and stores
 // of blocks 6 and 7 are compiled out and the memory schedule is unchanged: the A DMAs of rows
 // past tile_m fall outside the bounded resource (zeros, no traffic).
+// SHAPE kShapeShortWide (cross-tile 16-bit forward): tiles of args.tile_m <= 192 rows x 288. Each
+// wave takes 6 interleaved row blocks and 9 column blocks (columns 144 wn ..), on its own slot
+// plan (PlanSW) with A stages of 192 rows and B stages of 288 rows; the ninth column block is
+// stored on its own (16-byte lines) in the fused stores and as a second pass of the LDS epilogue.
 // TAIL (cross-tile 16-bit forward only): the plan cuts its last-round tiles into K ranges (tail
 // split: K ranges of last-round tiles store partial sums from epilogue_lds); instances without it
 // carry none of its state.
@@ -660,11 +786,14 @@ grouped_gemm_kernel(const KernelArgs args) {
     // is K-major, so that the valid rows of a partial tile split evenly between the wm = 0 and
     // wm = 1 waves; contiguous (128 wm + 16 mi ..) for the MN-major A of wgrad.
     constexpr bool NARROW = SHAPE == kShapeNarrow;
-    constexpr bool SHORT  = SHAPE == kShapeShort;
+    constexpr bool SWIDE  = SHAPE == kShapeShortWide;
+    constexpr bool SHORT  = SHAPE == kShapeShort || SWIDE; // at most 192 rows per tile
     static_assert(!NARROW || (!CROSS && MODE == make_mode(kFwd, kIn16)), "narrow tiles: per-tile 16-bit forward");
     static_assert(!SHORT || MODE == make_mode(kFwd, kIn16) || MODE == make_mode(kDgrad, kIn16),
                   "short tiles: 16-bit forward and dgrad");
-    constexpr int  TN     = NARROW ? kNarrowTileN : kTileN; // output columns per tile
+    static_assert(!SWIDE || (CROSS && !TAIL && MODE == make_mode(kFwd, kIn16)),
+                  "short-wide tiles: cross-tile 16-bit forward, no tail split");
+    constexpr int  TN     = NARROW ? kNarrowTileN : SWIDE ? kShortWideTileN : kTileN; // output columns per tile
     constexpr int  WCOLS  = TN / 2;                          // columns per wave (wn)
     constexpr int  NBLK   = WCOLS / 16;                      // column blocks per wave with MFMAs
     constexpr int  RB     = SHORT ? kShortTileM / 32 : 8;    // row blocks per wave with MFMAs
@@ -676,7 +805,14 @@ grouped_gemm_kernel(const KernelArgs args) {
     // the launch time whatever the partial ones save, and the per-tile instances stay smaller.
     constexpr bool kThin  = kTailSkip && CROSS;
     using P = std::conditional_t<F8, Plan8<reads_per_frag(A_MN), reads_per_frag(B_MN)>,
-                                 Plan<reads_per_frag(A_MN), reads_per_frag(B_MN), RB>>;
+                                 std::conditional_t<SWIDE, PlanSW, Plan<reads_per_frag(A_MN), reads_per_frag(B_MN), RB>>>;
+    static_assert(!SWIDE || (NBLK == P::nc && RB == P::rows), "short-wide plan");
+    constexpr int NC   = P::nc;                                     // column blocks in the registers
+    constexpr int A_ST = P::la * kWaves * 1024;                     // bytes of an A stage
+    constexpr int B_ST = P::lb * kWaves * 1024;                     // bytes of a B stage
+    constexpr int LV   = P::la > P::lb ? P::la : P::lb;             // DMA lane offsets per operand
+    constexpr int CSTR = SWIDE ? kShortWideTileN * 2 + 16 : kCStride; // staged C row stride
+    static_assert(kAStages * A_ST + kBStages * B_ST <= kLdsBytes && kShortTileM * CSTR <= kLdsBytes, "LDS");
     static_assert(!(F8 && F16), "fp8 writes bf16");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kLdsBytes];
     typedef __attribute__((address_space(3))) uint8_t lds_u8;
@@ -755,8 +891,8 @@ grouped_gemm_kernel(const KernelArgs args) {
     };
     // voff[0]: A's offsets; voff[1]: B's (the forward op shares A's: both row strides are K).
     constexpr bool kSameOff = LAYOUT == kFwd;
-    int            voff[kSameOff ? 1 : 2][kLoads];
-    sfor<0, kLoads>([&](auto j) {
+    int            voff[kSameOff ? 1 : 2][LV];
+    sfor<0, LV>([&](auto j) {
         voff[0][j] = dma_off(A_MN, j, args.lda);
         if constexpr (!kSameOff)
             voff[1][j] = dma_off(B_MN, j, args.ldb);
@@ -797,7 +933,7 @@ grouped_gemm_kernel(const KernelArgs args) {
     // Register epilogue: in store s = 2h + half of a 16-row block, lane l writes 16 bytes of
     // row 8 half + l%8 at column ecol + 64 h (see pack_pair).
     const int q    = lane >> 4;
-    const int ecol = wn * 128 + ((lane >> 3) & 1) * 32 + (q & 1) * 16 + (q >> 1) * 8;
+    const int ecol = wn * (SWIDE ? WCOLS : 128) + ((lane >> 3) & 1) * 32 + (q & 1) * 16 + (q >> 1) * 8;
     int       voffc = ((wm * (ILV ? 16 : 128) + (lane & 7)) * N + ecol) * 2;
     const int blk_stride = A_BLK * N * 2; // bytes between a wave's 16-row blocks of C
 
@@ -809,21 +945,21 @@ grouped_gemm_kernel(const KernelArgs args) {
     uint32_t a_dst[2], b_dst[3];     // this wave's DMA destination per logical stage
     auto set_stages = [&]() {
         sfor<0, 2>([&](auto L) {
-            const int p = ((L + rot_a) & 1) * kOpBytes;
+            const int p = ((L + rot_a) & 1) * A_ST;
             a_dst[L]    = lds0 + wave * 1024 + a_stage(0) + p;
             sfor<0, 2>([&](auto h) { a_rd[L][h] = frag_a[h] + a_stage(0) + p; });
         });
         sfor<0, 3>([&](auto L) {
             int s = L + rot_b;
             s     = s >= 3 ? s - 3 : s;
-            const int p = b_stage(0) + s * kOpBytes;
+            const int p = kAStages * A_ST + s * B_ST;
             b_dst[L]    = lds0 + wave * 1024 + p;
             sfor<0, 2>([&](auto h) { b_rd[L][h] = frag_b[h] + p; });
         });
     };
     // Re-materialise loop-invariant offsets at the top of every loop body (see fresh_v).
     auto refresh = [&]() {
-        sfor<0, kLoads>([&](auto j) {
+        sfor<0, LV>([&](auto j) {
             fresh_v(voff[0][j]);
             if constexpr (!kSameOff)
                 fresh_v(voff[1][j]);
@@ -873,9 +1009,9 @@ grouped_gemm_kernel(const KernelArgs args) {
         }
     };
 
-    f32x4 acc[8][8];
-    i32x4 fa[2][2];    // x fragments: row ring x k-half
-    i32x4 fb[2][8][2]; // w fragments: step parity x column block x k-half
+    f32x4 acc[8][NC];
+    i32x4 fa[2][2];     // x fragments: row ring x k-half
+    i32x4 fb[2][NC][2]; // w fragments: step parity x column block x k-half
 
     // One output tile: its DMA sources and where its C block goes.
     struct Tile {
@@ -1009,7 +1145,7 @@ grouped_gemm_kernel(const KernelArgs args) {
         }
         if constexpr (F8)
             tl.scale = to_const_space(args.x_scale)[0] * to_const_space(args.w_scale)[g];
-        tl.rows = __builtin_amdgcn_readfirstlane(active_rows(ILV, tl.m_valid, tl.n_valid, wm, wn));
+        tl.rows = __builtin_amdgcn_readfirstlane(active_rows(ILV, tl.m_valid, tl.n_valid, wm, wn, SWIDE ? WCOLS : 128));
         return tl;
     };
     auto c_rsrc = [&](const Tile &tl) {
@@ -1143,16 +1279,16 @@ grouped_gemm_kernel(const KernelArgs args) {
     // ---- prologue of a tile that starts cold: A(0), B(0..2), the first DMAs of A(1) ----------
     auto issue_prologue = [&]() {
         refresh();
-        sfor<0, kLoads>([&](auto j) { dma_now(a_dst[0], A_OP{}, j, 0); });
-        sfor<0, kLoads>([&](auto j) { dma_now(b_dst[0], B_OP{}, j, 0); });
-        sfor<0, kLoads>([&](auto j) { dma_now(b_dst[1], B_OP{}, j, 1); });
-        sfor<0, kLoads>([&](auto j) { dma_now(b_dst[2], B_OP{}, j, 2); });
+        sfor<0, P::la>([&](auto j) { dma_now(a_dst[0], A_OP{}, j, 0); });
+        sfor<0, P::lb>([&](auto j) { dma_now(b_dst[0], B_OP{}, j, 0); });
+        sfor<0, P::lb>([&](auto j) { dma_now(b_dst[1], B_OP{}, j, 1); });
+        sfor<0, P::lb>([&](auto j) { dma_now(b_dst[2], B_OP{}, j, 2); });
         sfor<0, P::early>([&](auto j) { dma_now(a_dst[1], A_OP{}, j, 1); });
     };
     // Then B(0) and A(0) row 0 into registers. VM: DMAs/stores issued after B(1)'s last.
     auto finish_prologue = [&]<int VM>() {
         wait_vm_lds_barrier<VM>(); // A(0), B(0), B(1) landed everywhere
-        sfor<0, 8>([&](auto ni) {
+        sfor<0, NC>([&](auto ni) {
             sfor<0, reads_per_frag(B_MN)>([&](auto r) {
                 read_frag.template operator()<B_MN, r>(fb[0][ni], b_rd[0], ni);
             });
@@ -1224,12 +1360,12 @@ grouped_gemm_kernel(const KernelArgs args) {
         int row = wm * (ILV ? 16 : 128) + (lane & 15);
         fresh_v(row);
         const int col = wn * WCOLS + (lane >> 4) * 4;
-        return row * kCStride + col * 2;
+        return row * CSTR + col * 2;
     };
     auto stage_block = [&](const Tile &tl, int off, auto mi, auto ni, f32x4 v) {
         if constexpr (F8)
             v *= tl.scale;
-        *reinterpret_cast<u32x2 *>(smem + off + mi * A_BLK * kCStride + ni * 16 * 2) = pack4<F16>(v);
+        *reinterpret_cast<u32x2 *>(smem + off + mi * A_BLK * CSTR + ni * 16 * 2) = pack4<F16>(v);
     };
     // Second half of the LDS epilogue: the staged tile to global memory.
     auto store_staged = [&](const Tile &tl) {
@@ -1237,18 +1373,32 @@ grouped_gemm_kernel(const KernelArgs args) {
         int row = wave * 64 + (lane >> 5);
         fresh_v(row);
         const int chunk = lane & 31;
-        const int loff  = row * kCStride + chunk * 16;
+        const int loff  = row * CSTR + chunk * 16;
         const int goff  = chunk * 8 < tl.n_valid ? (row * N + chunk * 8) * 2 : static_cast<int>(0x80000000u);
         const __amdgpu_buffer_rsrc_t crs = c_rsrc(tl);
         sfor<0, 2>([&](auto half) {
             i32x4 d[16];
-            sfor<0, 16>([&](auto i) { d[i] = lds_read(loff + (half * 16 + i) * 2 * kCStride); });
+            sfor<0, 16>([&](auto i) { d[i] = lds_read(loff + (half * 16 + i) * 2 * CSTR); });
             sfor<0, 16>([&](auto i) {
                 __builtin_amdgcn_raw_buffer_store_b128(
                     __builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, d[i]), crs,
                     goff + (half * 16 + i) * 2 * N * 2, 0, /*nt*/ 2);
             });
         });
+        if constexpr (SWIDE) {
+            // columns 256-287: four 16-byte chunks per row, 16 rows per store, rows 48 wave .. +48
+            int row2 = wave * 48 + (lane >> 2);
+            fresh_v(row2);
+            const int chunk2 = 32 + (lane & 3);
+            const int goff2  = chunk2 * 8 < tl.n_valid ? (row2 * N + chunk2 * 8) * 2 : static_cast<int>(0x80000000u);
+            i32x4     d2[3];
+            sfor<0, 3>([&](auto i) { d2[i] = lds_read((row2 + 16 * i) * CSTR + chunk2 * 16); });
+            sfor<0, 3>([&](auto i) {
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    __builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, d2[i]), crs,
+                    goff2 + 16 * i * N * 2, 0, /*nt*/ 2);
+            });
+        }
         wait_vm_lds_barrier<63>(); // every wave is done reading the staged C
     };
     // TAIL: a K range of a last-round tile leaves through here too, as fp32 partial sums (slab
@@ -1309,18 +1459,38 @@ grouped_gemm_kernel(const KernelArgs args) {
     __amdgpu_buffer_rsrc_t prev_crs = null_crs;
     int                    prev_n   = 0;
     u32x4                  pair[2];
-    // Store s (0-3) of the previous tile's row block r: packed with the next one for even s.
+    // Short-wide tiles: the ninth column block of row block r (columns 144 wn + 128 ..), lane l
+    // writing the 8 bytes it holds (row l%16, columns 4 (l/16) ..) of 16 rows x 32 bytes.
+    auto store_block9 = [&](auto r, const __amdgpu_buffer_rsrc_t &crs, int n_valid) {
+        asm volatile("" : "+a"(acc[r][NC - 1]));
+        f32x4 v = acc[r][NC - 1];
+        if constexpr (F8)
+            v *= prev_scale;
+        const int col = wn * WCOLS + 128 + (lane >> 4) * 4;
+        uint32_t  bs  = static_cast<uint32_t>(blk_stride);
+        fresh_s(bs);
+        const int vo = col < n_valid ? ((wm * 16 + (lane & 15)) * N + col) * 2 + r * static_cast<int>(bs)
+                                     : static_cast<int>(0x80000000u);
+        __builtin_amdgcn_raw_buffer_store_b64(pack4<F16>(v), crs, vo, 0, kStoreCpol);
+    };
+    // Store s (0-3) of the previous tile's row block r: packed with the next one for even s;
+    // s = 4 (short-wide tiles): the ninth column block.
+    constexpr int kEpiStores = SWIDE ? 5 : 4;
     auto epi_store = [&](auto r, auto s_) {
         sched_fence();
-        if constexpr (s_ % 2 == 0)
-            pack_pair(r, ic<s_ / 2>{}, pair[0], pair[1]);
-        store_line(pair[s_ % 2], r, s_, prev_crs, prev_n);
+        if constexpr (s_ == 4) {
+            store_block9(r, prev_crs, prev_n);
+        } else {
+            if constexpr (s_ % 2 == 0)
+                pack_pair(r, ic<s_ / 2>{}, pair[0], pair[1]);
+            store_line(pair[s_ % 2], r, s_, prev_crs, prev_n);
+        }
         sched_fence();
     };
     // MFMA idx of row mi of a K step (w register set SA; FIRST: the tile's first step, C = 0).
     auto row_mfma = [&]<int SA, bool FIRST>(auto mi_, auto idx_) {
         constexpr int mi = decltype(mi_)::value, idx = decltype(idx_)::value;
-        constexpr int kh = idx / 8, ni = idx % 8; // fp8: one MFMA per (mi, ni), kh = 0
+        constexpr int kh = idx / P::nc, ni = idx % P::nc; // fp8: one MFMA per (mi, ni), kh = 0
         if constexpr (ni >= NBLK || mi >= RB) {
             // narrow tiles: no 8th column block; short tiles: no row blocks 6 and 7
         } else if constexpr (F8) {
@@ -1461,13 +1631,13 @@ grouped_gemm_kernel(const KernelArgs args) {
     if constexpr (CROSS) {
         set_stages();
         issue_prologue();
-        finish_prologue.template operator()<kLoads + P::early>();
+        finish_prologue.template operator()<P::lb + P::early>();
     }
     while (true) {
         if constexpr (!CROSS) {
             set_stages();
             issue_prologue();
-            finish_prologue.template operator()<kLoads + P::early>();
+            finish_prologue.template operator()<P::lb + P::early>();
         }
         refresh();
         const int  t_next = t + gridDim.x;
@@ -1482,7 +1652,7 @@ grouped_gemm_kernel(const KernelArgs args) {
             // First step: stores the previous tile's accumulators while it overwrites them (to
             // nowhere for the first tile). Always the same code, so the accumulators never
             // merge across branches and stay in AGPRs.
-            sfor<0, 4>([&](auto s_) { epi_store(ic<0>{}, s_); });
+            sfor<0, kEpiStores>([&](auto s_) { epi_store(ic<0>{}, s_); });
             step.template operator()<0, 0, true, true, true>(0);
         } else {
             step.template operator()<0, 0, true, true, false>(0);
@@ -1540,7 +1710,7 @@ grouped_gemm_kernel(const KernelArgs args) {
                 rot_b    = rot_b >= 3 ? rot_b - 3 : rot_b;
                 set_stages();
                 if (T & 1) // the first step reads w set 0
-                    sfor<0, 8>([&](auto ni) { sfor<0, 2>([&](auto h) { fb[0][ni][h] = fb[1][ni][h]; }); });
+                    sfor<0, NC>([&](auto ni) { sfor<0, 2>([&](auto h) { fb[0][ni][h] = fb[1][ni][h]; }); });
                 if (LAYOUT == kWgrad || TAIL) // the next group's or K range's step count
                     T = __builtin_amdgcn_readfirstlane(cur.T);
                 continue;

@@ -36,6 +36,7 @@ constexpr int kTileK = 64;  // K per main-loop step: one 128-byte cache line per
 constexpr int kBand  = 4;   // M-tiles per band of the in-group order
 constexpr int kNarrowTileN = 224; // output columns of a narrow tile (one-round forward problems)
 constexpr int kShortTileM  = 192; // most output rows of a short tile (6 row blocks per wave)
+constexpr int kShortWideTileN = 288; // output columns of a short-wide tile (9 column blocks per wave)
 
 // Logical tile index of physical slot `t` (t = round * grid + workgroup).
 // Bijective on [0, total): every full round maps onto itself, and the last, partial round
@@ -68,15 +69,15 @@ GG_HD void band_coords(int local, int m_tiles, int n_tiles, int band, int *tm, i
 }
 
 // Partial tiles: the row blocks (bit mi) of wave (wm, wn) of the 2 x 2 wave grid that hold a
-// valid output in a tile of m_valid rows and n_valid columns; none when the wave's 128 columns
-// (128 wn ..) are all past n_valid. Row block mi of the wave is tile rows 16 (2 mi + wm) .. +16
-// when interleaved (ilv, a K-major A), 128 wm + 16 mi .. otherwise. The kernel skips the MFMAs of
-// the other row blocks (thin K steps).
-GG_HD uint32_t active_rows(bool ilv, int m_valid, int n_valid, int wm, int wn) {
+// valid output in a tile of m_valid rows and n_valid columns; none when the wave's wcols columns
+// (wcols wn ..: 128, or 144 in a short-wide tile) are all past n_valid. Row block mi of the wave
+// is tile rows 16 (2 mi + wm) .. +16 when interleaved (ilv, a K-major A), 128 wm + 16 mi ..
+// otherwise. The kernel skips the MFMAs of the other row blocks (thin K steps).
+GG_HD uint32_t active_rows(bool ilv, int m_valid, int n_valid, int wm, int wn, int wcols = 128) {
     const int nb_m = (m_valid + 15) >> 4; // 16-row blocks with a valid row
     int       ra   = ilv ? (nb_m - wm + 1) >> 1 : nb_m - 8 * wm;
     ra             = ra < 0 ? 0 : (ra > 8 ? 8 : ra);
-    return n_valid > 128 * wn ? (1u << ra) - 1 : 0u;
+    return n_valid > wcols * wn ? (1u << ra) - 1 : 0u;
 }
 
 // Ceil division for non-negative values.

@@ -42,8 +42,10 @@ def _run(pkg, x, w, gm, env, monkeypatch):
     else:
         monkeypatch.setenv("GG_SHORT", env)
     # bit-identity needs the same K order per output in both plans: no tail split (it sums the
-    # K ranges of other last-round tiles in the two tilings)
+    # K ranges of other last-round tiles in the two tilings); 256-column tiles (short-wide tiles
+    # are tests/test_gpu_short_wide.py's)
     monkeypatch.setenv("GG_TAIL_SPLIT", "0")
+    monkeypatch.setenv("GG_WIDE", "0")
     b, n, k = w.shape
     out = torch.full((x.shape[0], n), float("nan"), dtype=x.dtype, device=DEV)
     s = torch.cuda.current_stream(DEV).cuda_stream

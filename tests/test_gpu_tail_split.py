@@ -47,6 +47,7 @@ def _run_fwd(pkg, x, w, gm, monkeypatch, split):
         monkeypatch.delenv("GG_TAIL_SPLIT", raising=False)
     else:
         monkeypatch.setenv("GG_TAIL_SPLIT", split)
+    monkeypatch.setenv("GG_WIDE", "0")  # 256-column tiles (short-wide plans have no tail split)
     b, n, k = w.shape
     out = torch.full((x.shape[0], n), float("nan"), dtype=x.dtype, device=DEV)
     s = torch.cuda.current_stream(DEV).cuda_stream

@@ -9,7 +9,7 @@ NaN-prefilled, so an unwritten tile fails.
 
 Cases (forward through the backend, fp8 forward and dgrad through their plans):
 - 256 x 256 cross-tile bf16 with ragged and empty groups and a column tail;
-- config 5a's short tiles (176 rows) in fp16;
+- config 5a's short tiles (176 rows) in fp16, 256 and 288 columns wide;
 - a one-round per-tile plan with narrow tiles (256 x 224);
 - exactly 64 tiles per workgroup (the last descriptor lane), and 68 (no descriptors: the kernel
   walks the table itself), checked on sampled rows against float32;
@@ -26,15 +26,18 @@ if not torch.cuda.is_available():
 DEV = torch.device("cuda:0")
 ATOL = RTOL = 1e-2
 
-# dtype, group_m, N, K, tile shape expected in the plan
+# dtype, group_m, N, K, tile shape expected in the plan (short-wide tiles taken by the plan's model
+# unless GG_WIDE=0)
 FWD = [
     (torch.bfloat16, [700, 0, 1300, 256, 0, 2049, 513, 900] * 4, 2000, 576, "256x256x64"),
     (torch.float16, [520] * 32, 2880, 2880, "176x256x64"),
     (torch.bfloat16, [2048], 7168, 2048, "256x224x64"),
+    (torch.float16, [520] * 32, 2880, 2880, "176x288x64"),
 ]
 
 
-def _fwd(pkg, x, w, gm, desc, monkeypatch):
+def _fwd(pkg, x, w, gm, desc, monkeypatch, wide=False):
+    monkeypatch.setenv("GG_WIDE", "-1" if wide else "0")
     if desc:
         monkeypatch.delenv("GG_TILE_DESC", raising=False)
     else:
@@ -75,8 +78,9 @@ def test_forward_descriptors_match_walk(pkg, monkeypatch, case):
     g = torch.Generator(device=DEV).manual_seed(90 + case)
     x = torch.randn((sum(gm), k), generator=g, device=DEV).to(dt)
     w = torch.randn((len(gm), n, k), generator=g, device=DEV).to(dt)
-    with_desc, d1 = _fwd(pkg, x, w, gm, True, monkeypatch)
-    walk, d2 = _fwd(pkg, x, w, gm, False, monkeypatch)
+    wide = "x288x" in shape
+    with_desc, d1 = _fwd(pkg, x, w, gm, True, monkeypatch, wide)
+    walk, d2 = _fwd(pkg, x, w, gm, False, monkeypatch, wide)
     assert shape in d1 and d1 == d2, (d1, d2)
     assert torch.equal(with_desc.view(torch.int16), walk.view(torch.int16)), d1
     _check_rows(x, w, gm, with_desc)
