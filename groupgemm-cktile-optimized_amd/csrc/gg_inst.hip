@@ -87,6 +87,19 @@ template <bool F16> void launch_short_wide(const KernelArgs &args, dim3 g, dim3 
 }
 #endif
 
+#if GG_STAMPS
+// Instrumented builds: this unit's cycle stamps (its own g_stamps) to the host, and cleared.
+#define GG_STAMP_CAT2(a, b) a##b
+#define GG_STAMP_CAT(a, b) GG_STAMP_CAT2(a, b)
+extern "C" int GG_STAMP_CAT(gg_stamps_read_p, GG_PART)(unsigned long long *dst) {
+    return static_cast<int>(hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_stamps), sizeof(g_stamps)));
+}
+extern "C" int GG_STAMP_CAT(gg_stamps_clear_p, GG_PART)() {
+    static unsigned long long zeros[kStampWgs * kStampSlots];
+    return static_cast<int>(hipMemcpyToSymbol(HIP_SYMBOL(g_stamps), zeros, sizeof(zeros)));
+}
+#endif
+
 // part -> (fp16 MFMA, mode); the dispatch's switch in gg_kernel.hip covers the same 14 pairs
 #if GG_PART == 0
 template void launch_mode<false, make_mode(kFwd, kIn16)>(const KernelArgs &, bool, dim3, dim3, hipStream_t);

@@ -740,6 +740,30 @@ __device__ __forceinline__ LaneGroup lane_group_table(const int64_t *lens, const
     return lg;
 }
 
+// Cycle stamps (instrumented builds only: `make stamps` compiles the library into lib_stamps/ with
+// GG_STAMPS=1; stamps.py reads them). Lane 0 of wave 0 of workgroup w writes the shader clock
+// (s_memtime) into slot i of g_stamps[w * kStampSlots ..] with a vector store: 0 kernel start,
+// 1 after the prologue, 2 + 5 j .. 6 + 5 j for the workgroup's tile j < 7 (before its first K
+// step, after it, after the unchecked steps, after locating the next tile, after the last step),
+// 62 before the final LDS epilogue (cross-tile), 63 kernel end. The stores count in vmcnt and only make the hand-placed waits longer.
+#ifndef GG_STAMPS
+#define GG_STAMPS 0
+#endif
+constexpr int kStampSlots = 64, kStampWgs = 1024;
+#if GG_STAMPS
+__device__ unsigned long long g_stamps[kStampWgs * kStampSlots];
+#define GG_STAMP(i)                                                                                   \
+    do {                                                                                              \
+        const unsigned long long t_stamp_ = __builtin_readcyclecounter();                             \
+        if (threadIdx.x == 0 && (i) < kStampSlots && blockIdx.x < kStampWgs)                          \
+            g_stamps[blockIdx.x * kStampSlots + (i)] = t_stamp_;                                      \
+    } while (0)
+#else
+#define GG_STAMP(i) \
+    do {            \
+    } while (0)
+#endif
+
 // Partial tiles: a wave skips the MFMAs of its 16-row blocks that hold no valid output (1), or
 // computes every block (0).
 #ifndef GG_TAIL_SKIP
@@ -1159,6 +1183,8 @@ grouped_gemm_kernel(const KernelArgs args) {
     int t = blockIdx.x;
     if (t >= total_units)
         return;
+    GG_STAMP(0);
+    [[maybe_unused]] int stamp_tile = 0; // GG_STAMPS: tiles of this workgroup so far
     int  tile_i = 0; // this workgroup's tile count so far (unit t = blockIdx.x + tile_i * grid)
     Tile cur = make_tile(t, 0), nxt = cur;
     if (!CROSS || LAYOUT == kWgrad || TAIL)
@@ -1632,6 +1658,7 @@ grouped_gemm_kernel(const KernelArgs args) {
         set_stages();
         issue_prologue();
         finish_prologue.template operator()<P::lb + P::early>();
+        GG_STAMP(1);
     }
     while (true) {
         if constexpr (!CROSS) {
@@ -1642,6 +1669,11 @@ grouped_gemm_kernel(const KernelArgs args) {
         refresh();
         const int  t_next = t + gridDim.x;
         const bool more   = t_next < total_units;
+#if GG_STAMPS
+        const int stamp_base = stamp_tile < 7 ? 2 + 5 * stamp_tile : kStampSlots;
+        ++stamp_tile;
+#endif
+        GG_STAMP(stamp_base);
         // A partial tile in which this wave has at most 4 row blocks with a valid output (kThin)
         // runs its steps after the first as thin steps (step_thin) in a loop of their own; a
         // full tile never enters it. (A thin step's memory operations do not overlap its MFMAs:
@@ -1657,6 +1689,7 @@ grouped_gemm_kernel(const KernelArgs args) {
         } else {
             step.template operator()<0, 0, true, true, false>(0);
         }
+        GG_STAMP(stamp_base + 1);
         int kt = 1; // kt % 6 == 1 at the top of each block of six steps
         if constexpr (A_MN || B_MN)
             set_mn_offsets(cur);
@@ -1670,9 +1703,11 @@ grouped_gemm_kernel(const KernelArgs args) {
             step.template operator()<1, 2, false, false, false>(kt + 4);
             step.template operator()<0, 0, false, false, false>(kt + 5);
         }
+        GG_STAMP(stamp_base + 2);
         cross_next = CROSS && more;
         if (cross_next)
             nxt = make_tile(t_next, tile_i + 1);
+        GG_STAMP(stamp_base + 3);
         for (; !thin && kt < T; kt += 6) { // with CROSS the last three steps prefetch `nxt`
             refresh();
             step.template operator()<1, 1, false, true, false>(kt);
@@ -1693,6 +1728,7 @@ grouped_gemm_kernel(const KernelArgs args) {
                 if (kt + 5 < T) step_thin.template operator()<0, 0>(kt + 5);
             }
         }
+        GG_STAMP(stamp_base + 4);
         if constexpr (CROSS) {
             if (!cross_next)
                 break; // last tile of the workgroup: stored after the loop
@@ -1724,8 +1760,10 @@ grouped_gemm_kernel(const KernelArgs args) {
                 store_partial(t);
             else
                 epilogue_lds(cur);
-            if (!more)
+            if (!more) {
+                GG_STAMP(kStampSlots - 1);
                 return;
+            }
             t   = t_next;
             ++tile_i;
             cur = make_tile(t, tile_i);
@@ -1733,8 +1771,10 @@ grouped_gemm_kernel(const KernelArgs args) {
         }
     }
     if constexpr (CROSS) {
+        GG_STAMP(kStampSlots - 2);
         epilogue_lds(cur); // TAIL: a K range's partial sums instead of its C tile
     }
+    GG_STAMP(kStampSlots - 1);
 }
 
 } // namespace

@@ -1,0 +1,181 @@
+"""Where a cross-tile launch spends its cycles: the kernel's s_memtime stamps, per workgroup and tile.
+
+Needs the instrumented library (GG_STAMPS=1 in csrc/gg_kernel_impl.h), built on the CPU with
+
+    make -C groupgemm-cktile-optimized_amd -j16 stamps      # -> lib_stamps/libgg_mi355x.so
+
+and runs on the GPU box from the repository root:
+
+    python3 groupgemm-cktile-optimized_amd/stamps.py [--shapes '[[b, m, n, k], ...]'] [--fp16]
+        [--json gpurun_out/stamps.json]
+
+Per shape (balanced groups of m rows, 16-bit forward through the mi355x backend): 10 warm
+launches, then one launch whose stamps are read back. Lane 0 of wave 0 of every workgroup stamps
+the shader clock at kernel start, after the prologue, and for each of its first 7 tiles before
+its first K step, after it, after the unchecked K steps, after locating the next tile and after
+the tile's last K step, before the final LDS epilogue and at kernel end. The shader clocks of
+different CUs are not synchronised (they differ by millions of cycles, also within an XCD), so
+only differences of one workgroup's own stamps are used. Printed, averaged over workgroups
+(cycles):
+  - the launch per workgroup (start to end), the prologue and the final LDS epilogue;
+  - per tile: the first K step (which also stores the previous tile's C from registers), the
+    unchecked steps (and their cost per step), the next tile's lookup, the checked steps (the
+    last ones, whose DMAs fetch the next tile), and the gap to the next tile's first step;
+  - the tile's cost beyond its K steps at the unchecked rate ("boundary").
+The stamps' own stores count in vmcnt, so an instrumented launch is a little slower than a plain
+one; the stamped launch also follows a pause (the host clears the stamps), so its clock and
+memory state differ from back-to-back launches, and a shape's first launches in a process run
+slower than later ones. Compare segments of one launch, and shapes run in the same order.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import importlib.util
+import json
+import os
+import sys
+
+import numpy as np
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+STAMP_LIB = os.path.join(PKG_DIR, "lib_stamps", "libgg_mi355x.so")
+SLOTS, WGS, PARTS = 64, 1024, 20
+
+
+def load_package():
+    spec = importlib.util.spec_from_file_location("gg_stamps_pkg", os.path.join(PKG_DIR, "__init__.py"),
+                                                  submodule_search_locations=[PKG_DIR])
+    pkg = importlib.util.module_from_spec(spec)
+    sys.modules["gg_stamps_pkg"] = pkg
+    spec.loader.exec_module(pkg)
+    if not os.path.exists(STAMP_LIB):
+        raise SystemExit(f"{STAMP_LIB} missing: build it with `make -C {PKG_DIR} -j16 stamps`")
+    lib = pkg.load_library(STAMP_LIB)
+    return pkg, lib
+
+
+def part_fns(lib):
+    fns = []
+    for p in range(PARTS):
+        rd = getattr(lib, f"gg_stamps_read_p{p}", None)
+        clr = getattr(lib, f"gg_stamps_clear_p{p}", None)
+        if rd is None or clr is None:
+            raise SystemExit("the library has no stamp functions: it is not the GG_STAMPS build")
+        rd.argtypes = [ctypes.c_void_p]
+        fns.append((rd, clr))
+    return fns
+
+
+def unchecked_steps(T: int) -> int:
+    """K steps the kernel's unchecked loop runs (kt = 1, 7, ... while kt + 9 < T, six per pass)."""
+    passes = max(0, (T - 10 + 5) // 6)
+    return 6 * passes
+
+
+def analyse(st: np.ndarray, T: int) -> dict:
+    """st: [grid, 64] stamps of one launch (int64)."""
+    grid = st.shape[0]
+    total = st[:, 63] - st[:, 0]
+    tiles = np.array([int(sum(1 for j in range(7) if st[w, 2 + 5 * j] > 0)) for w in range(grid)])
+    nun = unchecked_steps(T)
+    seg = {"first step": [], "unchecked": [], "next tile lookup": [], "checked": [], "gap to next tile": []}
+    for w in range(grid):
+        for j in range(tiles[w]):
+            s = st[w, 2 + 5 * j: 7 + 5 * j]
+            seg["first step"].append(s[1] - s[0])
+            seg["unchecked"].append(s[2] - s[1])
+            seg["next tile lookup"].append(s[3] - s[2])
+            seg["checked"].append(s[4] - s[3])
+            if j + 1 < tiles[w]:
+                seg["gap to next tile"].append(st[w, 2 + 5 * (j + 1)] - s[4])
+    out = {
+        "grid": grid, "k_steps": T, "unchecked_steps_per_tile": nun,
+        "launch_cycles_mean": float(total.mean()), "launch_cycles_max": float(total.max()),
+        "tiles_per_wg_max": int(tiles.max()),
+        "prologue": float((st[:, 1] - st[:, 0]).mean()),
+        "final_epilogue": float((st[:, 63] - st[:, 62]).mean()) if (st[:, 62] > 0).all() else float("nan"),
+    }
+    for k, v in seg.items():
+        out[k] = float(np.mean(v)) if v else 0.0
+    per_step = out["unchecked"] / nun if nun else float("nan")
+    out["unchecked_per_step"] = per_step
+    if nun:
+        tile = out["first step"] + out["unchecked"] + out["next tile lookup"] + out["checked"] + out["gap to next tile"]
+        out["tile_cycles"] = tile
+        out["boundary"] = tile - T * per_step
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--shapes", default="[[8, 4096, 7168, 2048], [32, 520, 2880, 2880], [8, 4096, 4096, 7168]]")
+    ap.add_argument("--fp16", action="store_true")
+    ap.add_argument("--json", default="")
+    args = ap.parse_args()
+    import torch
+
+    pkg, lib = load_package()
+    fns = part_fns(lib)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    sh = torch.cuda.current_stream(dev).cuda_stream
+    dt = pkg.DType.FP16 if args.fp16 else pkg.DType.BF16
+    tdt = torch.float16 if args.fp16 else torch.bfloat16
+    results = []
+    for b, m, n, k in json.loads(args.shapes):
+        print(f"[stamps] shape {b} x {m} x {n} x {k}", flush=True)
+        x = torch.empty((b * m, k), dtype=tdt, device=dev)
+        w = torch.empty((b, n, k), dtype=tdt, device=dev)
+        out = torch.zeros((b * m, n), dtype=tdt, device=dev)
+        pkg.fill_randn(dt, x.data_ptr(), x.numel(), 1, sh)
+        pkg.fill_randn(dt, w.data_ptr(), w.numel(), 2, sh)
+        be = pkg.make_mi355x_backend()
+        why = be.prepare(pkg.GroupedGemmProblem(dt, b, n, k, [m] * b, x.data_ptr(), w.data_ptr(), out.data_ptr()), sh)
+        if why:
+            raise SystemExit(f"prepare: {why}")
+        detail = be.detail()
+        for _ in range(10):
+            be.run(sh)
+        torch.cuda.synchronize()
+        for _, clr in fns:
+            if clr() != 0:
+                raise SystemExit("stamp clear failed")
+        be.run(sh)
+        torch.cuda.synchronize()
+        grid = be.grid()
+        best = None
+        for rd, _ in fns:
+            buf = np.zeros(WGS * SLOTS, dtype=np.uint64)
+            if rd(buf.ctypes.data) != 0:
+                raise SystemExit("stamp read failed")
+            st = buf.reshape(WGS, SLOTS)[:grid].astype(np.int64)
+            if (st[:, 0] > 0).all() and (st[:, 63] > 0).all():
+                best = st
+                break
+        be.release()
+        del x, w, out
+        if best is None:
+            print(f"  {detail}: no part holds a complete set of stamps (per-tile plan?)", flush=True)
+            continue
+        r = analyse(best, -(-k // 64))
+        r.update({"shape": [b, m, n, k], "plan": detail, "stamps": best.tolist()})
+        results.append(r)
+        print(f"  {detail}", flush=True)
+        print(f"  launch per workgroup: mean {r['launch_cycles_mean']:.0f}, max {r['launch_cycles_max']:.0f} cycles; "
+              f"{r['tiles_per_wg_max']} tiles stamped (a workgroup's first 7 at most), {r['k_steps']} K steps each", flush=True)
+        print(f"  prologue {r['prologue']:.0f}; final epilogue {r['final_epilogue']:.0f}", flush=True)
+        print(f"  per tile: first step {r['first step']:.0f} | unchecked {r['unchecked']:.0f} "
+              f"({r['unchecked_steps_per_tile']} steps, {r['unchecked_per_step']:.0f} each) | next-tile lookup "
+              f"{r['next tile lookup']:.0f} | checked {r['checked']:.0f} | gap {r['gap to next tile']:.0f}", flush=True)
+        if "boundary" in r:
+            print(f"  tile {r['tile_cycles']:.0f} cycles, of which {r['boundary']:.0f} beyond its K steps at the "
+                  f"unchecked rate", flush=True)
+    if args.json:
+        os.makedirs(os.path.dirname(os.path.abspath(args.json)), exist_ok=True)
+        with open(args.json, "w") as f:
+            json.dump(results, f, indent=1)
+
+
+if __name__ == "__main__":
+    main()

@@ -5,6 +5,7 @@
 - Accumulator reads after an inline-asm MFMA (csrc/check_mfma_acc_hazard.py): caught within 19
   wait states, across a fall-through and a loop's back edge; reads of other AGPRs pass; SGPR
   spill traffic in a K-loop block (many MFMAs) fails, in a single step's block it does not.
+- The product library carries no cycle stamps (those are the `make stamps` build's).
 """
 import importlib.util
 import os
@@ -152,3 +153,15 @@ def test_spill_traffic_in_the_k_loop_is_flagged():
     assert len(spills) == 1
     _, spills = _acc(".LBB0_3:\n    v_readlane_b32 s4, v185, 12\n" + "\n".join([mfma] * 16))
     assert not spills  # a single step's block (first or checked steps) may reload
+
+
+def test_product_library_has_no_cycle_stamps():
+    """The cycle stamps (GG_STAMPS) are compiled only into lib_stamps/ (`make stamps`): the product
+    library exports none of their read-back functions."""
+    import ctypes
+    import pytest
+    path = os.path.join(ROOT, "groupgemm-cktile-optimized_amd", "lib", "libgg_mi355x.so")
+    if not os.path.exists(path):
+        pytest.skip("library not built")
+    lib = ctypes.CDLL(path)
+    assert not hasattr(lib, "gg_stamps_read_p0") and not hasattr(lib, "gg_stamps_clear_p18")
