@@ -17,6 +17,7 @@ Cases:
 - N = 440: the last N-tile's wn = 1 waves hold 8 valid columns (their first block);
 - N = 2000, two tiles per workgroup: the last N-tile's ninth block of the wn = 1 waves is past N,
   through the fused stores of the next tile's first step;
+- fp16 with K % 64 = 8 and three tile heights' worth of groups (520, 264 and 17 rows);
 - a one-round plan stays on 256-column tiles even when forced (short-wide tiles need the
   cross-tile variant).
 """
@@ -38,6 +39,7 @@ CASES = [
     (torch.bfloat16, [100, 7, 1, 64, 112, 33, 180, 0] * 12, 1000, 1096, True, 192),
     (torch.bfloat16, [300, 520, 0, 176, 1] * 20, 440, 640, True, 176),
     (torch.bfloat16, [520] * 24, 2000, 512, True, 176),
+    (torch.float16, [520, 264, 17] * 30, 1152, 712, True, 176),
 ]
 
 
