@@ -7,9 +7,10 @@ Needs the instrumented library (GG_STAMPS=1 in csrc/gg_kernel_impl.h), built on 
 and runs on the GPU box from the repository root:
 
     python3 groupgemm-cktile-optimized_amd/stamps.py [--shapes '[[b, m, n, k], ...]'] [--fp16]
-        [--json gpurun_out/stamps.json]
+        [--op fwd|dgrad|wgrad|fp8_e4m3|fp8_e5m2|dgrad_fp8|wgrad_fp8] [--json gpurun_out/stamps.json]
 
-Per shape (balanced groups of m rows, 16-bit forward through the mi355x backend): 10 warm
+Per shape (balanced groups of m rows in forward terms: x [b m, k], w [b, n, k]; 16-bit forward
+through the mi355x backend, or the pass --op names, planned as bench.py plans it): 10 warm
 launches, then one launch whose stamps are read back. Lane 0 of wave 0 of every workgroup stamps
 the shader clock at kernel start, after the prologue, and for each of its first 7 tiles before
 its first K step, after it, after the unchecked K steps, after locating the next tile and after
@@ -111,6 +112,8 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--shapes", default="[[8, 4096, 7168, 2048], [32, 520, 2880, 2880], [8, 4096, 4096, 7168]]")
     ap.add_argument("--fp16", action="store_true")
+    ap.add_argument("--op", default="fwd",
+                    choices=["fwd", "dgrad", "wgrad", "fp8_e4m3", "fp8_e5m2", "dgrad_fp8", "wgrad_fp8"])
     ap.add_argument("--json", default="")
     args = ap.parse_args()
     import torch
@@ -124,16 +127,27 @@ def main():
     tdt = torch.float16 if args.fp16 else torch.bfloat16
     results = []
     for b, m, n, k in json.loads(args.shapes):
-        print(f"[stamps] shape {b} x {m} x {n} x {k}", flush=True)
-        x = torch.empty((b * m, k), dtype=tdt, device=dev)
-        w = torch.empty((b, n, k), dtype=tdt, device=dev)
-        out = torch.zeros((b * m, n), dtype=tdt, device=dev)
-        pkg.fill_randn(dt, x.data_ptr(), x.numel(), 1, sh)
-        pkg.fill_randn(dt, w.data_ptr(), w.numel(), 2, sh)
-        be = pkg.make_mi355x_backend()
-        why = be.prepare(pkg.GroupedGemmProblem(dt, b, n, k, [m] * b, x.data_ptr(), w.data_ptr(), out.data_ptr()), sh)
-        if why:
-            raise SystemExit(f"prepare: {why}")
+        print(f"[stamps] {args.op} shape {b} x {m} x {n} x {k}", flush=True)
+        keep = None
+        if args.op == "fwd":
+            x = torch.empty((b * m, k), dtype=tdt, device=dev)
+            w = torch.empty((b, n, k), dtype=tdt, device=dev)
+            out = torch.zeros((b * m, n), dtype=tdt, device=dev)
+            pkg.fill_randn(dt, x.data_ptr(), x.numel(), 1, sh)
+            pkg.fill_randn(dt, w.data_ptr(), w.numel(), 2, sh)
+            keep = (x, w, out)
+            be = pkg.make_mi355x_backend()
+            why = be.prepare(pkg.GroupedGemmProblem(dt, b, n, k, [m] * b, x.data_ptr(), w.data_ptr(),
+                                                    out.data_ptr()), sh)
+            if why:
+                raise SystemExit(f"prepare: {why}")
+            grid_of = be.grid
+        else:
+            sys.path.insert(0, os.path.dirname(PKG_DIR))
+            import bench  # the other passes' plans and inputs, as the benchmark makes them
+
+            be, _, keep = bench.other_pass(pkg, args.op, 1 if args.fp16 else 0, b, m, n, k, sh, dev)
+            grid_of = lambda: lib.gg_plan_grid(be._plan)  # noqa: E731
         detail = be.detail()
         for _ in range(10):
             be.run(sh)
@@ -143,7 +157,7 @@ def main():
                 raise SystemExit("stamp clear failed")
         be.run(sh)
         torch.cuda.synchronize()
-        grid = be.grid()
+        grid = grid_of()
         best = None
         for rd, _ in fns:
             buf = np.zeros(WGS * SLOTS, dtype=np.uint64)
@@ -154,11 +168,12 @@ def main():
                 best = st
                 break
         be.release()
-        del x, w, out
+        del keep
         if best is None:
             print(f"  {detail}: no part holds a complete set of stamps (per-tile plan?)", flush=True)
             continue
-        r = analyse(best, -(-k // 64))
+        contraction = {"dgrad": n, "wgrad": m}.get(args.op.split("_")[0], k)
+        r = analyse(best, -(-contraction // (128 if "fp8" in args.op else 64)))
         r.update({"shape": [b, m, n, k], "plan": detail, "stamps": best.tolist()})
         results.append(r)
         print(f"  {detail}", flush=True)
