@@ -557,7 +557,8 @@ int plan_device_lens(gg_plan *plan, bool noalloc, int op, int a_dtype, int b_dty
     if (op == GG_OP_DGRAD && (n + steps) * k * es >= lim)
         return fail(GG_ERR_UNSUPPORTED, "one group's w must be smaller than 2 GiB");
     // wgrad: a group may hold every row
-    if (op == GG_OP_WGRAD && ((total_m + steps) * n * es >= lim || (total_m + steps) * k * es >= lim))
+    const int64_t wg_rows = std::max<int64_t>(total_m, gg::kCrossMinStepsHost * steps) + steps;
+    if (op == GG_OP_WGRAD && (wg_rows * n * es >= lim || wg_rows * k * es >= lim))
         return fail(GG_ERR_UNSUPPORTED, "grad_out and x rows must be smaller than 2 GiB");
     const int64_t n_tiles = gg::cdiv(n_out, gg::kTileN);
     // wgrad: output tiles do not depend on the sizes, m_out rows per group
@@ -638,9 +639,10 @@ int plan_device_lens(gg_plan *plan, bool noalloc, int op, int a_dtype, int b_dty
         ka.ldb = static_cast<int>(k);
     }
     if (op == GG_OP_WGRAD) {
-        // The K-step counts depend on the sizes, so the per-tile variant runs (min_steps = 0).
+        // The K-step counts depend on the sizes; a cross-tile wgrad tile runs at least
+        // kCrossMinStepsHost of them (zeros past its group's rows), so the cross-tile variant runs.
         ka.m_out          = static_cast<int>(n);
-        ka.min_steps      = 0;
+        ka.min_steps      = gg::kCrossMinStepsHost;
         plan->total_tiles = static_cast<int>(wgrad_tiles);
         plan->grid        = static_cast<int>(std::min<int64_t>(cus, wgrad_tiles));
         ka.total_tiles    = plan->total_tiles;
@@ -899,7 +901,9 @@ static int prepare_backward(int layout, int dtype_a, int dtype_b, int group_num,
     const int64_t steps = f8 ? 128 : gg::kTileK; // contraction rows per K step
     if (dgrad && (n + steps) * k * es >= lim)
         return fail(GG_ERR_UNSUPPORTED, "one group's w must be smaller than 2 GiB");
-    if (!dgrad && ((max_m + steps) * n * es >= lim || (max_m + steps) * k * es >= lim))
+    // (wgrad: a short group's tile addresses kCrossMinStepsHost steps)
+    const int64_t rows_addr = std::max<int64_t>(max_m, gg::kCrossMinStepsHost * steps) + steps;
+    if (!dgrad && (rows_addr * n * es >= lim || rows_addr * k * es >= lim))
         return fail(GG_ERR_UNSUPPORTED, "one group's rows of grad_out and x must be smaller than 2 GiB");
 
     auto *plan = new (std::nothrow) gg_plan;
@@ -958,22 +962,19 @@ static int prepare_backward(int layout, int dtype_a, int dtype_b, int group_num,
         ka.ldb             = static_cast<int>(k);
         ka.m_out           = dgrad ? 0 : static_cast<int>(n);
         ka.k_tiles         = dgrad ? static_cast<int>(gg::cdiv(n, steps)) : 1;
-        if (!dgrad) { // fewest K steps of a group: the cross-tile variant needs every group's
-            int64_t mn = max_m;
-            for (int g = 0; g < group_num; ++g)
-                mn = std::min(mn, group_m[g]);
-            ka.min_steps = static_cast<int>(gg::cdiv(mn, steps));
-        }
+        if (!dgrad) // fewest K steps of a tile: a cross-tile wgrad tile runs at least
+                    // kCrossMinStepsHost (zeros past a short or empty group's rows)
+            ka.min_steps = gg::kCrossMinStepsHost;
         ka.x_scale         = f8 ? a_scale : nullptr;
         ka.w_scale         = f8 ? b_scale : nullptr;
         // tails (see KernelArgs). dgrad: the contraction n and w's columns k. wgrad: every group's
         // rows (its contraction) and the columns of grad_out (n) and x (k).
         if (dgrad) {
             ka.tails = n % steps != 0 || k % gg::kTileN != 0;
-        } else {
+        } else { // and the zero steps of a group shorter than kCrossMinStepsHost steps
             bool t = n % gg::kTileN != 0 || k % gg::kTileN != 0;
             for (int g = 0; g < group_num; ++g)
-                t = t || group_m[g] % steps != 0;
+                t = t || group_m[g] % steps != 0 || group_m[g] < gg::kCrossMinStepsHost * steps;
             ka.tails = t;
         }
         // wgrad's K steps differ per group: no split

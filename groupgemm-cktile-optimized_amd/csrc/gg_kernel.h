@@ -53,7 +53,8 @@ struct KernelArgs {
     int               band;        // M-tiles per band of the in-group tile order
     int               lda, ldb;    // row strides (elements) of the A and B storage
     int               m_out;       // wgrad: output rows per group (0 otherwise)
-    int               min_steps;   // wgrad: fewest K steps of any group (0 with an empty group)
+    int               min_steps;   // wgrad: fewest K steps of a tile (kCrossMinStepsHost: a
+                                   // cross-tile wgrad tile of a shorter group runs zero steps)
     const float      *x_scale;     // fp8: device scale of the A operand (1 value)
     const float      *w_scale;     // fp8: device scale of each group's B operand (group_num values)
     const int        *d_total;     // device tile count (device-resident group sizes), or null:

@@ -1148,7 +1148,10 @@ grouped_gemm_kernel(const KernelArgs args) {
             tl.o0b     = static_cast<int>(col0);
             tl.c_ptr   = static_cast<uint16_t *>(args.out) +
                        (static_cast<int64_t>(g) * args.m_out + o0a) * N + col0;
-            tl.T     = max(1, static_cast<int>(cdiv(ge.m, KS)));
+            // at least the cross-tile pipeline's kCrossMinSteps: the steps past the group's rows
+            // read zeros (rows past ge.m fall outside rsrc_a / rsrc_b), so a short or empty group
+            // costs a few zero steps instead of the whole launch's cross-tile variant
+            tl.T     = max(CROSS ? kCrossMinSteps : 1, static_cast<int>(cdiv(ge.m, KS)));
             tl.k0    = 0;
             tl.klast = 1;
         } else {
