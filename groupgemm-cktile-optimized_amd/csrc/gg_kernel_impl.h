@@ -1696,8 +1696,10 @@ grouped_gemm_kernel(const KernelArgs args) {
         int kt = 1; // kt % 6 == 1 at the top of each block of six steps
         if constexpr (A_MN || B_MN)
             set_mn_offsets(cur);
-        // Unchecked: every prefetch of the block (up to kt + 8) is a full step before T-1.
-        for (; !thin && kt + 9 < T; kt += 6) {
+        // Unchecked: every prefetch of the block (up to kt + 8) is a full step of this tile: before
+        // T-1, which may be partial, or up to T-1 in instances without tail masks (no partial K
+        // step), which thus leave 3 checked steps instead of up to 8 when T % 6 == 4.
+        for (; !thin && kt + (KT ? 9 : 8) < T; kt += 6) {
             refresh();
             step.template operator()<1, 1, false, false, false>(kt);
             step.template operator()<0, 2, false, false, false>(kt + 1);

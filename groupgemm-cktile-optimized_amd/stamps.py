@@ -68,18 +68,20 @@ def part_fns(lib):
     return fns
 
 
-def unchecked_steps(T: int) -> int:
-    """K steps the kernel's unchecked loop runs (kt = 1, 7, ... while kt + 9 < T, six per pass)."""
-    passes = max(0, (T - 10 + 5) // 6)
+def unchecked_steps(T: int, masks: bool) -> int:
+    """K steps the kernel's unchecked loop runs: kt = 1, 7, ... while kt + 9 < T (instances with
+    tail masks) or kt + 8 < T (without), six per pass."""
+    lead = 9 if masks else 8
+    passes = max(0, (T - lead - 1 + 5) // 6)
     return 6 * passes
 
 
-def analyse(st: np.ndarray, T: int) -> dict:
-    """st: [grid, 64] stamps of one launch (int64)."""
+def analyse(st: np.ndarray, T: int, masks: bool) -> dict:
+    """st: [grid, 64] stamps of one launch (int64); masks: the instance has tail masks."""
     grid = st.shape[0]
     total = st[:, 63] - st[:, 0]
     tiles = np.array([int(sum(1 for j in range(7) if st[w, 2 + 5 * j] > 0)) for w in range(grid)])
-    nun = unchecked_steps(T)
+    nun = unchecked_steps(T, masks)
     seg = {"first step": [], "unchecked": [], "next tile lookup": [], "checked": [], "gap to next tile": []}
     for w in range(grid):
         for j in range(tiles[w]):
@@ -173,7 +175,16 @@ def main():
             print(f"  {detail}: no part holds a complete set of stamps (per-tile plan?)", flush=True)
             continue
         contraction = {"dgrad": n, "wgrad": m}.get(args.op.split("_")[0], k)
-        r = analyse(best, -(-contraction // (128 if "fp8" in args.op else 64)))
+        ks = 128 if "fp8" in args.op else 64
+        # the plan's tails flag (KernelArgs::tails), for balanced groups
+        kind = args.op.split("_")[0]
+        if kind == "dgrad":
+            masks = n % ks != 0 or k % 256 != 0
+        elif kind == "wgrad":
+            masks = m % ks != 0 or m < 4 * ks or n % 256 != 0 or k % 256 != 0
+        else:
+            masks = k % ks != 0
+        r = analyse(best, -(-contraction // ks), masks)
         r.update({"shape": [b, m, n, k], "plan": detail, "stamps": best.tolist()})
         results.append(r)
         print(f"  {detail}", flush=True)
