@@ -835,6 +835,9 @@ grouped_gemm_kernel(const KernelArgs args) {
     constexpr int A_ST = P::la * kWaves * 1024;                     // bytes of an A stage
     constexpr int B_ST = P::lb * kWaves * 1024;                     // bytes of a B stage
     constexpr int LV   = P::la > P::lb ? P::la : P::lb;             // DMA lane offsets per operand
+    // 256-column short tiles keep the 8-DMA A stage of the wide plan; its DMAs j >= 6 cover tile
+    // rows 192-255, which a short tile never reads (and which lie outside its resource): not issued
+    constexpr auto a_dead = [](int j) { return SHORT && !SWIDE && j * 32 >= kShortTileM; };
     constexpr int CSTR = SWIDE ? kShortWideTileN * 2 + 16 : kCStride; // staged C row stride
     static_assert(kAStages * A_ST + kBStages * B_ST <= kLdsBytes && kShortTileM * CSTR <= kLdsBytes, "LDS");
     static_assert(!(F8 && F16), "fp8 writes bf16");
@@ -1308,7 +1311,10 @@ grouped_gemm_kernel(const KernelArgs args) {
     // ---- prologue of a tile that starts cold: A(0), B(0..2), the first DMAs of A(1) ----------
     auto issue_prologue = [&]() {
         refresh();
-        sfor<0, P::la>([&](auto j) { dma_now(a_dst[0], A_OP{}, j, 0); });
+        sfor<0, P::la>([&](auto j) {
+            if constexpr (!a_dead(j))
+                dma_now(a_dst[0], A_OP{}, j, 0);
+        });
         sfor<0, P::lb>([&](auto j) { dma_now(b_dst[0], B_OP{}, j, 0); });
         sfor<0, P::lb>([&](auto j) { dma_now(b_dst[1], B_OP{}, j, 1); });
         sfor<0, P::lb>([&](auto j) { dma_now(b_dst[2], B_OP{}, j, 2); });
@@ -1545,7 +1551,8 @@ grouped_gemm_kernel(const KernelArgs args) {
             constexpr int mi = decltype(mi_)::value;
             sfor<0, P::slots>([&](auto idx_) {
                 constexpr int idx = decltype(idx_)::value;
-                constexpr int dk = P::dma_kind(mi, idx), dj = P::dma_j(mi, idx);
+                constexpr int dj = P::dma_j(mi, idx);
+                constexpr int dk = P::dma_kind(mi, idx) == 1 && a_dead(dj) ? 0 : P::dma_kind(mi, idx);
                 if constexpr (dk == 1)
                     set_m0<dj * 4096>(a_dst[NX]); // the MFMA below is the wait state
                 else if constexpr (dk == 2)
@@ -1615,7 +1622,8 @@ grouped_gemm_kernel(const KernelArgs args) {
             constexpr int mi = decltype(mi_)::value;
             sfor<0, P::slots>([&](auto idx_) {
                 constexpr int idx = decltype(idx_)::value;
-                constexpr int dk = P::dma_kind(mi, idx), dj = P::dma_j(mi, idx);
+                constexpr int dj = P::dma_j(mi, idx);
+                constexpr int dk = P::dma_kind(mi, idx) == 1 && a_dead(dj) ? 0 : P::dma_kind(mi, idx);
                 if constexpr (mi == P::last && idx == P::bar) {
                     sched_fence();
                     wait_vm_lds_barrier<P::vm_at_barrier()>();
