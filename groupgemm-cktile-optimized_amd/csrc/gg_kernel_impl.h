@@ -557,6 +557,16 @@ __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0
 // invariants (which would keep dozens of precomputed addresses live across the K loop).
 __device__ __forceinline__ void fresh_v(int &v) { asm volatile("" : "+v"(v)); }
 __device__ __forceinline__ void fresh_s(uint32_t &v) { asm volatile("" : "+s"(v)); }
+// v ^ X as one VALU instruction at this point (opaque: not merged with another, not hoisted).
+template <int X> __device__ __forceinline__ int xor_here(int v) {
+    if constexpr (X == 0) {
+        return v;
+    } else {
+        int r;
+        asm volatile("v_xor_b32 %0, %1, %2" : "=v"(r) : "i"(X), "v"(v));
+        return r;
+    }
+}
 
 // Buffer resource for the LDS DMA (SGPR quad): base, stride 0, byte bound, gfx9 raw format.
 __device__ __forceinline__ i32x4 dma_rsrc(const void *p, uint32_t bytes) {
@@ -896,24 +906,33 @@ grouped_gemm_kernel(const KernelArgs args) {
     // (lane%8)/2, 8 columns at 8 (lane%2). The column-block swap in every other pair of row
     // blocks puts the blocks that lanes 0-15 and 16-31 of one transposed read take (row blocks
     // rb and rb + 2) in different halves of the 256-byte bank window.
-    // fp8 MN-major: blocks of 8 rows x 16 columns (one 16-byte row per lane); LDS row block p
-    // holds stored row block p ^ (2 ((p / 4) & 1)) with column blocks swapped when (p / 4) is odd:
-    // DMA j (rows of LDS block 2j + wave/2) reads stored row block 2 (j ^ s) + wave/2, column
-    // block (8 (wave%2) + lane/8) ^ s, s = (j / 2) & 1, row lane%8 of the block. The row block
-    // swap gives each lane the K order of a K-major fp8 fragment (halves swapped for odd lane/16,
-    // see below); the column swap separates the blocks of lanes 0-15 and 16-31 in the banks.
+    // fp8 MN-major: in LDS the step is 128 rows of 256 bytes (16 column blocks of 16 columns);
+    // LDS row p holds stored row p ^ (16 s), s = (p / 32) & 1, and its 16-byte slot u holds
+    // column block 8 ((u / 8) ^ s) + ((u % 8) ^ (p % 8)). DMA j lands at 1024 (4j + wave): LDS
+    // rows 16 j + 4 wave + lane/16, slot lane%16, so that 16 lanes read one stored row's 256
+    // contiguous bytes (4 consecutive lanes: 64 bytes). The DMA unit takes one cycle per 4-lane
+    // group and cache line it touches: 16 per DMA here, against 64 with a lane per stored row.
+    // The row swap gives each lane the K order of a K-major fp8 fragment (halves swapped for odd
+    // lane/16, see below); the slot permutation spreads the 8 rows of one transposed read over
+    // 8 slots, and the half swap puts lanes 0-15 and 16-31 in different halves of the banks.
     const int ld_row   = lane >> 3;
     const int ld_chunk = (lane & 7) ^ ld_row;
     const int mn_c     = (wave & 1) * 8 + (lane >> 3);
+    const int f8_rlo   = (4 * wave + (lane >> 4)) & 7; // fp8: LDS row % 8 of the lane's DMA rows
     // column of the lane in a transposed DMA (elements), with column-block swap sw
-    auto mn_col = [&](int sw) { return (mn_c ^ sw) * 16 + (F8 ? 0 : (lane & 1) * 8); };
+    auto mn_col = [&](int sw) {
+        if constexpr (F8)
+            return (8 * (((lane & 15) >> 3) ^ sw) + ((lane & 7) ^ f8_rlo)) * 16;
+        else
+            return (mn_c ^ sw) * 16 + (lane & 1) * 8;
+    };
     // the column-block swap of transposed DMA j
     auto mn_swz = [](int j) { return F8 ? (j >> 1) & 1 : j & 1; };
     auto dma_off = [&](bool mn, int j, int ld) {
         if (!mn)
             return (j * 32 + wave * 8 + ld_row) * ld * ES + ld_chunk * 16;
         if (F8)
-            return (8 * (2 * (j ^ mn_swz(j)) + (wave >> 1)) + (lane & 7)) * ld + mn_col(mn_swz(j));
+            return (16 * (j ^ mn_swz(j)) + 4 * wave + (lane >> 4)) * ld + mn_col(mn_swz(j));
         return ((4 * (2 * j + (wave >> 1)) + ((lane & 7) >> 1)) * ld + mn_col(mn_swz(j))) * 2;
     };
     // voff[0]: A's offsets; voff[1]: B's (the forward op shares A's: both row strides are K).
@@ -944,17 +963,27 @@ grouped_gemm_kernel(const KernelArgs args) {
     // the chunks of such a pair differ in bit 0 as well and take different banks. The lane's K
     // order is then permuted the same way in x and w, which leaves the dot product unchanged.
     // fp8 MN-major: ds_read_b64_tr_b8 gives lane i of each 16-lane group column i of 8 rows when
-    // source lane s points at row s/2, column 8 (s%2): read t (0-3) of lane l takes LDS row block
-    // 4 (l/16) + t, i.e. base + 8192 (l/16) + 2048 t + 128 (blk ^ (l/16 & 1)), which holds the
-    // lane's K values in the K-major fragment's order.
+    // source lane s points at row s/2, column 8 (s%2): read t = 2 kh + half of lane l (q = l/16,
+    // s = l%16) takes LDS rows 32 q + 8 t + s/2 (stored rows 32 q + 16 (kh ^ (q & 1)) + 8 half
+    // + s/2: the lane's K values in the K-major fragment's order), column block 8 h + blk of
+    // the wave's half h, i.e. slot 8 (h ^ (q & 1)) + (blk ^ (s/2)):
+    //   (base ^ 16 blk) + 4096 kh + 2048 half,
+    //   base = 8192 q + 256 (s/2) + 128 (h ^ (q & 1)) + 16 (s/2) + 8 (s%2),
+    // one base per stage (bits 4-6 of it are s/2, so the XOR picks the slot). In one read the
+    // 8 rows of a group take 8 different slots, and groups of odd q the other half of the banks.
     const int fr_row = lane & 15, fr_q = lane >> 4;
+    const int mn8    = fr_q * 8192 + (fr_row >> 1) * (256 + 16) + (fr_row & 1) * 8;
     int frag_a[2], frag_b[2];
     sfor<0, 2>([&](auto kh) {
         const int off = fr_row * kRowBytes +
                         (((F8 ? 2 * fr_q + (kh ^ (fr_q & 1)) : kh * 4 + fr_q) ^ (fr_row & 7)) * 16);
-        const int mn  = (lane >> 4) * (F8 ? 8192 : 4096) + (lane & 15) * 8 + (kh ? -128 : 128) * (fr_q & 1);
-        frag_a[kh]    = A_MN ? wm * 1024 + mn : wm * (ILV ? 16 : 128) * kRowBytes + off;
-        frag_b[kh]    = B_MN ? wn * 1024 + mn : wn * WCOLS * kRowBytes + off;
+        const int mn  = F8 ? 0 : (lane >> 4) * 4096 + (lane & 15) * 8 + (kh ? -128 : 128) * (fr_q & 1);
+        frag_a[kh]    = !A_MN ? wm * (ILV ? 16 : 128) * kRowBytes + off
+                        : F8  ? mn8 + 128 * (wm ^ (fr_q & 1))
+                              : wm * 1024 + mn;
+        frag_b[kh]    = !B_MN ? wn * WCOLS * kRowBytes + off
+                        : F8  ? mn8 + 128 * (wn ^ (fr_q & 1))
+                              : wn * 1024 + mn;
     });
 
     // Register epilogue: in store s = 2h + half of a 16-row block, lane l writes 16 bytes of
@@ -1030,7 +1059,11 @@ grouped_gemm_kernel(const KernelArgs args) {
             f[R] = lds_read(rd[R] + blk * BLK_ROWS * kRowBytes);
         } else {
             constexpr int kh = R >> 1, half = R & 1;
-            const u32x2   v  = lds_read_tr(rd[blk & 1] + kh * (F8 ? 4096 : 16384) + half * 2048 + blk * 128);
+            u32x2         v;
+            if constexpr (F8)
+                v = lds_read_tr(xor_here<16 * decltype(blk)::value>(rd[0]) + kh * 4096 + half * 2048);
+            else
+                v = lds_read_tr(rd[blk & 1] + kh * 16384 + half * 2048 + blk * 128);
             f[kh][2 * half]     = static_cast<int>(v[0]);
             f[kh][2 * half + 1] = static_cast<int>(v[1]);
         }
