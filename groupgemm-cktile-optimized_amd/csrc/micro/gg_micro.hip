@@ -3,6 +3,7 @@
 // memory, and what a transposed LDS read costs by the way its lanes address LDS. Every address
 // stays inside the buffers below; each kernel ends after a fixed number of iterations.
 //   ./bin/gg_micro            -> one line per pattern: cycles per instruction per CU
+// C-tile stores run on all 256 CUs (st256) and on 64 (st 64).
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
@@ -148,6 +149,41 @@ __global__ __launch_bounds__(256) void tr_kernel(int *out, unsigned long long *c
         cyc[blockIdx.x] = t1 - t0;
 }
 
+// ---- C-tile stores: 128 buffer_store_dwordx4 (1 KB each) per workgroup, one 256 x 256 bf16 tile
+// per workgroup of a 4096 x 4096 output, by lane pattern; all CUs at once or a quarter of them.
+enum StorePattern { kStRowPerLane, kStRowPer8Lanes, kStorePatterns };
+const char *kStoreNames[kStorePatterns] = {
+    "C store, lane%8 = row: 8 rows x 128 B (the kernel's fused stores)",
+    "C store, 8 consecutive lanes per row: 8 rows x 128 B",
+};
+constexpr int kCN = 4096, kStoreReps = 50;
+
+template <int PAT>
+__global__ __launch_bounds__(256) void store_kernel(unsigned short *c, unsigned long long *cyc) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int tile = static_cast<int>(blockIdx.x); // < 256: 16 x 16 tiles
+    const int row0 = (tile / 16) * 256, col0 = (tile % 16) * 256;
+    const int r = PAT == kStRowPerLane ? (lane & 7) : (lane >> 3);
+    const int ch = PAT == kStRowPerLane ? (lane >> 3) : (lane & 7);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(c, 0, kCN * kCN * 2, 0x00020000);
+    const unsigned v = static_cast<unsigned>(lane);
+    const __attribute__((ext_vector_type(4))) unsigned d = {v, v + 1, v + 2, v + 3};
+    const unsigned long long t0 = __builtin_readcyclecounter();
+    for (int rep = 0; rep < kStoreReps; ++rep) {
+        const int wr = (wave >> 1) * 128, wc = (wave & 1) * 128; // the wave's 128 x 128 quadrant
+#pragma unroll
+        for (int s = 0; s < 32; ++s) {
+            const int row = row0 + wr + (s >> 1) * 8 + r;          // < 4096
+            const int col = col0 + wc + (s & 1) * 64 + ch * 8;    // + 8 <= 4096
+            __builtin_amdgcn_raw_buffer_store_b128(d, rs, (row * kCN + col) * 2, 0, /*nt*/ 2);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    const unsigned long long t1 = __builtin_readcyclecounter();
+    if (threadIdx.x == 0)
+        cyc[blockIdx.x] = t1 - t0;
+}
+
 #define CHECK(x)                                                                                   \
     do {                                                                                           \
         if ((x) != hipSuccess) {                                                                   \
@@ -156,13 +192,13 @@ __global__ __launch_bounds__(256) void tr_kernel(int *out, unsigned long long *c
         }                                                                                          \
     } while (0)
 
-double mean_cycles(const unsigned long long *d) {
-    std::vector<unsigned long long> h(kGrid);
-    if (hipMemcpy(h.data(), d, kGrid * 8, hipMemcpyDeviceToHost) != hipSuccess)
+double mean_cycles(const unsigned long long *d, int grid = kGrid) {
+    std::vector<unsigned long long> h(grid);
+    if (hipMemcpy(h.data(), d, grid * 8, hipMemcpyDeviceToHost) != hipSuccess)
         return -1;
     double s = 0;
     for (auto v : h) s += static_cast<double>(v);
-    return s / kGrid;
+    return s / grid;
 }
 
 template <int P> void launch_dma(const char *buf, unsigned long long *cyc) {
@@ -199,6 +235,22 @@ int main() {
             CHECK(hipDeviceSynchronize());
         }
         std::printf("lds  %-70s %6.2f cycles per read per CU\n", kTrNames[p], mean_cycles(cyc) / (4.0 * 16 * kIters));
+    }
+    unsigned short *cbuf = nullptr;
+    CHECK(hipMalloc(&cbuf, static_cast<size_t>(kCN) * kCN * 2));
+    for (int grid : {256, 64}) {
+        for (int p = 0; p < kStorePatterns; ++p) {
+            for (int rep = 0; rep < 3; ++rep) {
+                if (p == kStRowPerLane)
+                    hipLaunchKernelGGL((store_kernel<kStRowPerLane>), dim3(grid), dim3(256), 0, 0, cbuf, cyc);
+                else
+                    hipLaunchKernelGGL((store_kernel<kStRowPer8Lanes>), dim3(grid), dim3(256), 0, 0, cbuf, cyc);
+                CHECK(hipDeviceSynchronize());
+            }
+            const double c = mean_cycles(cyc, grid) / (kStoreReps * 128.0);
+            std::printf("st%3d %-70s %6.2f cycles per store per CU (%.1f B/clk per CU)\n", grid, kStoreNames[p], c,
+                        1024.0 / c);
+        }
     }
     return 0;
 }
