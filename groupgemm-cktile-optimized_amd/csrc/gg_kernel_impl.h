@@ -557,13 +557,14 @@ __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0
 // invariants (which would keep dozens of precomputed addresses live across the K loop).
 __device__ __forceinline__ void fresh_v(int &v) { asm volatile("" : "+v"(v)); }
 __device__ __forceinline__ void fresh_s(uint32_t &v) { asm volatile("" : "+s"(v)); }
-// v ^ X as one VALU instruction at this point (opaque: not merged with another, not hoisted).
+// v ^ X as one VALU instruction (a pure asm statement: the four transposed reads of a fragment
+// share it; volatile, one per read, the fp8 wgrad kernel took 3 % longer).
 template <int X> __device__ __forceinline__ int xor_here(int v) {
     if constexpr (X == 0) {
         return v;
     } else {
         int r;
-        asm volatile("v_xor_b32 %0, %1, %2" : "=v"(r) : "i"(X), "v"(v));
+        asm("v_xor_b32 %0, %1, %2" : "=v"(r) : "i"(X), "v"(v));
         return r;
     }
 }
