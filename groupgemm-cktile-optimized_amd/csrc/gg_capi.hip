@@ -392,7 +392,7 @@ void free_plan(gg_plan *plan) {
     delete plan;
 }
 
-// Tile descriptors of forward and dgrad plans of whole tiles (host-size tables): every
+// Tile descriptors of forward, dgrad and wgrad plans of whole tiles (host-size tables): every
 // workgroup's tiles in the kernel's own walk (xcd_remap, then locate_tile over the plan's group
 // table with its tile rows and N-tiles), so that the kernel reads a tile's first row, group and
 // N-tile from a lane of a register instead of recomputing them between its K loops. Not built
@@ -402,13 +402,18 @@ int setup_tile_desc(gg_plan *plan, const int64_t *group_m, hipStream_t s) {
     gg::KernelArgs &a   = plan->args;
     const char     *env = std::getenv("GG_TILE_DESC");
     if ((env != nullptr && env[0] == '0') || a.splits > 1 || a.tail_splits > 1 || plan->grid <= 0 ||
-        plan->mode % 4 == gg::kWgrad || plan->total_m >= INT32_MAX)
+        plan->total_m >= INT32_MAX)
         return GG_OK;
     const int per_wg = static_cast<int>(gg::cdiv(plan->total_tiles, plan->grid));
     if (per_wg > gg::kMaxDescPerWg)
         return GG_OK;
+    // wgrad: every group owns m_out / 256 x N-tiles output tiles whatever its size
+    const bool    wgrad    = plan->mode % 4 == gg::kWgrad;
+    const int64_t out_rows = wgrad ? a.m_out : 0;
+    if (wgrad && (gg::cdiv(out_rows, a.tile_m) > 0xffff || a.n_tiles > 0x7fff))
+        return GG_OK;
     std::vector<gg::GroupEntry> table(static_cast<size_t>(plan->group_num));
-    const int64_t tiles = gg::build_group_table(group_m, plan->group_num, a.n_tiles, table.data(), 0, a.tile_m);
+    const int64_t tiles = gg::build_group_table(group_m, plan->group_num, a.n_tiles, table.data(), out_rows, a.tile_m);
     if (tiles != plan->total_tiles)
         return fail(GG_ERR_INVALID, "tile descriptors: the group table's tile count differs from the plan's");
     std::vector<gg::TileDesc> desc(static_cast<size_t>(plan->grid) * per_wg, gg::TileDesc{0, 0, 0, 0});
@@ -420,7 +425,13 @@ int setup_tile_desc(gg_plan *plan, const int64_t *group_m, hipStream_t s) {
                 break;
             const int L = gg::xcd_remap(t, plan->total_tiles, plan->grid, a.n_xcd);
             int       tm, tn;
-            gg::locate_tile(L, table.data(), plan->group_num, a.n_tiles, a.band, &g, &tm, &tn, 0, a.tile_m);
+            gg::locate_tile(L, table.data(), plan->group_num, a.n_tiles, a.band, &g, &tm, &tn,
+                            static_cast<int>(out_rows), a.tile_m);
+            if (wgrad) { // the group's first token, (N-tile << 16) | M-tile, the group's tokens
+                desc[static_cast<size_t>(wg) * per_wg + i] =
+                    gg::TileDesc{static_cast<int32_t>(table[g].row0), g, (tn << 16) | tm, table[g].m};
+                continue;
+            }
             const int64_t r0 = table[g].row0 + static_cast<int64_t>(tm) * a.tile_m;
             const int     mv = static_cast<int>(std::min<int64_t>(a.tile_m, table[g].m - static_cast<int64_t>(tm) * a.tile_m));
             desc[static_cast<size_t>(wg) * per_wg + i] = gg::TileDesc{static_cast<int32_t>(r0), g, (tn << 9) | mv, 0};
@@ -988,11 +999,9 @@ static int prepare_backward(int layout, int dtype_a, int dtype_b, int group_num,
                 return st2;
             }
         }
-        if (dgrad) {
-            if (const int st3 = setup_tile_desc(plan, group_m, s); st3 != GG_OK) {
-                free_plan(plan);
-                return st3;
-            }
+        if (const int st3 = setup_tile_desc(plan, group_m, s); st3 != GG_OK) {
+            free_plan(plan);
+            return st3;
         }
 
         plan->detail = "mi355x " + what + " persistent " + std::to_string(ka.tile_m) + "x256x" +

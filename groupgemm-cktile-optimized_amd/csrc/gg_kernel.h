@@ -92,10 +92,10 @@ struct KernelArgs {
 
 // One tile descriptor (see KernelArgs::desc).
 struct TileDesc {
-    int32_t row0;  // first row of the tile in A (x or grad_out) and out
+    int32_t row0;  // first row of the tile in A (x or grad_out) and out; wgrad: the group's first token
     int32_t g;     // group
-    int32_t tn_mv; // (N-tile << 9) | valid rows (at most 256)
-    int32_t pad;
+    int32_t tn_mv; // (N-tile << 9) | valid rows (at most 256); wgrad: (N-tile << 16) | M-tile
+    int32_t m;     // wgrad: the group's tokens (0 otherwise)
 };
 constexpr int kMaxDescPerWg = 64; // one per lane of a wave
 

@@ -1096,18 +1096,21 @@ grouped_gemm_kernel(const KernelArgs args) {
     // compiler issues vector loads and waits for them with vmcnt(0), which also drains every
     // operand DMA in flight, once per table entry the tile walk reads.
     const const_space<GroupEntry> const_table = to_const_space(args.groups);
-    // Tile descriptors (host-size forward and dgrad plans of whole tiles, at most 64 per
-    // workgroup): lane i holds this workgroup's i-th tile, its first row in x / out, its group and
-    // (N-tile << 9 | valid rows). make_tile reads them with three v_readlane instead of walking
+    // Tile descriptors (host-size plans of whole tiles, at most 64 per workgroup): lane i holds
+    // this workgroup's i-th tile, its first row in x / out, its group and (N-tile << 9 | valid
+    // rows); wgrad: the group's first token, its group, (N-tile << 16 | M-tile) and the group's
+    // tokens. make_tile reads them with three or four v_readlane instead of walking
     // the XCD remap, the group table and the band order (divisions and dependent scalar loads
     // between the K loops, where no MFMA issues).
-    const bool use_desc = LAYOUT != kWgrad && !TAIL && splits == 1 && args.desc != nullptr;
-    int        d_row0 = 0, d_g = 0, d_tnm = 0;
+    const bool use_desc = !TAIL && splits == 1 && args.desc != nullptr;
+    int        d_row0 = 0, d_g = 0, d_tnm = 0, d_m = 0;
     if (use_desc && lane < args.desc_per_wg) {
         const i32x4 dv = reinterpret_cast<const i32x4 *>(args.desc)[static_cast<int>(blockIdx.x) * args.desc_per_wg + lane];
         d_row0         = dv[0];
         d_g            = dv[1];
         d_tnm          = dv[2];
+        if constexpr (LAYOUT == kWgrad)
+            d_m = dv[3];
     }
     auto      make_tile = [&](int t, int ti) -> Tile {
         // split-K: one unit per workgroup, no L2 sharing across rounds to arrange
@@ -1140,8 +1143,15 @@ grouped_gemm_kernel(const KernelArgs args) {
             desc_row0 = __builtin_amdgcn_readlane(d_row0, ti);
             g         = __builtin_amdgcn_readlane(d_g, ti);
             const int tnm = __builtin_amdgcn_readlane(d_tnm, ti);
-            tn        = tnm >> 9;
-            desc_mv   = tnm & 511;
+            if constexpr (LAYOUT == kWgrad) { // the group's first token and size, M- and N-tile
+                ge.row0 = desc_row0;
+                ge.m    = __builtin_amdgcn_readlane(d_m, ti);
+                tm      = tnm & 0xffff;
+                tn      = tnm >> 16;
+            } else {
+                tn      = tnm >> 9;
+                desc_mv = tnm & 511;
+            }
         } else if (in_kernel_table) {
             // the one lane whose group owns logical tile L
             const uint64_t hit = __ballot(lane < args.group_num && lgrp.tile0 <= L && L - lgrp.tile0 < lgrp.tiles);

@@ -7,13 +7,14 @@ with them must give the bits of the same plan without them (GG_TILE_DESC=0), and
 must be within rtol = atol = 1e-2 of float32 (bench/bench_main.cpp:264-268). Outputs are
 NaN-prefilled, so an unwritten tile fails.
 
-Cases (forward through the backend, fp8 forward and dgrad through their plans):
+Cases (forward through the backend, fp8 forward, dgrad and wgrad through their plans):
 - 256 x 256 cross-tile bf16 with ragged and empty groups and a column tail;
 - config 5a's short tiles (176 rows) in fp16, 256 and 288 columns wide;
 - a one-round per-tile plan with narrow tiles (256 x 224);
 - exactly 64 tiles per workgroup (the last descriptor lane), and 68 (no descriptors: the kernel
   walks the table itself), checked on sampled rows against float32;
-- fp8 e4m3 forward and bf16 dgrad with empty groups.
+- fp8 e4m3 forward and bf16 dgrad with empty groups;
+- bf16 and fp8 wgrad with ragged and empty groups, a partial M-tile and a column tail.
 """
 import pytest
 import torch
@@ -160,6 +161,54 @@ def test_dgrad_descriptors_match_walk(pkg, monkeypatch):
     for gi, m in enumerate(gm):
         ref = go[row:row + m].float() @ w[gi].float()
         got = outs[0][row:row + m].float()
+        assert not torch.isnan(got).any(), f"group {gi}: unwritten outputs"
+        bad = int(((got - ref).abs() > ATOL + RTOL * ref.abs()).sum())
+        assert bad == 0, f"group {gi}: {bad} outputs off"
+        row += m
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_wgrad_descriptors_match_walk(pkg, monkeypatch, fp8):
+    """wgrad (bf16, and e5m2 x e4m3 fp8 with unit scales): descriptors hold each tile's group, its
+    first token and size and its (M-tile, N-tile); ragged and empty groups, a partial last M-tile
+    (N = 1000, fp8 1008) and a column tail (K = 2312, fp8 2320): 320 tiles, the cross-tile variant."""
+    gm = [1000, 0, 2500, 300, 4096, 0, 17, 129]
+    n, k = (1008, 2320) if fp8 else (1000, 2312)  # fp8: multiples of 16
+    print(f"[tile-desc] wgrad fp8={fp8}: groups={len(gm)} N={n} K={k}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(99)
+    go = torch.randn((sum(gm), n), generator=g, device=DEV)
+    x = torch.randn((sum(gm), k), generator=g, device=DEV)
+    if fp8:
+        go, x = go.to(torch.float8_e5m2), x.to(torch.float8_e4m3fn)
+    else:
+        go, x = go.to(torch.bfloat16), x.to(torch.bfloat16)
+    s = torch.cuda.current_stream(DEV).cuda_stream
+    gsd = torch.ones(1, dtype=torch.float32, device=DEV)
+    osd = torch.ones(len(gm), dtype=torch.float32, device=DEV)
+    outs, details = [], []
+    for desc in (True, False):
+        if desc:
+            monkeypatch.delenv("GG_TILE_DESC", raising=False)
+        else:
+            monkeypatch.setenv("GG_TILE_DESC", "0")
+        out = torch.full((len(gm), n, k), float("nan"), dtype=torch.bfloat16, device=DEV)
+        if fp8:
+            plan = pkg.BackwardPlan("wgrad", pkg.DType.FP8_E5M2, n, k, gm, go.data_ptr(), x.data_ptr(),
+                                    out.data_ptr(), s, other_dtype=pkg.DType.FP8_E4M3, grad_scale=gsd.data_ptr(),
+                                    other_scale=osd.data_ptr())
+        else:
+            plan = pkg.BackwardPlan("wgrad", pkg.DType.BF16, n, k, gm, go.data_ptr(), x.data_ptr(), out.data_ptr(), s)
+        plan.run(s)
+        torch.cuda.synchronize(DEV)
+        details.append(plan.detail())
+        plan.release()
+        outs.append(out)
+    assert "cross-tile" in details[0], details
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), details
+    row = 0
+    for gi, m in enumerate(gm):
+        ref = go[row:row + m].float().t().contiguous() @ x[row:row + m].float()
+        got = outs[0][gi].float()
         assert not torch.isnan(got).any(), f"group {gi}: unwritten outputs"
         bad = int(((got - ref).abs() > ATOL + RTOL * ref.abs()).sum())
         assert bad == 0, f"group {gi}: {bad} outputs off"
