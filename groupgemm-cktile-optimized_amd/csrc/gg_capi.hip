@@ -397,12 +397,13 @@ void free_plan(gg_plan *plan) {
 // table with its tile rows and N-tiles), so that the kernel reads a tile's first row, group and
 // N-tile from a lane of a register instead of recomputing them between its K loops. Not built
 // (the kernel walks the table itself) with split-K, a tail split, more than kMaxDescPerWg tiles
-// per workgroup or rows past 2^31. GG_TILE_DESC=0 in the environment turns them off.
+// per workgroup or rows past 2^31 (output rows, and for wgrad the input tokens whose offsets its
+// descriptors hold). GG_TILE_DESC=0 in the environment turns them off.
 int setup_tile_desc(gg_plan *plan, const int64_t *group_m, hipStream_t s) {
     gg::KernelArgs &a   = plan->args;
     const char     *env = std::getenv("GG_TILE_DESC");
     if ((env != nullptr && env[0] == '0') || a.splits > 1 || a.tail_splits > 1 || plan->grid <= 0 ||
-        plan->total_m >= INT32_MAX)
+        !gg::desc_rows_fit(group_m, plan->group_num, plan->total_m))
         return GG_OK;
     const int per_wg = static_cast<int>(gg::cdiv(plan->total_tiles, plan->grid));
     if (per_wg > gg::kMaxDescPerWg)

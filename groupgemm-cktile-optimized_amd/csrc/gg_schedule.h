@@ -130,6 +130,22 @@ inline int64_t build_group_table(const int64_t *group_m, int group_num, int64_t 
     return tiles;
 }
 
+// Whether a plan's rows fit the 32-bit first-row field of its tile descriptors (TileDesc::row0):
+// forward and dgrad descriptors hold a tile's first output row (below out_rows, the plan's
+// output rows), wgrad descriptors the group's first input token (below the sum of the group
+// sizes, which wgrad's out_rows = group_num * N does not bound). Sizes must be >= 0.
+inline bool desc_rows_fit(const int64_t *group_m, int group_num, int64_t out_rows) {
+    if (out_rows >= INT32_MAX)
+        return false;
+    int64_t rows = 0;
+    for (int g = 0; g < group_num; ++g) {
+        if (group_m[g] < 0 || group_m[g] >= INT32_MAX - rows)
+            return false;
+        rows += group_m[g];
+    }
+    return true;
+}
+
 // Group and (M-tile, N-tile) of logical tile L. *g is a hint: the group of a smaller L seen
 // before (0 at the start); logical tiles only grow for one workgroup, so the scan only moves
 // forward. Empty groups own no tiles and are stepped over. out_rows and tile_m as in

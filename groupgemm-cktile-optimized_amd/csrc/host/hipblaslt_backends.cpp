@@ -19,14 +19,19 @@
 // ends only if those workgroups get a CU, which the kernel is sure of only when it has the GPU to
 // itself. Four such kernels on four streams split the CUs between them, and each can fill its
 // share with workgroups that wait for ones still queued behind them: none of the four finishes.
-// The installed hipBLASLt's heuristic picks a stream-K kernel (SK3) first for every shape tried,
-// Primus-Turbo runs its first choice on 4 streams, and that loop hung on its first call for 8
-// groups of 1024 x 4096 x 7168 (shapes/full.csv TestID 3) while the same kernels one at a time
-// (hipblaslt_seq) finished all 360 cases. So the 4-stream mode takes the heuristic's best
-// algorithm that is not stream-K (of its first kCandidates), in prepare() and in every run(), and
-// reports N/A if there is none; hipblaslt_seq keeps the first choice. (With ROCm 7.2's hipBLASLt
-// on MI355X every bf16 and fp16 shape tried has only stream-K kernels among the first 16, so
-// the 4-stream loop is N/A there and hipblaslt_seq is the per-group baseline.)
+// Primus-Turbo runs the heuristic's first choice on 4 streams, and that loop hung on its first
+// call for 8 groups of 1024 x 4096 x 7168 (shapes/full.csv TestID 3) while the same kernels one
+// at a time (hipblaslt_seq) finished all 360 cases. The installed hipBLASLt's heuristic ranks
+// only stream-K kernels (SK3) in its first 64 results for every bf16 and fp16 shape tried on
+// MI355X, while the library holds about 45 other kernels that support each shape (all
+// getAllAlgos results that pass matmulIsAlgoSupported within the workspace limit and are not
+// stream-K). So the 4-stream mode, per distinct group size, times each of those kernels once in
+// prepare() (one untimed launch, then two timed ones, on the problem's own inputs, into a scratch
+// output so that the driver's cleared output stays cleared) and keeps the fastest. run() keeps
+// Primus-Turbo's per-call work, the heuristic query included, and launches the heuristic's first
+// choice unless it is stream-K, in which case it launches the kept kernel after checking it
+// against the call's descriptors (matmulIsAlgoSupported). No stream-K kernel ever runs on the 4
+// streams; hipblaslt_seq keeps the heuristic's first choice, stream-K or not.
 //
 // Failures of HIP or hipBLASLt calls throw std::runtime_error (the driver's ERROR row, a Python
 // exception through the shim); nothing here exits the process. Streams keep the default priority.
@@ -100,10 +105,15 @@ public:
         return best;
     }
 
-    // The heuristic's best choice among its first `count` that is not a stream-K kernel; false if
-    // there is none. *name gets the kernel's name.
-    bool choose_without_stream_k(hipblasLtHandle_t h, int count, hipblasLtMatmulHeuristicResult_t *pick,
-                                 std::string *name) const;
+    // Whether `algo` solves this matmul within the workspace limit (matmulIsAlgoSupported, which
+    // also records the problem in the algo, as hipblasLtMatmul expects).
+    bool supports(hipblasLtHandle_t h, hipblasLtMatmulAlgo_t &algo) const {
+        const float one = 1.0f, zero = 0.0f;
+        size_t      need = 0;
+        return hipblaslt_ext::matmulIsAlgoSupported(h, op_, &one, w_, x_, &zero, out_, out_, algo, need) ==
+                   HIPBLAS_STATUS_SUCCESS &&
+               need <= ws_bytes_;
+    }
 
     void launch(hipblasLtHandle_t h, const hipblasLtMatmulAlgo_t &algo, const void *w, const void *x, void *out,
                 void *ws, hipStream_t s) const {
@@ -129,22 +139,6 @@ bool stream_k_kernel(const std::string &name) {
             ++q;
         if (q > p + 3 && (q == name.size() || name[q] == '_') && std::stoi(name.substr(p + 3, q - p - 3)) > 0)
             return true;
-    }
-    return false;
-}
-
-bool GroupMatmul::choose_without_stream_k(hipblasLtHandle_t h, int count, hipblasLtMatmulHeuristicResult_t *pick,
-                                          std::string *name) const {
-    std::vector<hipblasLtMatmulHeuristicResult_t> cand(static_cast<size_t>(count));
-    int                                           n = 0;
-    lt_ok(hipblasLtMatmulAlgoGetHeuristic(h, op_, w_, x_, out_, out_, pref_, count, cand.data(), &n), "heuristic");
-    for (int i = 0; i < n; ++i) {
-        std::string kn = hipblaslt_ext::getKernelNameFromAlgo(h, cand[size_t(i)].algo);
-        if (!stream_k_kernel(kn)) {
-            *pick = cand[size_t(i)];
-            *name = std::move(kn);
-            return true;
-        }
     }
     return false;
 }
@@ -182,7 +176,7 @@ public:
 
     std::string name() const override { return streams_ > 1 ? "hipblaslt_loop" : "hipblaslt_seq"; }
 
-    std::string prepare(const GroupedGemmProblem &p, hipStream_t) override {
+    std::string prepare(const GroupedGemmProblem &p, hipStream_t stream) override {
         if (p.group_lens_pinned == nullptr)
             return "needs the group lengths in pinned host memory";
         if (int64_t(p.group_m.size()) != p.group_num)
@@ -190,24 +184,26 @@ public:
                                      std::to_string(p.group_num) + " groups");
         problem_ = p;
         kernels_.clear();
+        picks_.clear();
         std::set<int64_t> sizes(p.group_m.begin(), p.group_m.end());
         for (const int64_t m : sizes) {
             if (m <= 0)
                 continue;
-            const GroupMatmul                mm(lt_type(p.dtype), p.n, m, p.k, kLoopWorkspace);
-            hipblasLtMatmulHeuristicResult_t pick{};
-            std::string                      kn;
-            if (streams_ > 1) {
-                if (!mm.choose_without_stream_k(handles_[0], kCandidates, &pick, &kn))
-                    return "N/A: hipBLASLt offers only stream-K kernels for groups of " + std::to_string(m) +
-                           " rows (its first " + std::to_string(kCandidates) + " choices), and stream-K kernels on " +
-                           std::to_string(streams_) +
-                           " streams at once can deadlock (each waits on workgroups that need the whole GPU); "
-                           "hipblaslt_seq runs the same kernels one at a time";
-            } else {
-                pick = mm.choose(handles_[0]);
-                kn   = hipblaslt_ext::getKernelNameFromAlgo(handles_[0], pick.algo);
+            const GroupMatmul                      mm(lt_type(p.dtype), p.n, m, p.k, kLoopWorkspace);
+            const hipblasLtMatmulHeuristicResult_t first = mm.choose(handles_[0]);
+            hipblasLtMatmulAlgo_t                  algo  = first.algo;
+            std::string kn = hipblaslt_ext::getKernelNameFromAlgo(handles_[0], algo);
+            Pick        pick{hipblaslt_ext::getIndexFromAlgo(algo), false, first.algo};
+            if (streams_ > 1 && stream_k_kernel(kn)) {
+                std::string why;
+                if (!fastest_without_stream_k(p, m, mm, stream, &pick.kept, &kn, &why))
+                    return "N/A: no hipBLASLt kernel other than stream-K supports groups of " + std::to_string(m) +
+                           " rows (" + why + "), and stream-K kernels on " + std::to_string(streams_) +
+                           " streams at once can deadlock (each waits on workgroups that need the whole GPU)";
+                pick.replaced = true;
+                kn += " (timed pick: the heuristic's first choice is stream-K)";
             }
+            picks_[m] = pick;
             kernels_ += (kernels_.empty() ? "" : "; ") + kn;
         }
         return "";
@@ -228,16 +224,27 @@ public:
             const int64_t m = p.group_lens_pinned[g]; // read on the host each call
             if (m <= 0)
                 continue;
-            const int         s  = used++ % streams_;
-            const hipStream_t st = s == 0 ? stream : side_[size_t(s)];
+            const int                        s  = used++ % streams_;
+            const hipStream_t                st = s == 0 ? stream : side_[size_t(s)];
+            const hipblasLtHandle_t          h  = handles_[size_t(s)];
             const GroupMatmul                mm(t, p.n, m, p.k, kLoopWorkspace);
-            hipblasLtMatmulHeuristicResult_t pick{};
-            std::string                      kn;
-            if (streams_ == 1)
-                pick = mm.choose(handles_[0]);
-            else if (!mm.choose_without_stream_k(handles_[size_t(s)], kCandidates, &pick, &kn))
-                throw std::runtime_error("no kernel other than stream-K for a group (it had one in prepare)");
-            mm.launch(handles_[size_t(s)], pick.algo, static_cast<const char *>(p.w) + size_t(g) * p.n * p.k * es,
+            hipblasLtMatmulHeuristicResult_t pick = mm.choose(h); // the heuristic, every call
+            if (streams_ > 1) {
+                // a stream-K first choice never runs on the 4 streams: the kernel timed in
+                // prepare() for this group size replaces it
+                const auto it = picks_.find(m);
+                if (it == picks_.end())
+                    throw std::runtime_error("group of " + std::to_string(m) + " rows: sizes changed since prepare()");
+                if (hipblaslt_ext::getIndexFromAlgo(pick.algo) != it->second.first_index &&
+                    stream_k_kernel(hipblaslt_ext::getKernelNameFromAlgo(h, pick.algo)))
+                    throw std::runtime_error("the heuristic changed its stream-K choice since prepare()");
+                if (it->second.replaced) {
+                    pick.algo = it->second.kept;
+                    if (!mm.supports(h, pick.algo))
+                        throw std::runtime_error("the kept kernel no longer supports the group");
+                }
+            }
+            mm.launch(h, pick.algo, static_cast<const char *>(p.w) + size_t(g) * p.n * p.k * es,
                       static_cast<const char *>(p.x) + size_t(row) * p.k * es,
                       static_cast<char *>(p.out) + size_t(row) * p.n * es,
                       static_cast<char *>(workspace_) + size_t(s) * kLoopWorkspace, st);
@@ -255,7 +262,82 @@ public:
     }
 
 private:
-    static constexpr int           kCandidates = 16; // heuristic results searched for a non-stream-K kernel
+    // Per group size: the heuristic's first choice (its solution index) and, when that is
+    // stream-K, the kernel that replaces it on the 4 streams.
+    struct Pick {
+        int                   first_index = -1;
+        bool                  replaced    = false;
+        hipblasLtMatmulAlgo_t kept{};
+    };
+
+    // The fastest kernel that is not stream-K among all the library's kernels that support one
+    // group of m rows within the workspace limit: each is launched once untimed and twice timed
+    // on the caller's stream, reading the problem's x and w (group 0's rows and weights) and
+    // writing a scratch output. False (with *why) if none supports the group or every launch fails.
+    bool fastest_without_stream_k(const GroupedGemmProblem &p, int64_t m, const GroupMatmul &mm, hipStream_t stream,
+                                  hipblasLtMatmulAlgo_t *best, std::string *name, std::string *why) {
+        const hipDataType t = lt_type(p.dtype);
+        auto             &all = all_algos_[int(t)];
+        if (all.empty())
+            lt_ok(hipblaslt_ext::getAllAlgos(handles_[0], hipblaslt_ext::GemmType::HIPBLASLT_GEMM, HIPBLAS_OP_T,
+                                             HIPBLAS_OP_N, t, t, t, t, HIPBLAS_COMPUTE_32F, all),
+                  "all algorithms");
+        std::vector<hipblasLtMatmulAlgo_t> cand;
+        for (const auto &r : all) {
+            hipblasLtMatmulAlgo_t a = r.algo;
+            if (mm.supports(handles_[0], a) && !stream_k_kernel(hipblaslt_ext::getKernelNameFromAlgo(handles_[0], a)))
+                cand.push_back(a);
+        }
+        if (cand.empty()) {
+            *why = std::to_string(all.size()) + " kernels checked";
+            return false;
+        }
+        const size_t es   = dtype_bytes(p.dtype);
+        void        *out  = nullptr;
+        hipEvent_t   e[2] = {nullptr, nullptr};
+        hip_ok(hipMalloc(&out, size_t(m) * size_t(p.n) * es), "scratch output");
+        float best_ms = -1.0f;
+        try {
+            for (auto &ev : e)
+                hip_ok(hipEventCreate(&ev), "timing event");
+            for (auto &a : cand) {
+                try {
+                    mm.launch(handles_[0], a, p.w, p.x, out, workspace_, stream);
+                    hip_ok(hipEventRecord(e[0], stream), "timing event");
+                    for (int r = 0; r < 2; ++r)
+                        mm.launch(handles_[0], a, p.w, p.x, out, workspace_, stream);
+                    hip_ok(hipEventRecord(e[1], stream), "timing event");
+                    hip_ok(hipEventSynchronize(e[1]), "timing sync");
+                } catch (const std::runtime_error &) {
+                    hip_ok(hipStreamSynchronize(stream), "timing sync");
+                    continue; // a kernel that fails to launch is not a candidate
+                }
+                float ms = 0.0f;
+                hip_ok(hipEventElapsedTime(&ms, e[0], e[1]), "timing");
+                if (best_ms < 0.0f || ms < best_ms) {
+                    best_ms = ms;
+                    *best   = a;
+                }
+            }
+        } catch (...) {
+            for (auto ev : e)
+                if (ev != nullptr)
+                    (void)hipEventDestroy(ev);
+            (void)hipFree(out);
+            throw;
+        }
+        for (auto ev : e)
+            (void)hipEventDestroy(ev);
+        hip_ok(hipFree(out), "scratch output");
+        if (best_ms < 0.0f) {
+            *why = std::to_string(cand.size()) + " candidates failed to launch";
+            return false;
+        }
+        *name = hipblaslt_ext::getKernelNameFromAlgo(handles_[0], *best) + ", fastest of " + std::to_string(cand.size()) +
+                " non-stream-K kernels (" + std::to_string(best_ms / 2.0f) + " ms)";
+        return true;
+    }
+
     const int                      streams_;
     const int                      slots_;
     std::vector<hipblasLtHandle_t> handles_;
@@ -264,6 +346,8 @@ private:
     void                          *workspace_ = nullptr;
     GroupedGemmProblem             problem_;
     std::string                    kernels_;
+    std::map<int64_t, Pick>        picks_;     // per group size (4-stream mode)
+    std::map<int, std::vector<hipblasLtMatmulHeuristicResult_t>> all_algos_; // getAllAlgos, per data type
 };
 
 // ---------------------------------------------------------------------------------------

@@ -9,7 +9,10 @@
 //     with empty groups owning nothing, and each workgroup's logical tiles only increase;
 //   * active_rows: for every tile size (1..256 valid rows and columns, both row mappings) each
 //     16 x 16 block that holds a valid output belongs to exactly one wave's active row blocks,
-//     and every active block holds a valid row (no MFMA skipped that a stored output needs).
+//     and every active block holds a valid row (no MFMA skipped that a stored output needs);
+//   * desc_rows_fit: tile descriptors (32-bit first rows) are refused when a wgrad plan's input
+//     tokens pass 2^31 although its output rows (group_num * N) are few, and accepted when every
+//     group's first token from build_group_table fits.
 #include <cstdio>
 #include <cstdlib>
 #include <set>
@@ -174,7 +177,35 @@ static void check_short(const std::vector<int64_t> &group_m, int64_t n, int want
     check_walk(group_m, n, 24, 8, 0, rows);
 }
 
+// Descriptor row guard on a synthetic group list (no device memory: the sizes are only summed).
+static void check_desc_rows() {
+    // wgrad with n = k = 8: one 8 x 8 output tile per group, 20 groups of 2^27 tokens
+    const std::vector<int64_t> big(20, int64_t(1) << 27);
+    std::vector<gg::GroupEntry> table(big.size());
+    const int64_t tiles = gg::build_group_table(big.data(), int(big.size()), 1, table.data(), 8);
+    CHECK(tiles == 20, "wgrad table of 20 groups: %lld tiles", (long long)tiles);
+    CHECK(table.back().row0 > INT32_MAX, "the last group's first token passes 2^31");
+    CHECK(!gg::desc_rows_fit(big.data(), int(big.size()), 20 * 8), "wgrad tokens past 2^31 must not use descriptors");
+    // the same groups up to the largest count whose tokens fit: every first token fits too
+    const std::vector<int64_t> fits(15, int64_t(1) << 27); // 15 * 2^27 = 2^31 - 2^27
+    std::vector<gg::GroupEntry> t2(fits.size());
+    gg::build_group_table(fits.data(), int(fits.size()), 1, t2.data(), 8);
+    CHECK(gg::desc_rows_fit(fits.data(), int(fits.size()), 15 * 8), "15 x 2^27 tokens fit");
+    for (const auto &e : t2)
+        CHECK(e.row0 <= INT32_MAX, "first token %lld", (long long)e.row0);
+    // one token short of / at the limit, and forward plans bounded by their output rows
+    const std::vector<int64_t> edge{INT32_MAX - 1};
+    CHECK(gg::desc_rows_fit(edge.data(), 1, INT32_MAX - 1), "2^31 - 2 rows fit");
+    const std::vector<int64_t> at{INT32_MAX};
+    CHECK(!gg::desc_rows_fit(at.data(), 1, 8), "2^31 - 1 tokens do not");
+    CHECK(!gg::desc_rows_fit(edge.data(), 1, INT32_MAX), "2^31 - 1 output rows do not");
+    const std::vector<int64_t> neg{5, -1};
+    CHECK(!gg::desc_rows_fit(neg.data(), 2, 4), "negative sizes are refused");
+    CHECK(gg::desc_rows_fit(nullptr, 0, 0), "an empty plan fits");
+}
+
 int main() {
+    check_desc_rows();
     check_short(std::vector<int64_t>(32, 520), 2880, 176); // config 5a: 3 x 176 instead of 256 + 256 + 8
     check_short({300, 0, 260, 130}, 1000, 160);
     check_short({100, 7, 1}, 264, 112);

@@ -76,14 +76,21 @@ def _stream_k(name):
 
 
 def test_four_stream_loop_runs_no_stream_k_kernel(tmp_path):
-    """hipblaslt_loop takes the heuristic's best non-stream-K kernel (stream-K kernels wait on each
-    other's workgroups and must have the GPU to themselves); hipblaslt_seq keeps the first choice."""
+    """hipblaslt_loop never runs a stream-K kernel on its 4 streams (stream-K kernels wait on each
+    other's workgroups and must have the GPU to themselves): where the heuristic's first choice is
+    stream-K it launches the fastest other kernel, timed in prepare(). Every loop row must be
+    measured (PASS with named kernels), so this cannot pass on N/A rows; hipblaslt_seq keeps the
+    heuristic's first choice."""
     out = tmp_path / "rows.csv"
     r = _run([os.path.join(PKG, "bin", "gg_bench"), "--shapes", SHAPES, "--only", "1001,1005,1006", "--backends",
               "hipblaslt_loop,hipblaslt_seq", "--warmup", "1", "--iters", "3", "--out", str(out)])
     assert r.returncode == 0, r.stderr
-    for row in _rows(out):
-        assert row["Check"] in ("PASS", "N/A"), row
+    rows = _rows(out)
+    loop = [row for row in rows if row["Backend"] == "hipblaslt_loop"]
+    assert len(loop) == 3, rows
+    for row in rows:
+        assert row["Check"] == "PASS", row
+        assert float(row["TFLOPS"]) > 0, row
+    for row in loop:
         kernels = re.findall(r"Cijk_\w+", row["Detail"])
-        if row["Backend"] == "hipblaslt_loop" and row["Check"] == "PASS":
-            assert kernels and not any(_stream_k(kn) for kn in kernels), row["Detail"]
+        assert kernels and not any(_stream_k(kn) for kn in kernels), row["Detail"]
