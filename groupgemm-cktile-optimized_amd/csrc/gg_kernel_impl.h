@@ -423,6 +423,133 @@ static_assert(Plan8<2, 2>::check() && Plan8<2, 4>::check() && Plan8<4, 4>::check
 static_assert(Plan8<2, 2>::vm_at_barrier() == 7, "fp8 forward plan unchanged");
 static_assert(Plan<2, 2>::bar == GG_BAR_IDX, "forward plan keeps the tuned barrier slot");
 
+// Front-loaded slot plan of a full 16-bit K-major step (8 rows of 16 MFMAs, idx = kh * 8 + ni),
+// selected by GG_PLAN=1. Each gap holds at most one memory operation, reads and DMAs in any gap:
+// - the w fragments of step kt+1 in rows 0-3 (blocks 2 mi and 2 mi + 1 after MFMAs 6, 10, 12,
+//   14 of rows 0-2; blocks 6 and 7 after MFMAs 3, 5, 6, 7 of row 3);
+// - the x fragments of row mi+1 after MFMAs 2 and 4 of row mi;
+// - A(kt+1) DMAs 2-7 after MFMAs 8 and 13 of row 0 and 0, 5, 8, 13 of row 1;
+// - B(kt+3) DMAs after MFMAs 1 and 9 of rows 4-7;
+// - the barrier after MFMA 10 of row 7, then row 0 of the next step's x (after MFMAs 11, 13)
+//   and the early A(kt+2) DMAs 0-1 (after MFMAs 12, 14);
+// - a cross tile's first step: the previous tile's row block mi+1 in four stores at the free
+//   slots of row mi (epi_slot).
+// A(kt+1) then has 5.5 rows to land before the barrier instead of 4.5, and the w reads are done
+// before the B DMAs start.
+struct PlanFront {
+    static constexpr int NA = 2, NB = 2;
+    static constexpr int rows = 8, last = 7, slots = 16, nc = 8, early = kEarlyA, bar = 10;
+    static constexpr int la = kLoads, lb = kLoads;
+    static constexpr int read_a_next(int mi, int idx) { return (mi < last && (idx == 2 || idx == 4)) ? idx / 4 : -1; }
+    static constexpr int b_q(int mi, int idx) { // (block << 1) | read, or -1
+        if (mi < 3) {
+            const int q = idx == 6 ? 0 : idx == 10 ? 1 : idx == 12 ? 2 : idx == 14 ? 3 : -1;
+            return q < 0 ? -1 : ((2 * mi + q / 2) << 1) | (q & 1);
+        }
+        if (mi == 3) {
+            const int q = idx == 3 ? 0 : idx == 5 ? 1 : idx == 6 ? 2 : idx == 7 ? 3 : -1;
+            return q < 0 ? -1 : ((6 + q / 2) << 1) | (q & 1);
+        }
+        return -1;
+    }
+    static constexpr int read_b_next(int mi, int idx) { return b_q(mi, idx) >= 0 ? b_q(mi, idx) & 1 : -1; }
+    static constexpr int read_b_blk(int mi, int idx) { return b_q(mi, idx) >= 0 ? b_q(mi, idx) >> 1 : -1; }
+    static constexpr int read_a_row0(int mi, int idx) {
+        return mi == last ? (idx == bar + 1 ? 0 : idx == bar + 3 ? 1 : -1) : -1;
+    }
+    static constexpr int load_a(int mi, int idx) {
+        if (mi == 0)
+            return idx == 8 ? 2 : idx == 13 ? 3 : -1;
+        if (mi == 1)
+            return idx == 0 ? 4 : idx == 5 ? 5 : idx == 8 ? 6 : idx == 13 ? 7 : -1;
+        return -1;
+    }
+    static constexpr int load_b(int mi, int idx) {
+        return (mi >= 4 && (idx == 1 || idx == 9)) ? 2 * (mi - 4) + idx / 8 : -1;
+    }
+    static constexpr int load_a_early(int mi, int idx) {
+        return mi == last ? (idx == bar + 2 ? 0 : idx == bar + 4 ? 1 : -1) : -1;
+    }
+    static constexpr int epi_slot(int mi, int s) { // four free slots of each row 0-6, in order
+        constexpr int lo[4] = {1, 3, 7, 11}, r3[4] = {1, 9, 11, 13}, hi[4] = {3, 7, 11, 13};
+        return mi < 3 ? lo[s] : mi == 3 ? r3[s] : hi[s];
+    }
+    static constexpr int epi(int mi, int idx) {
+        if (mi >= last)
+            return -1;
+        for (int s = 0; s < 4; ++s)
+            if (epi_slot(mi, s) == idx)
+                return s;
+        return -1;
+    }
+    static constexpr int dma_kind(int mi, int idx) {
+        return load_a(mi, idx) >= 0 ? 1 : load_b(mi, idx) >= 0 ? 2 : load_a_early(mi, idx) >= 0 ? 3 : 0;
+    }
+    static constexpr int dma_j(int mi, int idx) {
+        return load_a(mi, idx) >= 0 ? load_a(mi, idx) : load_b(mi, idx) >= 0 ? load_b(mi, idx) : load_a_early(mi, idx);
+    }
+    static constexpr int vm_at_barrier() { // loads issued after A(kt+1)'s last DMA, as in Plan
+        int last_a = -1;
+        for (int p = 0; p < rows * slots; ++p)
+            if (load_a(p / slots, p % slots) >= 0)
+                last_a = p;
+        int n = 0;
+        for (int p = last_a + 1; p < last * slots + bar; ++p)
+            n += (load_b(p / slots, p % slots) >= 0) + (load_a_early(p / slots, p % slots) >= 0);
+        return n;
+    }
+    template <typename F> static constexpr int count(F f) {
+        int n = 0;
+        for (int p = 0; p < rows * slots; ++p)
+            n += f(p / slots, p % slots) >= 0;
+        return n;
+    }
+    static constexpr bool check() {
+        int per_block[nc] = {};
+        int per_row_epi[rows] = {};
+        int a_seen = kEarlyA;
+        for (int p = 0; p < rows * slots; ++p) {
+            const int mi = p / slots, idx = p % slots;
+            const int ops = (load_a(mi, idx) >= 0) + (load_b(mi, idx) >= 0) + (load_a_early(mi, idx) >= 0) +
+                            (read_a_next(mi, idx) >= 0) + (read_b_next(mi, idx) >= 0) +
+                            (read_a_row0(mi, idx) >= 0) + (epi(mi, idx) >= 0);
+            if (ops > 1)
+                return false;
+            // every w read of step kt+1 and every A(kt+1) DMA precede the barrier; row 0 of x
+            // and the early A(kt+2) DMAs follow it
+            if (p >= last * slots + bar && (read_b_next(mi, idx) >= 0 || load_a(mi, idx) >= 0))
+                return false;
+            if (p <= last * slots + bar && (read_a_row0(mi, idx) >= 0 || load_a_early(mi, idx) >= 0))
+                return false;
+            if (load_a(mi, idx) >= 0 && load_a(mi, idx) != a_seen++)
+                return false;
+            if (read_b_next(mi, idx) >= 0) {
+                const int b = read_b_blk(mi, idx);
+                if (b < 0 || b >= nc || read_b_next(mi, idx) != per_block[b])
+                    return false;
+                ++per_block[b];
+            }
+            if (epi(mi, idx) >= 0) {
+                if (epi(mi, idx) != per_row_epi[mi])
+                    return false;
+                ++per_row_epi[mi];
+            }
+        }
+        for (int b = 0; b < nc; ++b)
+            if (per_block[b] != NB)
+                return false;
+        for (int r = 0; r < last; ++r)
+            if (per_row_epi[r] != 4)
+                return false;
+        return count(load_a) == la - early && count(load_b) == lb && count(load_a_early) == early &&
+               count(read_b_next) == nc * NB && count(read_a_next) == last * NA && count(read_a_row0) == NA;
+    }
+};
+static_assert(PlanFront::check() && PlanFront::vm_at_barrier() == 8, "front-loaded slot plan");
+#ifndef GG_PLAN
+#define GG_PLAN 1 // slot plan of full 16-bit K-major steps: 0 Plan<2, 2>, 1 PlanFront
+#endif
+
 // Slot plan of a short-wide tile (at most 192 rows x 288 columns, 16-bit forward, K-major
 // operands): 6 rows of 18 MFMAs per wave (9 column blocks, idx = kh * 9 + ni), A stages of 192
 // rows (6 DMAs per wave) and B stages of 288 rows (9 DMAs per wave).
@@ -839,8 +966,11 @@ grouped_gemm_kernel(const KernelArgs args) {
     // variant: with one tile per workgroup (the per-tile variant's usual case) the full tiles set
     // the launch time whatever the partial ones save, and the per-tile instances stay smaller.
     constexpr bool kThin  = kTailSkip && CROSS;
-    using P = std::conditional_t<F8, Plan8<reads_per_frag(A_MN), reads_per_frag(B_MN)>,
-                                 std::conditional_t<SWIDE, PlanSW, Plan<reads_per_frag(A_MN), reads_per_frag(B_MN), RB>>>;
+    constexpr bool FRONT = GG_PLAN == 1 && !F8 && !SWIDE && !A_MN && !B_MN && RB == 8;
+    using P = std::conditional_t<
+        F8, Plan8<reads_per_frag(A_MN), reads_per_frag(B_MN)>,
+        std::conditional_t<SWIDE, PlanSW,
+                           std::conditional_t<FRONT, PlanFront, Plan<reads_per_frag(A_MN), reads_per_frag(B_MN), RB>>>>;
     static_assert(!SWIDE || (NBLK == P::nc && RB == P::rows), "short-wide plan");
     constexpr int NC   = P::nc;                                     // column blocks in the registers
     constexpr int A_ST = P::la * kWaves * 1024;                     // bytes of an A stage
