@@ -373,3 +373,35 @@ def test_fill_randn_is_standard_normal(oracle, dt):
     assert stats.kstest(v, "norm").statistic < 0.01
     assert np.array_equal(oracle.fill_randn(dt, 1000, 1), oracle.fill_randn(dt, 4000, 1)[:1000])
     assert not np.array_equal(oracle.fill_randn(dt, 1000, 1), oracle.fill_randn(dt, 1000, 2))
+
+
+# Closed forms of the Box-Muller stage (bench_main.cpp:171-173). With r the splitmix64 output:
+# a 24-bit u2 field ((r >> 16) & 0xFFFFFF) of 0 gives cos(0) = 1, so the value is
+# +sqrt(-2 ln u1); a u2 field of 0x800000 gives cos(pi) = -1, so -sqrt(-2 ln u1); r >> 40 ==
+# 0xFFFFFF gives u1 = 1 exactly (the float 1/16777217 rounds to 2^-24), so a signed zero.
+# u1 = ((r >> 40) + 1) * 2^-24 is exact in float. The indices were found by scanning the fill's
+# splitmix64 inputs (seed ^ i * 0x2545F4914F6CDD1D) once; each case's condition is re-derived
+# here through the pinned splitmix64 stage. Swapped bit fields, sin for cos, a lost sign or
+# (r >> 40) without the + 1 each fail one of them.
+BOX_MULLER_CASES = [(1, 10663227, "cos_one"), (2, 14069789, "cos_minus_one"), (2, 1888246, "u1_one")]
+
+
+@pytest.mark.parametrize("dt", [0, 1])
+def test_fill_box_muller_closed_forms(oracle, dt):
+    c, mask = 0x2545F4914F6CDD1D, (1 << 64) - 1
+    for seed, i, case in BOX_MULLER_CASES:
+        r = oracle.splitmix64(seed ^ ((i * c) & mask))
+        u2_field, hi = (r >> 16) & 0xFFFFFF, r >> 40
+        u1 = (hi + 1) / float(1 << 24)
+        got = int(oracle.fill_randn(dt, i + 1, seed)[i])
+        if case == "u1_one":
+            assert hi == 0xFFFFFF
+            assert got & 0x7FFF == 0, hex(got)  # +0 or -0
+            continue
+        assert u2_field == (0 if case == "cos_one" else 0x800000)
+        v = np.float32((1.0 if case == "cos_one" else -1.0) * np.sqrt(-2.0 * np.log(u1)))
+        if dt == 0:
+            want = int(torch.tensor([v]).to(torch.bfloat16).view(torch.int16).item()) & 0xFFFF
+        else:
+            want = int(np.array([v]).astype(np.float16).view(np.uint16)[0])
+        assert got == want, (case, hex(got), hex(want), float(v))
