@@ -27,12 +27,17 @@ Prints ONE JSON line on stdout. Besides the driver's fields it carries:
                TFLOPS, or its N/A reason or error.
   cpu_baseline the CPU oracle (OpenMP fp32, test infrastructure) timed on a bounded sample
                of the same workload on this host; a reported baseline only.
-  clock_power  gfx clock (MHz) and socket power (W) sampled through amdsmi during a separate
-               sustained window of the same launches after the timed region (--power-seconds,
-               default 1 s; the timed region itself runs without a sampling thread) and that
-               window's TFLOPS; the reference records the same two figures (scripts/power.py:1-9).
-               "consistent" says whether the sampled clock could sustain the measured MFMA rate;
-               only then is the dense peak scaled to it reported.
+  timed_region_clock
+               the effective shader clock of the timed region: the matching profile's GRBM cycles
+               per launch over ms_per_step (null, with the reason, when no profile of this build
+               and plan exists).
+  clock_power  a separate sustained window of the same launches after the timed region
+               (--power-seconds, default 1 s; the timed region itself runs without probe or
+               sampling thread): its TFLOPS, its effective shader clock from the clock probe (one
+               wave beside the GEMM reading s_memtime against s_memrealtime) with the dense peak
+               scaled to that clock, and amdsmi's gfx clock and socket power, the two figures the
+               reference records (scripts/power.py:1-9); amdsmi's clock is marked inconsistent
+               when it is more than 5 % off the probe's.
 Human-readable progress goes to stderr.
 """
 from __future__ import annotations
@@ -233,43 +238,67 @@ def peak_of(op):
     return FP8_PEAK_TFLOPS if "fp8" in op else MFMA_PEAK_TFLOPS
 
 
-def sustained_clock_power(be, sh, stream, flops, ms, seconds, peak):
-    """Run the same launch back to back for about `seconds` while a background thread samples
-    the gfx clock and socket power (amdsmi). Returns the samples' means, this window's TFLOPS and
-    the dense peak scaled to the sampled clock (peak x MHz / 2400)."""
+def sustained_clock_power(pkg, be, sh, stream, flops, ms, seconds, peak):
+    """Run the same launch back to back for about `seconds`. The effective shader clock over the
+    window comes from the clock probe (gg_clock_probe: one wave on a second stream reading
+    s_memtime against s_memrealtime over the first 70 % of the window; it holds a few VGPRs and
+    no LDS, so the GEMM's workgroups run beside it). A background thread samples amdsmi's gfx clock
+    and socket power meanwhile. Returns the window's TFLOPS, the probe's clock and the dense peak
+    scaled to it (peak x MHz / 2400), and the amdsmi readings, whose clock is flagged inconsistent
+    when it differs from the probe's by more than 5 %."""
     import torch
 
     power = entry.load_submodule("power")
     sampler = power.PowerSampler(0)
     n = max(1, int(seconds / max(ms * 1e-3, 1e-6)))
+    words = torch.zeros(5, dtype=torch.int64, device=stream.device)
+    side = torch.cuda.Stream(device=stream.device)  # default priority
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
     with sampler:
+        # the probe first, so that it is resident before the GEMM's workgroups arrive
+        pkg.clock_probe(words.data_ptr(), 0.7 * n * ms * 1e-3, side.cuda_stream)
         t0.record(stream)
         for _ in range(n):
             be.run(sh)
         t1.record(stream)
         torch.cuda.synchronize()
     sampler.close()
-    res = sampler.summary()
+    smi = sampler.summary()
     w_ms = t0.elapsed_time(t1)
-    res["steps"] = n
-    res["seconds"] = round(w_ms * 1e-3, 3)
-    res["tflops"] = round(flops * n / (w_ms * 1e-3) / 1e12, 2)
-    res["power_cap_w"] = sampler.power_cap_w
-    mhz = res.get("gfx_mhz")
-    # The readings are only kept as measured when they could be true: the window's TFLOPS may not
-    # exceed the dense peak scaled to the sampled clock (peak x MHz / 2400). On this pool's boxes
-    # amdsmi's clock and power often do not follow the load (readings of a few hundred MHz under a
-    # full-rate GEMM); the effective clock over a launch comes from the GRBM cycle counters
-    # instead (rocprofv3 --pmc GRBM_GUI_ACTIVE, profiles/).
-    res["consistent"] = bool(mhz) and res["tflops"] <= peak * mhz / 2400.0
-    if res["consistent"]:
-        at_clk = peak * mhz / 2400.0
-        res["peak_at_clock_tflops"] = round(at_clk, 1)
-        res["frac_at_clock"] = round(res["tflops"] / at_clk, 4)
-    res["source"] = "amdsmi: clock_info(GFX).clk, power_info.current_socket_power, gpu_metrics current_gfxclks"
+    mask = (1 << 64) - 1
+    mhz = pkg.probe_mhz([int(v) & mask for v in words.cpu().tolist()])
+    res = {"steps": n, "seconds": round(w_ms * 1e-3, 3),
+           "tflops": round(flops * n / (w_ms * 1e-3) / 1e12, 2),
+           "gfx_mhz": round(mhz, 1),
+           "gfx_mhz_source": "clock probe: shader clock counter (s_memtime) over the wall clock (s_memrealtime) "
+                             "of one wave on a second stream, the window's first 70 %",
+           "peak_at_clock_tflops": round(peak * mhz / 2400.0, 1),
+           "frac_at_clock": round(flops * n / (w_ms * 1e-3) / 1e12 / (peak * mhz / 2400.0), 4),
+           "socket_w": smi.get("socket_w"), "socket_w_max": smi.get("socket_w_max"),
+           "power_cap_w": sampler.power_cap_w}
+    a_mhz = smi.get("gfx_mhz")
+    smi["consistent_with_probe"] = bool(a_mhz) and abs(a_mhz - mhz) <= 0.05 * mhz
+    smi["source"] = "amdsmi: clock_info(GFX).clk, power_info.current_socket_power, gpu_metrics current_gfxclks"
+    res["amdsmi"] = smi
     return res
+
+
+def timed_region_clock(ms, traffic_profile_status, workload, op):
+    """Effective clock of the timed region: the GRBM cycles per launch of the matching profile
+    (same kernel sources and plan) over this run's mean launch time; None with the reason if the
+    profile does not match."""
+    suffix = "" if op == "fwd" else f"_{op}"
+    rel = os.path.join("profiles", f"hbm_traffic_{workload}{suffix}.json")
+    if not traffic_profile_status.startswith("current"):
+        return {"gfx_mhz": None, "reason": f"{rel} was not measured on this build's kernel sources and plan"}
+    with open(os.path.join(ROOT, rel)) as f:
+        cycles = json.load(f).get("cycles_per_launch")
+    if not cycles:
+        return {"gfx_mhz": None, "reason": f"{rel} holds no cycles_per_launch"}
+    return {"gfx_mhz": round(cycles / (ms * 1e-3) / 1e6, 1), "cycles_per_launch": cycles,
+            "source": f"GRBM_GUI_ACTIVE per XCD from {rel} over this run's ms_per_step"}
 
 
 def main():
@@ -361,11 +390,13 @@ def main():
 
     clock_power = None
     if args.power_seconds > 0:
-        clock_power = sustained_clock_power(be, sh, stream, flops, ms, args.power_seconds, peak_of(args.op))
+        clock_power = sustained_clock_power(pkg, be, sh, stream, flops, ms, args.power_seconds, peak_of(args.op))
         log(f"[bench] sustained {clock_power.get('seconds')} s: {clock_power.get('tflops')} TFLOPS at "
-            f"{clock_power.get('gfx_mhz')} MHz, {clock_power.get('socket_w')} W")
+            f"{clock_power.get('gfx_mhz')} MHz (probe; amdsmi {clock_power['amdsmi'].get('gfx_mhz')} MHz), "
+            f"{clock_power.get('socket_w')} W")
 
     traffic, traffic_profile = traffic_for(pkg, args.workload, args.op, plan_detail)
+    timed_clock = timed_region_clock(ms, traffic_profile.get("status", ""), args.workload, args.op)
 
     cpu = None
     if not args.no_cpu_baseline and args.op == "fwd":
@@ -402,6 +433,7 @@ def main():
         "traffic_profile": traffic_profile,
         "baselines": baselines,
         "cpu_baseline": cpu,
+        "timed_region_clock": timed_clock,
         "clock_power": clock_power,
     }
     print(json.dumps(line), flush=True)

@@ -38,6 +38,7 @@ C_API = {
     "gg_last_error": (ctypes.c_char_p, []),
     "gg_fill_randn": (ctypes.c_int, [ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint64,
                                      ctypes.c_void_p]),
+    "gg_clock_probe": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_double, ctypes.c_void_p]),
     "gg_prepare_device_lens": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_int64,
                                               ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
                                               ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
@@ -510,6 +511,20 @@ def make_backend(name: str) -> Backend:
 def fill_randn(dtype: DType, ptr: int, count: int, seed: int, stream: int = 0) -> None:
     """Seeded N(0,1) device fill of the benchmark driver (bench/bench_main.cpp:160-176)."""
     _check(load_library().gg_fill_randn(int(dtype), ptr, count, seed, stream))
+
+
+def clock_probe(dev_out: int, seconds: float, stream: int = 0) -> None:
+    """Enqueue the clock probe (gg_clock_probe): after it ran, the five uint64 at dev_out are the
+    shader clock counter and the wall clock at its start and end, and the wall clock's rate in Hz."""
+    _check(load_library().gg_clock_probe(dev_out, float(seconds), stream))
+
+
+def probe_mhz(words) -> float:
+    """Effective shader clock (MHz) from the five words clock_probe wrote."""
+    c0, t0, c1, t1, hz = (int(v) for v in words)
+    if t1 <= t0 or hz <= 0:
+        raise ValueError("clock probe: no wall-clock ticks elapsed")
+    return (c1 - c0) / ((t1 - t0) / hz) / 1e6
 
 
 def _backward_shapes(kind, grad_out, other, group_m, device_sizes):

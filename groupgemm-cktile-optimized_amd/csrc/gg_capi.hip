@@ -1285,4 +1285,27 @@ int gg_fill_randn(int dtype, void *p, size_t count, uint64_t seed, void *stream)
     return GG_OK;
 }
 
+int gg_clock_probe(uint64_t *dev_out, double seconds, void *stream) {
+    g_last_error.clear();
+    if (dev_out == nullptr)
+        return fail(GG_ERR_INVALID, "dev_out is null");
+    if (!(seconds > 0.0 && seconds <= 10.0))
+        return fail(GG_ERR_INVALID, "seconds must be in (0, 10]");
+    int        dev = 0, khz = 0;
+    hipError_t e   = hipGetDevice(&dev);
+    if (e == hipSuccess)
+        e = hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev);
+    if (e != hipSuccess)
+        return hip_fail(e, "wall clock rate");
+    if (khz <= 0)
+        return fail(GG_ERR_UNSUPPORTED, "the device reports no wall clock rate");
+    const unsigned long long hz    = static_cast<unsigned long long>(khz) * 1000ull;
+    const unsigned long long ticks = static_cast<unsigned long long>(seconds * static_cast<double>(hz));
+    e = gg::launch_clock_probe(reinterpret_cast<unsigned long long *>(dev_out), ticks, hz,
+                               static_cast<hipStream_t>(stream));
+    if (e != hipSuccess)
+        return hip_fail(e, "clock probe launch");
+    return GG_OK;
+}
+
 } // extern "C"

@@ -160,5 +160,7 @@ hipError_t launch_zero_fill(void *out, size_t bytes, hipStream_t stream);
 
 // Seeded N(0,1) fill (benchmark input generator).
 hipError_t launch_fill_randn(void *p, size_t count, uint64_t seed, bool fp16, hipStream_t stream);
+hipError_t launch_clock_probe(unsigned long long *out, unsigned long long ticks, unsigned long long wall_hz,
+                              hipStream_t stream);
 
 } // namespace gg

@@ -171,6 +171,33 @@ template <bool F16> __global__ void fill_randn_kernel(uint16_t *p, size_t n, uin
     }
 }
 
+// ---------------------------------------------------------------------------------------
+// Clock probe (measurement helper): one wave that sleeps in steps of about 8k cycles until
+// `ticks` of the constant-rate wall clock (s_memrealtime) have passed, and records the shader
+// clock counter (s_memtime) and the wall clock at both ends. Launched beside a long run of the
+// GEMM (it needs a few VGPRs and no LDS, so it shares a CU with a GEMM workgroup), it gives the
+// run's effective shader clock: cycles / ticks * wall_hz. out: c0, t0, c1, t1, wall_hz.
+// ---------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(64) clock_probe_kernel(unsigned long long *out, unsigned long long ticks,
+                                                          unsigned long long wall_hz) {
+    const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+    const unsigned long long c0 = __builtin_readcyclecounter();
+    unsigned long long       t  = t0;
+    while (t - t0 < ticks) {
+        __builtin_amdgcn_s_sleep(127);
+        t = __builtin_amdgcn_s_memrealtime();
+    }
+    const unsigned long long c1 = __builtin_readcyclecounter();
+    const unsigned long long t1 = __builtin_amdgcn_s_memrealtime();
+    if (threadIdx.x == 0) {
+        out[0] = c0;
+        out[1] = t0;
+        out[2] = c1;
+        out[3] = t1;
+        out[4] = wall_hz;
+    }
+}
+
 } // namespace
 
 bool uses_cross_tile(const KernelArgs &args, int grid, int mode) {
@@ -293,6 +320,12 @@ hipError_t launch_zero_fill(void *out, size_t bytes, hipStream_t stream) {
     const size_t blocks = std::min<size_t>((n16 + 255) / 256, 4096);
     hipLaunchKernelGGL(zero_fill_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
                        static_cast<u32x4 *>(out), n16);
+    return hipGetLastError();
+}
+
+hipError_t launch_clock_probe(unsigned long long *out, unsigned long long ticks, unsigned long long wall_hz,
+                              hipStream_t stream) {
+    hipLaunchKernelGGL(clock_probe_kernel, dim3(1), dim3(64), 0, stream, out, ticks, wall_hz);
     return hipGetLastError();
 }
 

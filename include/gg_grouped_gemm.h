@@ -234,6 +234,17 @@ const char *gg_last_error(void);
  */
 int gg_fill_randn(int dtype, void *p, size_t count, uint64_t seed, void *stream);
 
+/*
+ * Clock probe: enqueues one wave on `stream` that waits `seconds` (at most 10) of the device's
+ * constant-rate wall clock and writes five uint64 to dev_out: the shader clock counter
+ * (s_memtime) and the wall clock (s_memrealtime) at its start, the same two at its end, and the
+ * wall clock's rate in Hz. Launched on a second stream beside a long run of gg_run, it gives the
+ * run's effective shader clock, (end - start cycles) / (end - start ticks) * rate. It uses a few
+ * VGPRs and no LDS, so it runs next to a GEMM workgroup. Measurement helper, not part of the op;
+ * the reference samples the clock with amd-smi instead (scripts/power.py:1-9).
+ */
+int gg_clock_probe(uint64_t *dev_out, double seconds, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

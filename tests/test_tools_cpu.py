@@ -158,3 +158,14 @@ def test_pmc_csv_parsing(tmp_path):
     assert pmc.mean_after_first({3: ds[3]}, "FETCH_SIZE") == 100.0
     assert pmc.mean_after_first(ds, "WRITE_SIZE") is None
     assert pmc.instance(kname) == "grouped_gemm_kernel<false, true, 0, 0, false, false>"
+
+
+def test_probe_mhz_arithmetic():
+    """Shader cycles over wall-clock seconds: 1.5e8 cycles in 1e7 ticks of a 100 MHz clock is
+    0.1 s at 1500 MHz; no elapsed ticks is an error."""
+    import __graft_entry__ as entry
+
+    pkg = entry.load_package()
+    assert abs(pkg.probe_mhz([10, 5, 10 + 150_000_000, 5 + 10_000_000, 100_000_000]) - 1500.0) < 1e-9
+    with pytest.raises(ValueError):
+        pkg.probe_mhz([1, 7, 2, 7, 100_000_000])
