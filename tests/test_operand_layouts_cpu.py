@@ -9,7 +9,7 @@ offsets), simulates the DMAs into a 32 KB stage and the reads out of it, and che
   the K-major fragment's order (fp8: lane group q takes 16-byte chunks 2q + (kh ^ (q & 1)),
   16-bit: chunk 4 kh + q), so both operands of an MFMA see the same K order;
 - fp8: every 4 consecutive lanes of a DMA read one 64-byte run of one stored row (the DMA unit's
-  cost is one cycle per 4-lane group and cache line, `bin/gg_micro`);
+  cost is one cycle per 4-lane group and cache line, as a DMA microbenchmark measured);
 - no bank holds more than 2 of a read's 4-byte words (64 banks; 512 bytes per read).
 The transposed reads follow the lane mapping pinned on the GPU: ds_read_b64_tr_b8 gives byte j of
 lane i from byte i%8 of source lane 2j + i/8 of its 16-lane group, ds_read_b64_tr_b16 element j of
