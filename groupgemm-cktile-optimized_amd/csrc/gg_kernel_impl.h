@@ -436,9 +436,12 @@ static_assert(Plan<2, 2>::bar == GG_BAR_IDX, "forward plan keeps the tuned barri
 //   slots of row mi (epi_slot).
 // A(kt+1) then has 5.5 rows to land before the barrier instead of 4.5, and the w reads are done
 // before the B DMAs start.
+// (Measured against it, same box, alternating, GRBM cycles: A(kt+1) after MFMAs 0, 5, 8, 13 of
+// row 0 and 0, 5 of row 1: +1 to +3 %; three early A(kt+2) DMAs: +1.5 to +4 %; the barrier one
+// MFMA later: -0.3 to +2 %.)
 struct PlanFront {
     static constexpr int NA = 2, NB = 2;
-    static constexpr int rows = 8, last = 7, slots = 16, nc = 8, early = kEarlyA, bar = 10;
+    static constexpr int rows = 8, last = 7, slots = 16, nc = 8, early = 2, bar = 10;
     static constexpr int la = kLoads, lb = kLoads;
     static constexpr int read_a_next(int mi, int idx) { return (mi < last && (idx == 2 || idx == 4)) ? idx / 4 : -1; }
     static constexpr int b_q(int mi, int idx) { // (block << 1) | read, or -1
@@ -507,7 +510,7 @@ struct PlanFront {
     static constexpr bool check() {
         int per_block[nc] = {};
         int per_row_epi[rows] = {};
-        int a_seen = kEarlyA;
+        int a_seen = early;
         for (int p = 0; p < rows * slots; ++p) {
             const int mi = p / slots, idx = p % slots;
             const int ops = (load_a(mi, idx) >= 0) + (load_b(mi, idx) >= 0) + (load_a_early(mi, idx) >= 0) +
@@ -545,7 +548,8 @@ struct PlanFront {
                count(read_b_next) == nc * NB && count(read_a_next) == last * NA && count(read_a_row0) == NA;
     }
 };
-static_assert(PlanFront::check() && PlanFront::vm_at_barrier() == 8, "front-loaded slot plan");
+static_assert(PlanFront::check() && PlanFront::vm_at_barrier() == 8 && PlanFront::early == kEarlyA,
+              "front-loaded slot plan");
 #ifndef GG_PLAN
 #define GG_PLAN 1 // slot plan of full 16-bit K-major steps: 0 Plan<2, 2>, 1 PlanFront
 #endif

@@ -217,7 +217,10 @@ int gg_compute_group_offs(const int64_t *group_lens, int64_t *group_offs, int gr
  * overlap on one GPU (other streams, other host threads) race on it; calls on one stream are
  * ordered. An empty contraction zero-fills the output with a kernel (no hipMemsetAsync). Sizes
  * found out of range on the device are not reported (their rows are not written): use a
- * gg_prepare_device_lens_op plan and gg_plan_device_status to check them.
+ * gg_prepare_device_lens_op plan and gg_plan_device_status to check them. The first call on a
+ * device looks up that device's scratch address and properties, so it must run outside stream
+ * capture; later calls may be captured into a HIP graph (they launch kernels only, no
+ * hipMemsetAsync).
  */
 int gg_run_device_lens_noalloc(int op, int a_dtype, int b_dtype, int group_num, int64_t total_m, int64_t n,
                                int64_t k, const int64_t *group_lens, const int64_t *group_offs, const void *a,

@@ -116,3 +116,66 @@ def test_too_many_groups_is_refused(pkg):
         pkg.run_device_lens_noalloc(pkg.OP_FORWARD, pkg.DType.BF16, pkg.DType.BF16, 8193, 8, 64, 64,
                                     lens.data_ptr(), 0, x.data_ptr(), w.data_ptr(), out.data_ptr(), _stream())
     assert "at most 8192 groups" in str(e.value)
+
+
+def test_wgrad_more_than_64_groups(pkg):
+    """wgrad through the scratch table with more than 64 groups (the table kernel writes its
+    out_rows-based tiles into scratch): the planned path's bits and torch fp32, on two calls in a
+    row, the second smaller."""
+    rng = np.random.default_rng(21)
+    for b, n, k in ((72, 256, 192), (66, 128, 64)):
+        lens = rng.integers(0, 200, size=b)
+        lens[[1, b - 1]] = 0
+        total = int(lens.sum())
+        print(f"[no_alloc] wgrad B={b} N={n} K={k} rows={total}", flush=True)
+        go = torch.randn((total, n), device=DEV).to(torch.bfloat16)
+        x = torch.randn((total, k), device=DEV).to(torch.bfloat16)
+        d_lens = torch.tensor(lens, dtype=torch.int64, device=DEV)
+        want = torch.full((b, n, k), float("nan"), dtype=torch.bfloat16, device=DEV)
+        plan = pkg.DeviceLensPlan(pkg.OP_WGRAD, pkg.DType.BF16, pkg.DType.BF16, b, total, n, k, d_lens.data_ptr(), 0,
+                                  go.data_ptr(), x.data_ptr(), want.data_ptr(), _stream())
+        plan.run(_stream())
+        torch.cuda.synchronize(DEV)
+        plan.release()
+        got = torch.full((b, n, k), float("nan"), dtype=torch.bfloat16, device=DEV)
+        pkg.run_device_lens_noalloc(pkg.OP_WGRAD, pkg.DType.BF16, pkg.DType.BF16, b, total, n, k, d_lens.data_ptr(),
+                                    0, go.data_ptr(), x.data_ptr(), got.data_ptr(), _stream())
+        torch.cuda.synchronize(DEV)
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), "not the bits of the planned run"
+        row = 0
+        for g, m in enumerate(int(v) for v in lens):
+            ref = go[row:row + m].float().t().contiguous() @ x[row:row + m].float()
+            row += m
+            assert bool(((got[g].float() - ref).abs() <= ATOL + RTOL * ref.abs()).all()), f"group {g}"
+
+
+@pytest.mark.parametrize("b", [6, 70])
+def test_graph_capture_replays(pkg, b):
+    """One call outside capture (it sets up the device's scratch address), then the call captured
+    in a CUDA graph (6 groups: one launch, the GEMM builds the table; 70: the table kernel and the
+    GEMM) and replayed three times, with eager work and synchronizations between the replays:
+    every replay gives the planned path's bits."""
+    rng = np.random.default_rng(31 + b)
+    lens = rng.integers(0, 300, size=b)
+    lens[0] = 0
+    n, k = 384, 200
+    print(f"[no_alloc] graph B={b} N={n} K={k} rows={int(lens.sum())}", flush=True)
+    x, w, d_lens, d_offs, offs, total = _case(pkg, b, n, k, lens, gap=3)
+    want = _planned(pkg, x, w, d_lens, d_offs, total)
+    first = _noalloc(pkg, x, w, d_lens, d_offs, total)
+    assert torch.equal(first.view(torch.int16), want.view(torch.int16))
+    out = torch.full((total, n), float("nan"), dtype=torch.bfloat16, device=DEV)
+    graph = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize(DEV)
+    with torch.cuda.graph(graph):
+        pkg.run_device_lens_noalloc(pkg.OP_FORWARD, pkg.DType.BF16, pkg.DType.BF16, b, total, n, k,
+                                    d_lens.data_ptr(), d_offs.data_ptr(), x.data_ptr(), w.data_ptr(), out.data_ptr(),
+                                    torch.cuda.current_stream(DEV).cuda_stream)
+    sx, sw, s_lens, s_offs, _, s_total = _case(pkg, 1, 64, 64, [5], seed=3)
+    for replay in range(3):
+        out.fill_(float("nan"))
+        _noalloc(pkg, sx, sw, s_lens, s_offs, s_total)  # another call on the scratch between replays
+        torch.cuda.synchronize(DEV)
+        graph.replay()
+        torch.cuda.synchronize(DEV)
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16)), f"replay {replay}"
