@@ -913,6 +913,17 @@ __device__ unsigned long long g_stamps[kStampWgs * kStampSlots];
 #endif
 constexpr bool kTailSkip = GG_TAIL_SKIP;
 
+// Row-major accumulators (whole-tile 16-bit forward, cross-tile, no tail split): the x fragment
+// is the MFMA's first source, so lane l of block (mi, ni) holds output column slot l%16 of rows
+// 4 (l/16) .. +3; column slot s of block ni is tile column 8 s + ni of the wave's 128 (the w
+// fragment of block ni gathers w rows ni, ni + 8, ..). Over its 8 blocks a lane then holds 8
+// consecutive columns of each of its 4 rows: one store is 4 rows x 256 bytes, 4 consecutive
+// lanes on 64 contiguous bytes of one row, with no cross-lane moves (0: C^T accumulators, w as
+// the first source, and the permlane / DPP line stores).
+#ifndef GG_CT
+#define GG_CT 1
+#endif
+
 
 // MODE: layout (forward, dgrad, wgrad: operand layouts and tile mapping) and input format.
 // CROSS: cross-tile pipeline (needs k_tiles >= kCrossMinSteps); otherwise every tile starts
@@ -976,6 +987,11 @@ grouped_gemm_kernel(const KernelArgs args) {
         std::conditional_t<SWIDE, PlanSW,
                            std::conditional_t<FRONT, PlanFront, Plan<reads_per_frag(A_MN), reads_per_frag(B_MN), RB>>>>;
     static_assert(!SWIDE || (NBLK == P::nc && RB == P::rows), "short-wide plan");
+    // row-major accumulators (GG_CT): whole 256 x 256 tiles of the 16-bit forward, cross-tile, no
+    // tail split (its K ranges leave through the LDS epilogue's C^T partial sums)
+    constexpr bool CT = GG_CT && MODE == make_mode(kFwd, kIn16) && SHAPE == kShapeWide && CROSS && !TAIL;
+    static_assert(!CT || (RB == 8 && NBLK == 8 && P::nc == 8), "row-major accumulators: whole tiles");
+    constexpr int B_BLK = CT ? 1 : 16; // LDS rows between the w fragments of consecutive column blocks
     constexpr int NC   = P::nc;                                     // column blocks in the registers
     constexpr int A_ST = P::la * kWaves * 1024;                     // bytes of an A stage
     constexpr int B_ST = P::lb * kWaves * 1024;                     // bytes of a B stage
@@ -1063,20 +1079,25 @@ grouped_gemm_kernel(const KernelArgs args) {
     };
     // the column-block swap of transposed DMA j
     auto mn_swz = [](int j) { return F8 ? (j >> 1) & 1 : j & 1; };
-    auto dma_off = [&](bool mn, int j, int ld) {
+    // ct: the B operand of row-major accumulators, whose LDS row r keeps its chunk c at c ^ (r / 8
+    // % 8) (its fragments gather rows 8 apart); the 8 rows of DMA j share r / 8 = 4 j + wave.
+    auto dma_off = [&](bool mn, int j, int ld, bool ct = false) {
+        if (ct)
+            return (j * 32 + wave * 8 + ld_row) * ld * ES + ((lane & 7) ^ ((4 * j + wave) & 7)) * 16;
         if (!mn)
             return (j * 32 + wave * 8 + ld_row) * ld * ES + ld_chunk * 16;
         if (F8)
             return (16 * (j ^ mn_swz(j)) + 4 * wave + (lane >> 4)) * ld + mn_col(mn_swz(j));
         return ((4 * (2 * j + (wave >> 1)) + ((lane & 7) >> 1)) * ld + mn_col(mn_swz(j))) * 2;
     };
-    // voff[0]: A's offsets; voff[1]: B's (the forward op shares A's: both row strides are K).
-    constexpr bool kSameOff = LAYOUT == kFwd;
+    // voff[0]: A's offsets; voff[1]: B's (the forward op shares A's: both row strides are K, and
+    // both LDS layouts are the same unless the accumulators are row-major).
+    constexpr bool kSameOff = LAYOUT == kFwd && !CT;
     int            voff[kSameOff ? 1 : 2][LV];
     sfor<0, LV>([&](auto j) {
         voff[0][j] = dma_off(A_MN, j, args.lda);
         if constexpr (!kSameOff)
-            voff[1][j] = dma_off(B_MN, j, args.ldb);
+            voff[1][j] = dma_off(B_MN, j, args.ldb, CT);
     });
     // MN-major operands in unchecked steps: the lane offsets with the current tile's column mask
     // already applied (set once per tile by set_mn_offsets), and the K step in soffset. Every
@@ -1086,6 +1107,13 @@ grouped_gemm_kernel(const KernelArgs args) {
     // Last K step when K % 64 != 0: chunks at k >= K get an offset past every bound.
     const int k_last    = K - (T - 1) * KS; // valid K of the last step
     int       ktail_bad = (ld_chunk * (16 / ES) >= k_last) ? static_cast<int>(0x80000000u) : 0;
+    // the same for B's DMAs with row-major accumulators, whose logical chunk is (lane % 8) ^
+    // ((4 j + wave) % 8): one mask for even DMAs j, one for odd ones
+    int ktail_ct[2];
+    sfor<0, 2>([&](auto p) {
+        const int c  = (lane & 7) ^ ((4 * p + wave) & 7);
+        ktail_ct[p] = CT && c * (16 / ES) >= k_last ? static_cast<int>(0x80000000u) : 0;
+    });
 
     // Fragment reads. K-major: lane -> row lane%16 of a 16-row block, logical chunk
     // kh*4 + lane/16 (one base per k-half). MN-major: ds_read_b64_tr_b16 gives lane i of each
@@ -1116,16 +1144,22 @@ grouped_gemm_kernel(const KernelArgs args) {
         frag_a[kh]    = !A_MN ? wm * (ILV ? 16 : 128) * kRowBytes + off
                         : F8  ? mn8 + 128 * (wm ^ (fr_q & 1))
                               : wm * 1024 + mn;
-        frag_b[kh]    = !B_MN ? wn * WCOLS * kRowBytes + off
+        // row-major accumulators: lane l reads w row 8 (l%16) + ni (block ni adds 128 ni), whose
+        // chunk c sits at c ^ (l%8)
+        const int ct_off = (8 * fr_row) * kRowBytes + (((kh * 4 + fr_q) ^ (fr_row & 7)) * 16);
+        frag_b[kh]    = CT    ? wn * WCOLS * kRowBytes + ct_off
+                        : !B_MN ? wn * WCOLS * kRowBytes + off
                         : F8  ? mn8 + 128 * (wn ^ (fr_q & 1))
                               : wn * 1024 + mn;
     });
 
     // Register epilogue: in store s = 2h + half of a 16-row block, lane l writes 16 bytes of
-    // row 8 half + l%8 at column ecol + 64 h (see pack_pair).
+    // row 8 half + l%8 at column ecol + 64 h (see pack_pair). Row-major accumulators: in store
+    // s of a 16-row block, lane l writes the 16 bytes of columns ecol .. +7 of row 4 (l/16) + s.
     const int q    = lane >> 4;
-    const int ecol = wn * (SWIDE ? WCOLS : 128) + ((lane >> 3) & 1) * 32 + (q & 1) * 16 + (q >> 1) * 8;
-    int       voffc = ((wm * (ILV ? 16 : 128) + (lane & 7)) * N + ecol) * 2;
+    const int ecol = CT ? wn * 128 + 8 * (lane & 15)
+                        : wn * (SWIDE ? WCOLS : 128) + ((lane >> 3) & 1) * 32 + (q & 1) * 16 + (q >> 1) * 8;
+    int       voffc = CT ? ((wm * 16 + 4 * q) * N + ecol) * 2 : ((wm * (ILV ? 16 : 128) + (lane & 7)) * N + ecol) * 2;
     const int blk_stride = A_BLK * N * 2; // bytes between a wave's 16-row blocks of C
 
     // Logical stage L of an operand (the K step's index mod 2 for A, mod 3 for B within the
@@ -1160,6 +1194,10 @@ grouped_gemm_kernel(const KernelArgs args) {
                 fresh_v(voffm[1][j]);
         });
         fresh_v(ktail_bad);
+        if constexpr (CT) {
+            fresh_v(ktail_ct[0]);
+            fresh_v(ktail_ct[1]);
+        }
         fresh_v(voffc);
         {
             // the step count, opaque: the checked steps' comparisons with it are made in the loop,
@@ -1426,7 +1464,9 @@ grouped_gemm_kernel(const KernelArgs args) {
                 d.vadd = 0;
                 // the unit's partial last K step (a next unit has at least kCrossMinSteps steps, so
                 // the three prefetched never include its last, and koff < 3 < T - 1 for them)
-                d.mask = (KT && koff == T - 1 && cur.klast) ? ktail_bad : 0;
+                const bool tail_step = KT && koff == T - 1 && cur.klast;
+                d.mask  = tail_step ? (B && CT ? ktail_ct[0] : ktail_bad) : 0;
+                d.mask1 = tail_step && B && CT ? ktail_ct[1] : 0; // odd DMAs of B (row-major acc.)
             }
         } else {
             d.rs = rc;
@@ -1456,7 +1496,7 @@ grouped_gemm_kernel(const KernelArgs args) {
         else if constexpr (MN)
             return (vo + d.vadd) | (mn_swz(j) ? d.mask1 : d.mask);
         else if constexpr (decltype(checked)::value)
-            return vo | d.mask;
+            return vo | ((B && CT && (j & 1)) ? d.mask1 : d.mask);
         else
             return vo;
     };
@@ -1503,7 +1543,7 @@ grouped_gemm_kernel(const KernelArgs args) {
         wait_vm_lds_barrier<VM>(); // A(0), B(0), B(1) landed everywhere
         sfor<0, NC>([&](auto ni) {
             sfor<0, reads_per_frag(B_MN)>([&](auto r) {
-                read_frag.template operator()<B_MN, r>(fb[0][ni], b_rd[0], ni);
+                read_frag.template operator()<B_MN, r, B_BLK>(fb[0][ni], b_rd[0], ni);
             });
         });
         sfor<0, reads_per_frag(A_MN)>([&](auto r) {
@@ -1686,12 +1726,38 @@ grouped_gemm_kernel(const KernelArgs args) {
                                      : static_cast<int>(0x80000000u);
         __builtin_amdgcn_raw_buffer_store_b64(pack4<F16>(v), crs, vo, 0, kStoreCpol);
     };
+    // Row-major accumulators: store s (0-3) of row block r, lane l writing row 4 (l/16) + s of
+    // the block at columns ecol .. +7, element s of its 8 column blocks' accumulators (column slot
+    // l%16 of block ni is column 8 (l%16) + ni). Columns past n_valid get an out-of-range offset
+    // (N % 8 == 0: a 16-byte chunk is all valid or all past N); rows past m_valid fall outside crs.
+    auto store_ct = [&](auto r, auto s_, const __amdgpu_buffer_rsrc_t &crs, int n_valid) {
+        u32x4 d;
+        sfor<0, 4>([&](auto u) {
+            // reads of these accumulators may not move above this point
+            asm volatile("" : "+a"(acc[r][2 * u]), "+a"(acc[r][2 * u + 1]));
+            const float v0 = acc[r][2 * u][int(s_)], v1 = acc[r][2 * u + 1][int(s_)];
+            if constexpr (F16)
+                d[int(u)] = __builtin_bit_cast(unsigned, f16x2{(_Float16)v0, (_Float16)v1});
+            else
+                d[int(u)] = __builtin_bit_cast(unsigned, bf16x2{(__bf16)v0, (__bf16)v1});
+        });
+        // offsets from opaque copies of the strides (two SALU), not loop-invariant ones the
+        // compiler would keep in (spilled) SGPRs
+        uint32_t bs = static_cast<uint32_t>(blk_stride), rs = static_cast<uint32_t>(N * 2);
+        fresh_s(bs);
+        fresh_s(rs);
+        const int vo = ecol < n_valid ? voffc + r * static_cast<int>(bs) + s_ * static_cast<int>(rs)
+                                      : static_cast<int>(0x80000000u);
+        __builtin_amdgcn_raw_buffer_store_b128(d, crs, vo, 0, kStoreCpol);
+    };
     // Store s (0-3) of the previous tile's row block r: packed with the next one for even s;
     // s = 4 (short-wide tiles): the ninth column block.
     constexpr int kEpiStores = SWIDE ? 5 : 4;
     auto epi_store = [&](auto r, auto s_) {
         sched_fence();
-        if constexpr (s_ == 4) {
+        if constexpr (CT) {
+            store_ct(r, s_, prev_crs, prev_n);
+        } else if constexpr (s_ == 4) {
             store_block9(r, prev_crs, prev_n);
         } else {
             if constexpr (s_ % 2 == 0)
@@ -1710,7 +1776,11 @@ grouped_gemm_kernel(const KernelArgs args) {
             const i32x8 bw = __builtin_shufflevector(fb[SA][ni][0], fb[SA][ni][1], 0, 1, 2, 3, 4, 5, 6, 7);
             const i32x8 ax = __builtin_shufflevector(fa[mi & 1][0], fa[mi & 1][1], 0, 1, 2, 3, 4, 5, 6, 7);
             mfma8<mode_b_e5(MODE), mode_a_e5(MODE), FIRST>(acc[mi][ni], bw, ax);
-        } else if constexpr (FIRST && kh == 0)
+        } else if constexpr (CT && FIRST && kh == 0) // row-major accumulators: x is the first source
+            mfma_first<F16>(acc[mi][ni], fa[mi & 1][0], fb[SA][ni][0]);
+        else if constexpr (CT)
+            mfma<F16>(acc[mi][ni], fa[mi & 1][kh], fb[SA][ni][kh]);
+        else if constexpr (FIRST && kh == 0)
             mfma_first<F16>(acc[mi][ni], fb[SA][ni][0], fa[mi & 1][0]);
         else
             mfma<F16>(acc[mi][ni], fb[SA][ni][kh], fa[mi & 1][kh]);
@@ -1751,7 +1821,7 @@ grouped_gemm_kernel(const KernelArgs args) {
                 }
                 if constexpr (P::read_b_next(mi, idx) >= 0) {
                     constexpr int bb = P::read_b_blk(mi, idx);
-                    read_frag.template operator()<B_MN, P::read_b_next(mi, idx)>(fb[NX][bb], b_rd[SB_NEXT],
+                    read_frag.template operator()<B_MN, P::read_b_next(mi, idx), B_BLK>(fb[NX][bb], b_rd[SB_NEXT],
                                                                                  ic<bb>{});
                     sched_fence();
                 }
@@ -1814,7 +1884,7 @@ grouped_gemm_kernel(const KernelArgs args) {
                 }
                 if constexpr (P::read_b_next(mi, idx) >= 0) {
                     constexpr int bb = P::read_b_blk(mi, idx);
-                    read_frag.template operator()<B_MN, P::read_b_next(mi, idx)>(fb[NX][bb], b_rd[SB_NEXT],
+                    read_frag.template operator()<B_MN, P::read_b_next(mi, idx), B_BLK>(fb[NX][bb], b_rd[SB_NEXT],
                                                                                  ic<bb>{});
                     sched_fence();
                 }
@@ -1961,7 +2031,15 @@ grouped_gemm_kernel(const KernelArgs args) {
             T   = __builtin_amdgcn_readfirstlane(cur.T);
         }
     }
-    if constexpr (CROSS) {
+    if constexpr (CT) {
+        // row-major accumulators: the last tile goes out from registers as well (whole 64-byte
+        // pieces of rows per 4 lanes), after the trailing DMAs into LDS have landed
+        GG_STAMP(kStampSlots - 2);
+        wait_vm_lds_barrier<0>();
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" ::: "memory"); // MFMA -> VALU read distance
+        const __amdgpu_buffer_rsrc_t crs = c_rsrc(cur);
+        sfor<0, 8>([&](auto mi) { sfor<0, 4>([&](auto s_) { store_ct(mi, s_, crs, cur.n_valid); }); });
+    } else if constexpr (CROSS) {
         GG_STAMP(kStampSlots - 2);
         epilogue_lds(cur); // TAIL: a K range's partial sums instead of its C tile
     }
