@@ -52,10 +52,12 @@ __global__ void __launch_bounds__(256) split_reduce_kernel(const KernelArgs args
 // ---------------------------------------------------------------------------------------
 // Tail split, second pass: block b takes 256 16-byte positions (b % 64) of last-round tile
 // b / 64 (the tile of physical slot full + b / 64, as the GEMM's xcd_remap placed it), in the
-// slab layout of split_reduce_kernel; the two K ranges are added (fp32, commutative) and stored.
-// Short tiles store row blocks 0-5 only: positions of rows past tile_m are never valid rows.
+// slab layout of split_reduce_kernel, or (CT: whole 256-row tiles with row-major accumulators,
+// ct_instance) in row-major order: position p is row p / 64, columns 4 (p % 64) .. +3. The two K
+// ranges are added (fp32, commutative) and stored. Short tiles store row blocks 0-5 only:
+// positions of rows past tile_m are never valid rows.
 // ---------------------------------------------------------------------------------------
-template <bool F16>
+template <bool F16, bool CT>
 __global__ void __launch_bounds__(256) tail_reduce_kernel(const KernelArgs args, int grid) {
     const int j    = blockIdx.x >> 6;
     const int full = (args.total_tiles / grid) * grid;
@@ -66,8 +68,8 @@ __global__ void __launch_bounds__(256) tail_reduce_kernel(const KernelArgs args,
     const GroupEntry ge  = args.groups[g];
     const int        p   = (blockIdx.x & 63) * 256 + static_cast<int>(threadIdx.x);
     const int        wv  = p >> 12, blk = (p >> 6) & 63, l = p & 63;
-    const int        row = (wv >> 1) * 16 + (blk >> 3) * 32 + (l & 15);
-    const int        col = (wv & 1) * 128 + (blk & 7) * 16 + (l >> 4) * 4;
+    const int        row = CT ? p >> 6 : (wv >> 1) * 16 + (blk >> 3) * 32 + (l & 15);
+    const int        col = CT ? (p & 63) * 4 : (wv & 1) * 128 + (blk & 7) * 16 + (l >> 4) * 4;
     const int        N   = args.n;
     const float     *src = args.ws + static_cast<int64_t>(j) * 65536 + p * 4;
     const f32x4      v0  = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(src));
@@ -280,10 +282,16 @@ hipError_t launch_tail_reduce(const KernelArgs &args, bool fp16, int grid, hipSt
     const int rem = args.total_tiles - (args.total_tiles / grid) * grid;
     if (rem <= 0)
         return hipSuccess;
-    if (fp16)
-        hipLaunchKernelGGL(tail_reduce_kernel<true>, dim3(rem * 64), dim3(256), 0, stream, args, grid);
+    // the GEMM instance of whole 256-row tiles keeps row-major accumulators (ct_instance)
+    const bool ct = args.tile_m == kTileM && ct_instance(make_mode(kFwd, kIn16), kShapeWide, true);
+    if (fp16 && ct)
+        hipLaunchKernelGGL((tail_reduce_kernel<true, true>), dim3(rem * 64), dim3(256), 0, stream, args, grid);
+    else if (fp16)
+        hipLaunchKernelGGL((tail_reduce_kernel<true, false>), dim3(rem * 64), dim3(256), 0, stream, args, grid);
+    else if (ct)
+        hipLaunchKernelGGL((tail_reduce_kernel<false, true>), dim3(rem * 64), dim3(256), 0, stream, args, grid);
     else
-        hipLaunchKernelGGL(tail_reduce_kernel<false>, dim3(rem * 64), dim3(256), 0, stream, args, grid);
+        hipLaunchKernelGGL((tail_reduce_kernel<false, false>), dim3(rem * 64), dim3(256), 0, stream, args, grid);
     return hipGetLastError();
 }
 

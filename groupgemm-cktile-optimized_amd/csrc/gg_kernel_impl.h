@@ -913,16 +913,20 @@ __device__ unsigned long long g_stamps[kStampWgs * kStampSlots];
 #endif
 constexpr bool kTailSkip = GG_TAIL_SKIP;
 
-// Row-major accumulators (whole-tile 16-bit forward, cross-tile, no tail split): the x fragment
+// Row-major accumulators (whole-tile 16-bit forward, cross-tile): the x fragment
 // is the MFMA's first source, so lane l of block (mi, ni) holds output column slot l%16 of rows
 // 4 (l/16) .. +3; column slot s of block ni is tile column 8 s + ni of the wave's 128 (the w
 // fragment of block ni gathers w rows ni, ni + 8, ..). Over its 8 blocks a lane then holds 8
 // consecutive columns of each of its 4 rows: one store is 4 rows x 256 bytes, 4 consecutive
 // lanes on 64 contiguous bytes of one row, with no cross-lane moves (0: C^T accumulators, w as
-// the first source, and the permlane / DPP line stores).
+// the first source, and the permlane / DPP line stores). A tail split's K ranges store their fp32
+// partial sums as a row-major 256 x 256 slab (tail_reduce_kernel's kCtSlab order).
 #ifndef GG_CT
 #define GG_CT 1
 #endif
+constexpr bool ct_instance(int mode, int shape, bool cross) {
+    return GG_CT && mode == make_mode(kFwd, kIn16) && shape == kShapeWide && cross;
+}
 
 
 // MODE: layout (forward, dgrad, wgrad: operand layouts and tile mapping) and input format.
@@ -987,9 +991,8 @@ grouped_gemm_kernel(const KernelArgs args) {
         std::conditional_t<SWIDE, PlanSW,
                            std::conditional_t<FRONT, PlanFront, Plan<reads_per_frag(A_MN), reads_per_frag(B_MN), RB>>>>;
     static_assert(!SWIDE || (NBLK == P::nc && RB == P::rows), "short-wide plan");
-    // row-major accumulators (GG_CT): whole 256 x 256 tiles of the 16-bit forward, cross-tile, no
-    // tail split (its K ranges leave through the LDS epilogue's C^T partial sums)
-    constexpr bool CT = GG_CT && MODE == make_mode(kFwd, kIn16) && SHAPE == kShapeWide && CROSS && !TAIL;
+    // row-major accumulators (GG_CT): whole 256 x 256 tiles of the 16-bit forward, cross-tile
+    constexpr bool CT = ct_instance(MODE, SHAPE, CROSS);
     static_assert(!CT || (RB == 8 && NBLK == 8 && P::nc == 8), "row-major accumulators: whole tiles");
     constexpr int B_BLK = CT ? 1 : 16; // LDS rows between the w fragments of consecutive column blocks
     constexpr int NC   = P::nc;                                     // column blocks in the registers
@@ -2033,12 +2036,37 @@ grouped_gemm_kernel(const KernelArgs args) {
     }
     if constexpr (CT) {
         // row-major accumulators: the last tile goes out from registers as well (whole 64-byte
-        // pieces of rows per 4 lanes), after the trailing DMAs into LDS have landed
+        // pieces of rows per 4 lanes), after the trailing DMAs into LDS have landed. TAIL: a K
+        // range stores its fp32 partial sums instead, as rows of a 256 x 256 slab (k * rem + tail
+        // of the workspace; lane l: 32 bytes, the 8 columns of its store), with its C stores
+        // dropped (no rows), and a whole tile's partial-sum stores go to a zero-length resource:
+        // one branch-free exit reads the accumulators.
         GG_STAMP(kStampSlots - 2);
         wait_vm_lds_barrier<0>();
         asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" ::: "memory"); // MFMA -> VALU read distance
-        const __amdgpu_buffer_rsrc_t crs = c_rsrc(cur);
-        sfor<0, 8>([&](auto mi) { sfor<0, 4>([&](auto s_) { store_ct(mi, s_, crs, cur.n_valid); }); });
+        Tile       tl   = cur;
+        const bool part = TAIL && tl.tail >= 0;
+        if constexpr (TAIL)
+            tl.m_valid = part ? 0 : tl.m_valid;
+        const __amdgpu_buffer_rsrc_t crs = c_rsrc(tl);
+        const __amdgpu_buffer_rsrc_t prs =
+            __builtin_amdgcn_make_buffer_rsrc(args.ws, static_cast<short>(0), part ? 0x7fffffff : 0, 0x00020000);
+        const int poff = part ? (((tl.tail_k * rem + tl.tail) * 256 + wm * 16 + 4 * (lane >> 4)) * 256 + ecol) * 4 : 0;
+        sfor<0, 8>([&](auto mi) {
+            sfor<0, 4>([&](auto s_) {
+                if constexpr (TAIL) {
+                    sfor<0, 2>([&](auto hf) {
+                        asm volatile("" : "+a"(acc[mi][4 * hf]), "+a"(acc[mi][4 * hf + 1]), "+a"(acc[mi][4 * hf + 2]),
+                                     "+a"(acc[mi][4 * hf + 3]));
+                        const f32x4 v = {acc[mi][4 * hf][int(s_)], acc[mi][4 * hf + 1][int(s_)],
+                                         acc[mi][4 * hf + 2][int(s_)], acc[mi][4 * hf + 3][int(s_)]};
+                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), prs,
+                                                               poff + ((32 * mi + s_) * 256) * 4 + 16 * hf, 0, 0);
+                    });
+                }
+                store_ct(mi, s_, crs, tl.n_valid);
+            });
+        });
     } else if constexpr (CROSS) {
         GG_STAMP(kStampSlots - 2);
         epilogue_lds(cur); // TAIL: a K range's partial sums instead of its C tile
