@@ -2,6 +2,7 @@
 //
 //   gg_bench --shapes shapes/configs.csv [--dtype bf16|fp16] [--backends mi355x,hipblaslt_seq]
 //            [--only 1001,1005] [--warmup 20] [--iters 100] [--no-check] [--out rows.csv] [--verbose]
+//            [--clock]
 //
 // What it keeps of the reference's driver (bench/bench_main.cpp), so that its CSVs compare row
 // for row with the reference's: the flags (:8-10), the CSV header (:306), balanced groups of M
@@ -19,7 +20,13 @@
 //   * the check is one launch with a wave per sampled output (fp32 dot over K, lane-strided,
 //     reduced with cross-lane adds), buffers allocated once for the largest case;
 //   * the summary compares every backend with the first one: geomean speedup and wins over the
-//     cases every backend passed.
+//     cases every backend passed;
+//   * --clock runs gg_clock_probe (one wave reading the shader clock against the wall clock) on a
+//     second stream over the first 60 % of the mi355x backend's timed loop and appends the
+//     effective clock to the row's Detail ("[clock 1712 MHz]"). Only there: the probe's wave needs a
+//     CU slot beside the GEMM's workgroups, which the mi355x kernel leaves (a few VGPRs, no LDS),
+//     while hipBLASLt's kernels can fill a CU's registers, so that the probe displaces one of their
+//     workgroups and both the timing and the clock it reads are no longer the kernel's own.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -85,11 +92,11 @@ struct Settings {
     std::vector<std::string> backends{"mi355x", "hipblaslt_grouped", "hipblaslt_loop"};
     std::set<int>            only;
     int                      warmup = 20, iters = 100;
-    bool                     check = true, verbose = false;
+    bool                     check = true, verbose = false, clock = false;
 };
 
 const char *kUsage = "usage: gg_bench --shapes FILE.csv [--dtype bf16|fp16] [--backends a,b,...] [--only ID,...]\n"
-                     "                [--warmup N] [--iters N] [--no-check] [--out FILE.csv] [--verbose]\n";
+                     "                [--warmup N] [--iters N] [--no-check] [--out FILE.csv] [--verbose] [--clock]\n";
 
 Settings parse(int argc, char **argv) {
     Settings s;
@@ -130,6 +137,7 @@ Settings parse(int argc, char **argv) {
         {"--iters", true, [&](const std::string &v) { s.iters = std::stoi(v); }},
         {"--no-check", false, [&](const std::string &) { s.check = false; }},
         {"--verbose", false, [&](const std::string &) { s.verbose = true; }},
+        {"--clock", false, [&](const std::string &) { s.clock = true; }},
     };
     for (int i = 1; i < argc; ++i) {
         const std::string arg = argv[i];
@@ -471,12 +479,20 @@ std::string default_path(const Settings &s) {
 
 // ---- one backend on one case -----------------------------------------------------------------
 struct Clock {
-    hipEvent_t a = nullptr, b = nullptr;
+    hipEvent_t  a = nullptr, b = nullptr, w = nullptr; // w: start of the warmup (--clock)
+    hipStream_t side  = nullptr;                       // the clock probe's stream (default priority)
+    uint64_t   *words = nullptr;                       // its five result words (device)
     Clock() {
         hip_or_die(hipEventCreate(&a), "event");
         hip_or_die(hipEventCreate(&b), "event");
+        hip_or_die(hipEventCreate(&w), "event");
+        hip_or_die(hipStreamCreateWithFlags(&side, hipStreamNonBlocking), "probe stream");
+        hip_or_die(hipMalloc(&words, 5 * sizeof(uint64_t)), "probe words");
     }
     ~Clock() {
+        (void)hipFree(words);
+        (void)hipStreamDestroy(side);
+        (void)hipEventDestroy(w);
         (void)hipEventDestroy(a);
         (void)hipEventDestroy(b);
     }
@@ -515,9 +531,22 @@ Result run_backend(Backend &be, const Shape &shape, const GroupedGemmProblem &p,
             r.check = "SKIP";
         }
         note("timing");
+        hip_or_die(hipEventRecord(clock.w, s), "warmup event");
         for (int i = 0; i < set.warmup; ++i)
             be.run(s);
         hip_or_die(hipEventRecord(clock.a, s), "start event");
+        const bool probe = set.clock && r.backend == "mi355x";
+        if (probe) {
+            // the probe starts with the timed loop and spans 60 % of it (its length estimated
+            // from the warmup)
+            hip_or_die(hipEventSynchronize(clock.a), "warmup sync");
+            float warm = 0.0f;
+            hip_or_die(hipEventElapsedTime(&warm, clock.w, clock.a), "warmup time");
+            const double per = set.warmup > 0 ? double(warm) / set.warmup : 1.0;
+            hip_or_die(hipStreamWaitEvent(clock.side, clock.a, 0), "probe wait");
+            if (gg_clock_probe(clock.words, 0.6e-3 * per * set.iters, clock.side) != GG_OK)
+                throw std::runtime_error(std::string("clock probe: ") + gg_last_error());
+        }
         for (int i = 0; i < set.iters; ++i)
             be.run(s);
         hip_or_die(hipEventRecord(clock.b, s), "stop event");
@@ -526,6 +555,13 @@ Result run_backend(Backend &be, const Shape &shape, const GroupedGemmProblem &p,
         hip_or_die(hipEventElapsedTime(&total, clock.a, clock.b), "elapsed");
         r.ms     = double(total) / set.iters;
         r.tflops = p.flops() / (r.ms * 1e-3) / 1e12;
+        if (probe) {
+            uint64_t v[5] = {};
+            hip_or_die(hipStreamSynchronize(clock.side), "probe sync");
+            hip_or_die(hipMemcpy(v, clock.words, sizeof(v), hipMemcpyDeviceToHost), "probe words");
+            if (v[3] > v[1] && v[4] > 0)
+                r.detail += " [clock " + std::to_string(std::llround(double(v[2] - v[0]) / (double(v[3] - v[1]) / double(v[4])) / 1e6)) + " MHz]";
+        }
     } catch (const std::exception &e) {
         (void)hipStreamSynchronize(s);
         r.check  = "ERROR";
