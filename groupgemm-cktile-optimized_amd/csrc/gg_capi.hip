@@ -111,6 +111,10 @@ void fill_args(gg_plan *plan, int n_xcd) {
     a.k_tiles   = static_cast<int>(gg::cdiv(plan->k, gg::kTileK));
     a.n_xcd     = plan->grid % n_xcd == 0 ? n_xcd : 1;
     a.band      = gg::kBand;
+    // GG_BAND=<1..64> in the environment overrides the M-tiles per band of the in-group order
+    // (measurements only)
+    if (const char *env = std::getenv("GG_BAND"); env != nullptr && std::atoi(env) >= 1 && std::atoi(env) <= 64)
+        a.band = std::atoi(env);
     a.lda       = static_cast<int>(plan->k);
     a.ldb       = static_cast<int>(plan->k);
     a.m_out     = 0;
