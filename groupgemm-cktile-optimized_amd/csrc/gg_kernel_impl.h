@@ -1082,11 +1082,15 @@ grouped_gemm_kernel(const KernelArgs args) {
     };
     // the column-block swap of transposed DMA j
     auto mn_swz = [](int j) { return F8 ? (j >> 1) & 1 : j & 1; };
-    // ct: the B operand of row-major accumulators, whose LDS row r keeps its chunk c at c ^ (r / 8
-    // % 8) (its fragments gather rows 8 apart); the 8 rows of DMA j share r / 8 = 4 j + wave.
+    // ct: the B operand of row-major accumulators, whose fragments gather rows 8 apart. LDS row p
+    // holds stored row p ^ ((p / 8) & 1) (adjacent rows swapped in every other group of 8, so that
+    // the 8 rows one read pass gathers alternate between the two halves of the banks) and keeps
+    // its chunk c at c ^ (p / 8 % 8). The 8 LDS rows of DMA j share p / 8 = 4 j + wave: lane l
+    // fetches stored row 8 (4 j + wave) + ((l / 8) ^ (wave & 1)), logical chunk
+    // (l % 8) ^ ((4 j + wave) % 8).
     auto dma_off = [&](bool mn, int j, int ld, bool ct = false) {
         if (ct)
-            return (j * 32 + wave * 8 + ld_row) * ld * ES + ((lane & 7) ^ ((4 * j + wave) & 7)) * 16;
+            return (j * 32 + wave * 8 + (ld_row ^ (wave & 1))) * ld * ES + ((lane & 7) ^ ((4 * j + wave) & 7)) * 16;
         if (!mn)
             return (j * 32 + wave * 8 + ld_row) * ld * ES + ld_chunk * 16;
         if (F8)
@@ -1139,7 +1143,7 @@ grouped_gemm_kernel(const KernelArgs args) {
     // 8 rows of a group take 8 different slots, and groups of odd q the other half of the banks.
     const int fr_row = lane & 15, fr_q = lane >> 4;
     const int mn8    = fr_q * 8192 + (fr_row >> 1) * (256 + 16) + (fr_row & 1) * 8;
-    int frag_a[2], frag_b[2];
+    int frag_a[2], frag_b[2], frag_bo[2]; // frag_bo: odd column blocks of row-major accumulators
     sfor<0, 2>([&](auto kh) {
         const int off = fr_row * kRowBytes +
                         (((F8 ? 2 * fr_q + (kh ^ (fr_q & 1)) : kh * 4 + fr_q) ^ (fr_row & 7)) * 16);
@@ -1147,9 +1151,11 @@ grouped_gemm_kernel(const KernelArgs args) {
         frag_a[kh]    = !A_MN ? wm * (ILV ? 16 : 128) * kRowBytes + off
                         : F8  ? mn8 + 128 * (wm ^ (fr_q & 1))
                               : wm * 1024 + mn;
-        // row-major accumulators: lane l reads w row 8 (l%16) + ni (block ni adds 128 ni), whose
-        // chunk c sits at c ^ (l%8)
-        const int ct_off = (8 * fr_row) * kRowBytes + (((kh * 4 + fr_q) ^ (fr_row & 7)) * 16);
+        // row-major accumulators: lane l reads stored w row 8 (l%16) + ni, at LDS row
+        // 8 (l%16) + (ni ^ (l & 1)), whose chunk c sits at c ^ (l%8): block ni adds 128 ni to the
+        // base of its parity (frag_b for even ni, frag_bo for odd ni, 256 lower for odd lanes)
+        const int ct_off = (8 * fr_row + (fr_row & 1)) * kRowBytes + (((kh * 4 + fr_q) ^ (fr_row & 7)) * 16);
+        frag_bo[kh]   = wn * WCOLS * kRowBytes + ct_off - (fr_row & 1) * 2 * kRowBytes;
         frag_b[kh]    = CT    ? wn * WCOLS * kRowBytes + ct_off
                         : !B_MN ? wn * WCOLS * kRowBytes + off
                         : F8  ? mn8 + 128 * (wn ^ (fr_q & 1))
@@ -1170,6 +1176,7 @@ grouped_gemm_kernel(const KernelArgs args) {
     // rotates by its predecessor's K-step count.
     int      rot_a = 0, rot_b = 0;
     int      a_rd[2][2], b_rd[3][2]; // LDS read base per logical stage and k-half
+    int      b_rdo[3][2];            // row-major accumulators: B's base for odd column blocks
     uint32_t a_dst[2], b_dst[3];     // this wave's DMA destination per logical stage
     auto set_stages = [&]() {
         sfor<0, 2>([&](auto L) {
@@ -1183,6 +1190,8 @@ grouped_gemm_kernel(const KernelArgs args) {
             const int p = kAStages * A_ST + s * B_ST;
             b_dst[L]    = lds0 + wave * 1024 + p;
             sfor<0, 2>([&](auto h) { b_rd[L][h] = frag_b[h] + p; });
+            if constexpr (CT)
+                sfor<0, 2>([&](auto h) { b_rdo[L][h] = frag_bo[h] + p; });
         });
     };
     // Re-materialise loop-invariant offsets at the top of every loop body (see fresh_v).
@@ -1216,6 +1225,8 @@ grouped_gemm_kernel(const KernelArgs args) {
         sfor<0, 3>([&](auto L) {
             fresh_s(b_dst[L]);
             sfor<0, 2>([&](auto h) { fresh_v(b_rd[L][h]); });
+            if constexpr (CT)
+                sfor<0, 2>([&](auto h) { fresh_v(b_rdo[L][h]); });
         });
     };
     auto lds_read = [&](int off) -> i32x4 { return *reinterpret_cast<const i32x4 *>(smem + off); };
@@ -1245,6 +1256,14 @@ grouped_gemm_kernel(const KernelArgs args) {
         }
     };
 
+    // B's read bases of logical stage L for column block blk (odd blocks of row-major
+    // accumulators have their own, see frag_bo)
+    auto b_base = [&](int L, auto blk) -> const int(&)[2] {
+        if constexpr (CT && (decltype(blk)::value & 1))
+            return b_rdo[L];
+        else
+            return b_rd[L];
+    };
     f32x4 acc[8][NC];
     i32x4 fa[2][2];     // x fragments: row ring x k-half
     i32x4 fb[2][NC][2]; // w fragments: step parity x column block x k-half
@@ -1546,7 +1565,7 @@ grouped_gemm_kernel(const KernelArgs args) {
         wait_vm_lds_barrier<VM>(); // A(0), B(0), B(1) landed everywhere
         sfor<0, NC>([&](auto ni) {
             sfor<0, reads_per_frag(B_MN)>([&](auto r) {
-                read_frag.template operator()<B_MN, r, B_BLK>(fb[0][ni], b_rd[0], ni);
+                read_frag.template operator()<B_MN, r, B_BLK>(fb[0][ni], b_base(0, ni), ni);
             });
         });
         sfor<0, reads_per_frag(A_MN)>([&](auto r) {
@@ -1824,7 +1843,7 @@ grouped_gemm_kernel(const KernelArgs args) {
                 }
                 if constexpr (P::read_b_next(mi, idx) >= 0) {
                     constexpr int bb = P::read_b_blk(mi, idx);
-                    read_frag.template operator()<B_MN, P::read_b_next(mi, idx), B_BLK>(fb[NX][bb], b_rd[SB_NEXT],
+                    read_frag.template operator()<B_MN, P::read_b_next(mi, idx), B_BLK>(fb[NX][bb], b_base(SB_NEXT, ic<bb>{}),
                                                                                  ic<bb>{});
                     sched_fence();
                 }
@@ -1887,7 +1906,7 @@ grouped_gemm_kernel(const KernelArgs args) {
                 }
                 if constexpr (P::read_b_next(mi, idx) >= 0) {
                     constexpr int bb = P::read_b_blk(mi, idx);
-                    read_frag.template operator()<B_MN, P::read_b_next(mi, idx), B_BLK>(fb[NX][bb], b_rd[SB_NEXT],
+                    read_frag.template operator()<B_MN, P::read_b_next(mi, idx), B_BLK>(fb[NX][bb], b_base(SB_NEXT, ic<bb>{}),
                                                                                  ic<bb>{});
                     sched_fence();
                 }
