@@ -1,4 +1,5 @@
-"""The transposed (MN-major) operand layouts of the kernel, checked on the CPU.
+"""The transposed (MN-major) operand layouts of the kernel and the row-major accumulators' B
+layout and stores, checked on the CPU.
 
 csrc/gg_kernel_impl.h stages an MN-major operand's K step in LDS with LDS DMAs (64 lanes x 16
 bytes at M0 + 16 * lane) and reads fragments back with transposed LDS reads. This test restates
@@ -14,6 +15,11 @@ offsets), simulates the DMAs into a 32 KB stage and the reads out of it, and che
 The transposed reads follow the lane mapping pinned on the GPU: ds_read_b64_tr_b8 gives byte j of
 lane i from byte i%8 of source lane 2j + i/8 of its 16-lane group, ds_read_b64_tr_b16 element j of
 lane i from element i%4 of source lane 4j + i/4. The GPU parity tests run the kernel itself.
+Row-major accumulators (GG_CT): B's DMAs fill each LDS byte once, every gathered fragment read
+finds its stored row and chunk, a ds_read_b128 pass (two 8-lane groups whose lane / 16 differ in
+bit 0) hits 64 distinct banks (and would hit 32 twice without the row swap, as the counters
+measured), every output of a tile is stored once from the accumulator holding it, and the
+partial-sum slabs are row-major as the tail reduction reads them.
 """
 import collections
 import itertools
@@ -128,3 +134,132 @@ def _planted_f8_dma(wave, j, lane):
 def test_layout_check_catches_a_planted_mistake():
     with pytest.raises(AssertionError):
         check_fp8_reads(stage(_planted_f8_dma, 1))
+
+
+# ---- row-major accumulators (whole-tile 16-bit forward, GG_CT) ----------------------------------
+# B (w) stage: 256 stored rows (tile columns) x 128 bytes of one K step. LDS row p holds stored
+# row p ^ ((p >> 3) & 1) and keeps its chunk c at slot c ^ ((p >> 3) & 7) (dma_off with ct,
+# frag_b / frag_bo in csrc/gg_kernel_impl.h). A fragment of column block ni (a wave's column half
+# wn) gathers stored rows wn * 128 + 8 (l % 16) + ni, chunk 4 kh + l / 16.
+def ct_dma(wave, j, lane, swap=True):
+    """(stored row, logical chunk) of lane `lane` of B's DMA j of wave `wave`."""
+    r = (lane >> 3) ^ ((wave & 1) if swap else 0)
+    return (4 * j + wave) * 8 + r, (lane & 7) ^ ((4 * j + wave) & 7)
+
+
+def ct_read(wn, ni, kh, lane, swap=True):
+    """LDS byte address of lane `lane`'s read (k-half kh) of column block ni (frag_b / frag_bo)."""
+    fr_row, q = lane & 15, lane >> 4
+    odd = (fr_row & 1) if swap else 0
+    ct_off = (8 * fr_row + odd) * 128 + (((kh * 4 + q) ^ (fr_row & 7)) * 16)
+    base_even = wn * 128 * 128 + ct_off
+    base_odd = base_even - odd * 256
+    return (base_odd if ni & 1 else base_even) + ni * 128
+
+
+def ct_stage(swap=True):
+    lds = {}
+    for w, j in itertools.product(range(4), range(8)):
+        for lane in range(64):
+            row, chunk = ct_dma(w, j, lane, swap)
+            a = 4096 * j + 1024 * w + 16 * lane
+            assert a not in lds
+            lds[a] = (row, chunk)
+    assert sorted(lds) == list(range(0, 32768, 16))
+    assert sorted(lds.values()) == [(r, c) for r in range(256) for c in range(8)]
+    return lds
+
+
+def read_pass_worst(addrs):
+    """Worst bank load of a ds_read_b128, served in passes of two 8-lane groups whose lane / 16
+    differ in bit 0 (lanes 0-7 with 16-23, 8-15 with 24-31, ...): 16 lanes x 4 banks of 64."""
+    worst = 0
+    for g0 in (0, 8, 32, 40):
+        cnt = collections.Counter()
+        for lane in list(range(g0, g0 + 8)) + list(range(g0 + 16, g0 + 24)):
+            for d in range(4):
+                cnt[((addrs[lane] // 4) + d) % 64] += 1
+        worst = max(worst, max(cnt.values()))
+    return worst
+
+
+def check_ct_reads(lds, swap=True):
+    worst = 0
+    for wn, ni, kh in itertools.product(range(2), range(8), range(2)):
+        addrs = [ct_read(wn, ni, kh, lane, swap) for lane in range(64)]
+        for lane, a in enumerate(addrs):
+            assert a % 16 == 0 and 0 <= a < 32768
+            assert lds[a] == (wn * 128 + 8 * (lane & 15) + ni, kh * 4 + (lane >> 4))
+        worst = max(worst, read_pass_worst(addrs))
+    return worst
+
+
+def test_row_major_acc_b_layout_conflict_free():
+    lds = ct_stage()
+    assert check_ct_reads(lds) == 1
+
+
+def test_row_major_acc_b_layout_without_the_row_swap_conflicts():
+    """The layout before the row swap: the same words, but every read pass puts its 16 requests on
+    one half of the banks (2-way; measured 33 % SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE)."""
+    assert check_ct_reads(ct_stage(swap=False), swap=False) == 2
+
+
+def test_read_pass_model_on_the_k_major_layout():
+    """The K-major fragment reads of A (and of B in C^T instances), chunk c at c ^ (r % 8), rows
+    16 ni + l % 16: conflict-free under the same pass model (measured 0.0-0.2 %)."""
+    for ni, kh in itertools.product(range(8), range(2)):
+        addrs = [(16 * ni + (lane & 15)) * 128 + (((4 * kh + (lane >> 4)) ^ (lane & 7)) * 16) for lane in range(64)]
+        assert read_pass_worst(addrs) == 1
+
+
+def test_row_major_acc_b_dma_k_tail_chunks():
+    """The partial last K step masks B's DMA lanes by the logical chunk of their DMA's parity
+    (ktail_ct[j & 1]): (l % 8) ^ ((4 p + wave) % 8) for p = j % 2."""
+    for w, j, lane in itertools.product(range(4), range(8), range(64)):
+        _, chunk = ct_dma(w, j, lane)
+        p = j & 1
+        assert chunk == (lane & 7) ^ ((4 * p + w) & 7)
+
+
+def test_row_major_acc_stores_cover_the_tile():
+    """store_ct: store s of row block mi, lane l writes row 16 (2 mi + wm) + 4 (l / 16) + s at
+    columns wn * 128 + 8 (l % 16) .. +7, element s of column blocks 0..7 (column slot l % 16 of
+    block ni = column 8 (l % 16) + ni); the MFMA output lane l of block (mi, ni) holds rows
+    4 (l / 16) + e, column slot l % 16. Every output of the 256 x 256 tile is written once, from
+    the accumulator that holds it, and 4 consecutive lanes write 64 contiguous bytes of a row."""
+    seen = {}
+    for wave, mi, s, lane in itertools.product(range(4), range(8), range(4), range(64)):
+        wm, wn, q = wave >> 1, wave & 1, lane >> 4
+        row = (wm * 16 + 4 * q) + 32 * mi + s
+        col0 = wn * 128 + 8 * (lane & 15)
+        for ni in range(8):
+            # the accumulator element (wave, mi, ni, lane, e = s): D[4 q + e][l % 16] of block (mi, ni)
+            out = (16 * (2 * mi + wm) + 4 * q + s, wn * 128 + 8 * (lane & 15) + ni)
+            assert out == (row, col0 + ni)
+            assert out not in seen
+            seen[out] = (wave, mi, ni, lane, s)
+    assert len(seen) == 256 * 256
+    for lane0 in range(0, 64, 4):
+        cols = [8 * ((lane0 + x) & 15) for x in range(4)]
+        rows = {(lane0 + x) >> 4 for x in range(4)}
+        assert len(rows) == 1 and cols == [cols[0] + 8 * x for x in range(4)] and cols[0] % 32 == 0
+
+
+def test_row_major_acc_partial_slab_order():
+    """Tail-split K ranges store fp32 partial sums as a row-major 256 x 256 slab (float index
+    row * 256 + column); tail_reduce_kernel's position p reads floats 4 p .. 4 p + 3 as row p / 64,
+    columns 4 (p % 64) .. +3."""
+    written = set()
+    for wave, mi, s, lane, hf in itertools.product(range(4), range(8), range(4), range(64), range(2)):
+        wm, wn, q = wave >> 1, wave & 1, lane >> 4
+        ecol = wn * 128 + 8 * (lane & 15)
+        byte = (((wm * 16 + 4 * q) * 256 + ecol) * 4) + ((32 * mi + s) * 256) * 4 + 16 * hf
+        for t in range(4):
+            f = byte // 4 + t
+            ni = 4 * hf + t
+            assert f == (16 * (2 * mi + wm) + 4 * q + s) * 256 + ecol + ni
+            written.add(f)
+    assert written == set(range(65536))
+    for p in range(16384):
+        assert 4 * p == (p >> 6) * 256 + 4 * (p & 63)
