@@ -913,7 +913,7 @@ __device__ unsigned long long g_stamps[kStampWgs * kStampSlots];
 #endif
 constexpr bool kTailSkip = GG_TAIL_SKIP;
 
-// Row-major accumulators (whole-tile 16-bit forward, cross-tile): the x fragment
+// Row-major accumulators (whole-tile 16-bit and fp8 forward, cross-tile): the x fragment
 // is the MFMA's first source, so lane l of block (mi, ni) holds output column slot l%16 of rows
 // 4 (l/16) .. +3; column slot s of block ni is tile column 8 s + ni of the wave's 128 (the w
 // fragment of block ni gathers w rows ni, ni + 8, ..). Over its 8 blocks a lane then holds 8
@@ -925,7 +925,10 @@ constexpr bool kTailSkip = GG_TAIL_SKIP;
 #define GG_CT 1
 #endif
 constexpr bool ct_instance(int mode, int shape, bool cross) {
-    return GG_CT && mode == make_mode(kFwd, kIn16) && shape == kShapeWide && cross;
+    // the 16-bit forward and the fp8 forward (both operands of one format: the MFMA's format
+    // modifiers follow the operands when x becomes its first source)
+    return GG_CT && (mode == make_mode(kFwd, kIn16) || mode == make_mode(kFwd, kInE4M3) || mode == make_mode(kFwd, kInE5M2)) &&
+           shape == kShapeWide && cross;
 }
 
 
@@ -1154,7 +1157,8 @@ grouped_gemm_kernel(const KernelArgs args) {
         // row-major accumulators: lane l reads stored w row 8 (l%16) + ni, at LDS row
         // 8 (l%16) + (ni ^ (l & 1)), whose chunk c sits at c ^ (l%8): block ni adds 128 ni to the
         // base of its parity (frag_b for even ni, frag_bo for odd ni, 256 lower for odd lanes)
-        const int ct_off = (8 * fr_row + (fr_row & 1)) * kRowBytes + (((kh * 4 + fr_q) ^ (fr_row & 7)) * 16);
+        const int ct_off = (8 * fr_row + (fr_row & 1)) * kRowBytes +
+                           (((F8 ? 2 * fr_q + (kh ^ (fr_q & 1)) : kh * 4 + fr_q) ^ (fr_row & 7)) * 16);
         frag_bo[kh]   = wn * WCOLS * kRowBytes + ct_off - (fr_row & 1) * 2 * kRowBytes;
         frag_b[kh]    = CT    ? wn * WCOLS * kRowBytes + ct_off
                         : !B_MN ? wn * WCOLS * kRowBytes + off
@@ -1752,12 +1756,17 @@ grouped_gemm_kernel(const KernelArgs args) {
     // the block at columns ecol .. +7, element s of its 8 column blocks' accumulators (column slot
     // l%16 of block ni is column 8 (l%16) + ni). Columns past n_valid get an out-of-range offset
     // (N % 8 == 0: a 16-byte chunk is all valid or all past N); rows past m_valid fall outside crs.
-    auto store_ct = [&](auto r, auto s_, const __amdgpu_buffer_rsrc_t &crs, int n_valid) {
+    // fp8: scaled by the tile's x scale * w[g] scale (`scale`) before the conversion.
+    auto store_ct = [&](auto r, auto s_, const __amdgpu_buffer_rsrc_t &crs, int n_valid, float scale) {
         u32x4 d;
         sfor<0, 4>([&](auto u) {
             // reads of these accumulators may not move above this point
             asm volatile("" : "+a"(acc[r][2 * u]), "+a"(acc[r][2 * u + 1]));
-            const float v0 = acc[r][2 * u][int(s_)], v1 = acc[r][2 * u + 1][int(s_)];
+            float v0 = acc[r][2 * u][int(s_)], v1 = acc[r][2 * u + 1][int(s_)];
+            if constexpr (F8) {
+                v0 *= scale;
+                v1 *= scale;
+            }
             if constexpr (F16)
                 d[int(u)] = __builtin_bit_cast(unsigned, f16x2{(_Float16)v0, (_Float16)v1});
             else
@@ -1778,7 +1787,7 @@ grouped_gemm_kernel(const KernelArgs args) {
     auto epi_store = [&](auto r, auto s_) {
         sched_fence();
         if constexpr (CT) {
-            store_ct(r, s_, prev_crs, prev_n);
+            store_ct(r, s_, prev_crs, prev_n, prev_scale);
         } else if constexpr (s_ == 4) {
             store_block9(r, prev_crs, prev_n);
         } else {
@@ -1797,7 +1806,10 @@ grouped_gemm_kernel(const KernelArgs args) {
         } else if constexpr (F8) {
             const i32x8 bw = __builtin_shufflevector(fb[SA][ni][0], fb[SA][ni][1], 0, 1, 2, 3, 4, 5, 6, 7);
             const i32x8 ax = __builtin_shufflevector(fa[mi & 1][0], fa[mi & 1][1], 0, 1, 2, 3, 4, 5, 6, 7);
-            mfma8<mode_b_e5(MODE), mode_a_e5(MODE), FIRST>(acc[mi][ni], bw, ax);
+            if constexpr (CT) // row-major accumulators: x is the first source (cbsz: x's format)
+                mfma8<mode_a_e5(MODE), mode_b_e5(MODE), FIRST>(acc[mi][ni], ax, bw);
+            else
+                mfma8<mode_b_e5(MODE), mode_a_e5(MODE), FIRST>(acc[mi][ni], bw, ax);
         } else if constexpr (CT && FIRST && kh == 0) // row-major accumulators: x is the first source
             mfma_first<F16>(acc[mi][ni], fa[mi & 1][0], fb[SA][ni][0]);
         else if constexpr (CT)
@@ -2083,7 +2095,7 @@ grouped_gemm_kernel(const KernelArgs args) {
                                                                poff + ((32 * mi + s_) * 256) * 4 + 16 * hf, 0, 0);
                     });
                 }
-                store_ct(mi, s_, crs, tl.n_valid);
+                store_ct(mi, s_, crs, tl.n_valid, tl.scale);
             });
         });
     } else if constexpr (CROSS) {
