@@ -926,9 +926,12 @@ constexpr bool kTailSkip = GG_TAIL_SKIP;
 #endif
 constexpr bool ct_instance(int mode, int shape, bool cross) {
     // the 16-bit forward and the fp8 forward (both operands of one format: the MFMA's format
-    // modifiers follow the operands when x becomes its first source)
-    return GG_CT && (mode == make_mode(kFwd, kIn16) || mode == make_mode(kFwd, kInE4M3) || mode == make_mode(kFwd, kInE5M2)) &&
-           shape == kShapeWide && cross;
+    // modifiers follow the operands when x becomes its first source), 256-column tiles; and the
+    // 16-bit forward's short-wide tiles, whose ninth column block keeps C^T accumulators
+    return GG_CT && cross &&
+           (((mode == make_mode(kFwd, kIn16) || mode == make_mode(kFwd, kInE4M3) || mode == make_mode(kFwd, kInE5M2)) &&
+             shape == kShapeWide) ||
+            (mode == make_mode(kFwd, kIn16) && shape == kShapeShortWide));
 }
 
 
@@ -946,9 +949,11 @@ constexpr bool ct_instance(int mode, int shape, bool cross) {
 // of blocks 6 and 7 are compiled out and the memory schedule is unchanged: the A DMAs of rows
 // past tile_m fall outside the bounded resource (zeros, no traffic).
 // SHAPE kShapeShortWide (cross-tile 16-bit forward): tiles of args.tile_m <= 192 rows x 288. Each
-// wave takes 6 interleaved row blocks and 9 column blocks (columns 144 wn ..), on its own slot
-// plan (PlanSW) with A stages of 192 rows and B stages of 288 rows; the ninth column block is
-// stored on its own (16-byte lines) in the fused stores and as a second pass of the LDS epilogue.
+// wave takes 6 interleaved row blocks and 9 column blocks, on its own slot
+// plan (PlanSW) with A stages of 192 rows and B stages of 288 rows. With row-major accumulators
+// (GG_CT) a wave's columns are 128 wn .. +128 (8 row-major blocks) and 256 + 16 wn .. +16 (the
+// ninth block, C^T, stored on its own with 8 bytes per lane); otherwise 144 wn .. +144 and the
+// ninth block goes out in the fused stores and as a second pass of the LDS epilogue.
 // TAIL (cross-tile 16-bit forward only): the plan cuts its last-round tiles into K ranges (tail
 // split: K ranges of last-round tiles store partial sums from epilogue_lds); instances without it
 // carry none of its state.
@@ -996,7 +1001,8 @@ grouped_gemm_kernel(const KernelArgs args) {
     static_assert(!SWIDE || (NBLK == P::nc && RB == P::rows), "short-wide plan");
     // row-major accumulators (GG_CT): whole 256 x 256 tiles of the 16-bit forward, cross-tile
     constexpr bool CT = ct_instance(MODE, SHAPE, CROSS);
-    static_assert(!CT || (RB == 8 && NBLK == 8 && P::nc == 8), "row-major accumulators: whole tiles");
+    static_assert(!CT || (RB == 8 && NBLK == 8 && P::nc == 8) || (SWIDE && NBLK == 9 && P::nc == 9),
+                  "row-major accumulators: whole tiles, or short-wide tiles (ninth block C^T)");
     constexpr int B_BLK = CT ? 1 : 16; // LDS rows between the w fragments of consecutive column blocks
     constexpr int NC   = P::nc;                                     // column blocks in the registers
     constexpr int A_ST = P::la * kWaves * 1024;                     // bytes of an A stage
@@ -1107,7 +1113,7 @@ grouped_gemm_kernel(const KernelArgs args) {
     sfor<0, LV>([&](auto j) {
         voff[0][j] = dma_off(A_MN, j, args.lda);
         if constexpr (!kSameOff)
-            voff[1][j] = dma_off(B_MN, j, args.ldb, CT);
+            voff[1][j] = dma_off(B_MN, j, args.ldb, CT && j < 8);
     });
     // MN-major operands in unchecked steps: the lane offsets with the current tile's column mask
     // already applied (set once per tile by set_mn_offsets), and the K step in soffset. Every
@@ -1146,7 +1152,8 @@ grouped_gemm_kernel(const KernelArgs args) {
     // 8 rows of a group take 8 different slots, and groups of odd q the other half of the banks.
     const int fr_row = lane & 15, fr_q = lane >> 4;
     const int mn8    = fr_q * 8192 + (fr_row >> 1) * (256 + 16) + (fr_row & 1) * 8;
-    int frag_a[2], frag_b[2], frag_bo[2]; // frag_bo: odd column blocks of row-major accumulators
+    int frag_a[2], frag_b[2], frag_bo[2], frag_b8[2]; // frag_bo / frag_b8: row-major accumulators'
+                                                      // odd column blocks / short-wide ninth block
     sfor<0, 2>([&](auto kh) {
         const int off = fr_row * kRowBytes +
                         (((F8 ? 2 * fr_q + (kh ^ (fr_q & 1)) : kh * 4 + fr_q) ^ (fr_row & 7)) * 16);
@@ -1159,8 +1166,11 @@ grouped_gemm_kernel(const KernelArgs args) {
         // base of its parity (frag_b for even ni, frag_bo for odd ni, 256 lower for odd lanes)
         const int ct_off = (8 * fr_row + (fr_row & 1)) * kRowBytes +
                            (((F8 ? 2 * fr_q + (kh ^ (fr_q & 1)) : kh * 4 + fr_q) ^ (fr_row & 7)) * 16);
-        frag_bo[kh]   = wn * WCOLS * kRowBytes + ct_off - (fr_row & 1) * 2 * kRowBytes;
-        frag_b[kh]    = CT    ? wn * WCOLS * kRowBytes + ct_off
+        frag_bo[kh]   = wn * 128 * kRowBytes + ct_off - (fr_row & 1) * 2 * kRowBytes;
+        // short-wide tiles: the ninth block (stored rows 256 + 16 wn + l%16, C^T layout), based so
+        // that read_frag's 128 * 8 for block 8 lands on it
+        frag_b8[kh]   = (256 + 16 * wn - 8) * kRowBytes + off;
+        frag_b[kh]    = CT    ? wn * 128 * kRowBytes + ct_off
                         : !B_MN ? wn * WCOLS * kRowBytes + off
                         : F8  ? mn8 + 128 * (wn ^ (fr_q & 1))
                               : wn * 1024 + mn;
@@ -1181,6 +1191,7 @@ grouped_gemm_kernel(const KernelArgs args) {
     int      rot_a = 0, rot_b = 0;
     int      a_rd[2][2], b_rd[3][2]; // LDS read base per logical stage and k-half
     int      b_rdo[3][2];            // row-major accumulators: B's base for odd column blocks
+    int      b_rd8[3][2];            // ... and for a short-wide tile's ninth block
     uint32_t a_dst[2], b_dst[3];     // this wave's DMA destination per logical stage
     auto set_stages = [&]() {
         sfor<0, 2>([&](auto L) {
@@ -1196,6 +1207,8 @@ grouped_gemm_kernel(const KernelArgs args) {
             sfor<0, 2>([&](auto h) { b_rd[L][h] = frag_b[h] + p; });
             if constexpr (CT)
                 sfor<0, 2>([&](auto h) { b_rdo[L][h] = frag_bo[h] + p; });
+            if constexpr (CT && SWIDE)
+                sfor<0, 2>([&](auto h) { b_rd8[L][h] = frag_b8[h] + p; });
         });
     };
     // Re-materialise loop-invariant offsets at the top of every loop body (see fresh_v).
@@ -1231,6 +1244,8 @@ grouped_gemm_kernel(const KernelArgs args) {
             sfor<0, 2>([&](auto h) { fresh_v(b_rd[L][h]); });
             if constexpr (CT)
                 sfor<0, 2>([&](auto h) { fresh_v(b_rdo[L][h]); });
+            if constexpr (CT && SWIDE)
+                sfor<0, 2>([&](auto h) { fresh_v(b_rd8[L][h]); });
         });
     };
     auto lds_read = [&](int off) -> i32x4 { return *reinterpret_cast<const i32x4 *>(smem + off); };
@@ -1263,7 +1278,9 @@ grouped_gemm_kernel(const KernelArgs args) {
     // B's read bases of logical stage L for column block blk (odd blocks of row-major
     // accumulators have their own, see frag_bo)
     auto b_base = [&](int L, auto blk) -> const int(&)[2] {
-        if constexpr (CT && (decltype(blk)::value & 1))
+        if constexpr (CT && decltype(blk)::value == 8)
+            return b_rd8[L];
+        else if constexpr (CT && (decltype(blk)::value & 1))
             return b_rdo[L];
         else
             return b_rd[L];
@@ -1417,7 +1434,9 @@ grouped_gemm_kernel(const KernelArgs args) {
         }
         if constexpr (F8)
             tl.scale = to_const_space(args.x_scale)[0] * to_const_space(args.w_scale)[g];
-        tl.rows = __builtin_amdgcn_readfirstlane(active_rows(ILV, tl.m_valid, tl.n_valid, wm, wn, SWIDE ? WCOLS : 128));
+        // a short-wide wave with row-major accumulators owns columns 128 wn .. +128 and 256 + 16 wn ..
+        // +16: it holds a valid column iff 128 wn < n_valid, as for 256-column tiles
+        tl.rows = __builtin_amdgcn_readfirstlane(active_rows(ILV, tl.m_valid, tl.n_valid, wm, wn, SWIDE && !CT ? WCOLS : 128));
         return tl;
     };
     auto c_rsrc = [&](const Tile &tl) {
@@ -1450,6 +1469,7 @@ grouped_gemm_kernel(const KernelArgs args) {
     struct DmaSrc {
         i32x4 rs;
         int   so, vadd, mask, mask1; // MN-major: mask for even / odd DMA j (column-block swap)
+        int   mask8;                 // B's DMA 8 of short-wide row-major tiles (C^T rows)
     };
     auto dma_src = [&](auto b_op, int kidx, auto checked) -> DmaSrc {
         constexpr bool B  = decltype(b_op)::value;
@@ -1493,6 +1513,7 @@ grouped_gemm_kernel(const KernelArgs args) {
                 const bool tail_step = KT && koff == T - 1 && cur.klast;
                 d.mask  = tail_step ? (B && CT ? ktail_ct[0] : ktail_bad) : 0;
                 d.mask1 = tail_step && B && CT ? ktail_ct[1] : 0; // odd DMAs of B (row-major acc.)
+                d.mask8 = tail_step ? ktail_bad : 0;
             }
         } else {
             d.rs = rc;
@@ -1522,7 +1543,7 @@ grouped_gemm_kernel(const KernelArgs args) {
         else if constexpr (MN)
             return (vo + d.vadd) | (mn_swz(j) ? d.mask1 : d.mask);
         else if constexpr (decltype(checked)::value)
-            return vo | ((B && CT && (j & 1)) ? d.mask1 : d.mask);
+            return vo | ((B && CT && j == 8) ? d.mask8 : (B && CT && (j & 1)) ? d.mask1 : d.mask);
         else
             return vo;
     };
@@ -1745,7 +1766,7 @@ grouped_gemm_kernel(const KernelArgs args) {
         f32x4 v = acc[r][NC - 1];
         if constexpr (F8)
             v *= prev_scale;
-        const int col = wn * WCOLS + 128 + (lane >> 4) * 4;
+        const int col = (CT ? 256 + 16 * wn : wn * WCOLS + 128) + (lane >> 4) * 4;
         uint32_t  bs  = static_cast<uint32_t>(blk_stride);
         fresh_s(bs);
         const int vo = col < n_valid ? ((wm * 16 + (lane & 15)) * N + col) * 2 + r * static_cast<int>(bs)
@@ -1786,7 +1807,7 @@ grouped_gemm_kernel(const KernelArgs args) {
     constexpr int kEpiStores = SWIDE ? 5 : 4;
     auto epi_store = [&](auto r, auto s_) {
         sched_fence();
-        if constexpr (CT) {
+        if constexpr (CT && s_ < 4) {
             store_ct(r, s_, prev_crs, prev_n, prev_scale);
         } else if constexpr (s_ == 4) {
             store_block9(r, prev_crs, prev_n);
@@ -1810,9 +1831,9 @@ grouped_gemm_kernel(const KernelArgs args) {
                 mfma8<mode_a_e5(MODE), mode_b_e5(MODE), FIRST>(acc[mi][ni], ax, bw);
             else
                 mfma8<mode_b_e5(MODE), mode_a_e5(MODE), FIRST>(acc[mi][ni], bw, ax);
-        } else if constexpr (CT && FIRST && kh == 0) // row-major accumulators: x is the first source
+        } else if constexpr (CT && ni < 8 && FIRST && kh == 0) // row-major accumulators: x is the first source
             mfma_first<F16>(acc[mi][ni], fa[mi & 1][0], fb[SA][ni][0]);
-        else if constexpr (CT)
+        else if constexpr (CT && ni < 8)
             mfma<F16>(acc[mi][ni], fa[mi & 1][kh], fb[SA][ni][kh]);
         else if constexpr (FIRST && kh == 0)
             mfma_first<F16>(acc[mi][ni], fb[SA][ni][0], fa[mi & 1][0]);
@@ -2083,7 +2104,9 @@ grouped_gemm_kernel(const KernelArgs args) {
         const __amdgpu_buffer_rsrc_t prs =
             __builtin_amdgcn_make_buffer_rsrc(args.ws, static_cast<short>(0), part ? 0x7fffffff : 0, 0x00020000);
         const int poff = part ? (((tl.tail_k * rem + tl.tail) * 256 + wm * 16 + 4 * (lane >> 4)) * 256 + ecol) * 4 : 0;
-        sfor<0, 8>([&](auto mi) {
+        sfor<0, RB>([&](auto mi) { // short-wide tiles: 6 row blocks, and the ninth column block
+            if constexpr (SWIDE)
+                store_block9(mi, crs, tl.n_valid);
             sfor<0, 4>([&](auto s_) {
                 if constexpr (TAIL) {
                     sfor<0, 2>([&](auto hf) {
