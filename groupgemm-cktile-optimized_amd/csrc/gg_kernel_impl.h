@@ -887,7 +887,9 @@ __device__ __forceinline__ LaneGroup lane_group_table(const int64_t *lens, const
 // (s_memtime) into slot i of g_stamps[w * kStampSlots ..] with a vector store: 0 kernel start,
 // 1 after the prologue, 2 + 5 j .. 6 + 5 j for the workgroup's tile j < 7 (before its first K
 // step, after it, after the unchecked steps, after locating the next tile, after the last step),
-// 62 before the final LDS epilogue (cross-tile), 63 kernel end. The stores count in vmcnt and only make the hand-placed waits longer.
+// 62 before the final LDS epilogue (cross-tile), 63 kernel end; slots 48 and 49 hold the constant
+// 100 MHz clock (s_memrealtime, one counter for the whole GPU) at kernel start and end. The stores
+// count in vmcnt and only make the hand-placed waits longer.
 #ifndef GG_STAMPS
 #define GG_STAMPS 0
 #endif
@@ -900,11 +902,21 @@ __device__ unsigned long long g_stamps[kStampWgs * kStampSlots];
         if (threadIdx.x == 0 && (i) < kStampSlots && blockIdx.x < kStampWgs)                          \
             g_stamps[blockIdx.x * kStampSlots + (i)] = t_stamp_;                                      \
     } while (0)
+#define GG_STAMP_REAL(i)                                                                              \
+    do {                                                                                              \
+        const unsigned long long t_stamp_ = __builtin_amdgcn_s_memrealtime();                         \
+        if (threadIdx.x == 0 && blockIdx.x < kStampWgs)                                               \
+            g_stamps[blockIdx.x * kStampSlots + (i)] = t_stamp_;                                      \
+    } while (0)
 #else
 #define GG_STAMP(i) \
     do {            \
     } while (0)
+#define GG_STAMP_REAL(i) \
+    do {                 \
+    } while (0)
 #endif
+constexpr int kStampRealStart = 48, kStampRealEnd = 49;
 
 // Partial tiles: a wave skips the MFMAs of its 16-row blocks that hold no valid output (1), or
 // computes every block (0).
@@ -1451,6 +1463,7 @@ grouped_gemm_kernel(const KernelArgs args) {
     if (t >= total_units)
         return;
     GG_STAMP(0);
+    GG_STAMP_REAL(kStampRealStart);
     [[maybe_unused]] int stamp_tile = 0; // GG_STAMPS: tiles of this workgroup so far
     int  tile_i = 0; // this workgroup's tile count so far (unit t = blockIdx.x + tile_i * grid)
     Tile cur = make_tile(t, 0), nxt = cur;
@@ -2077,6 +2090,7 @@ grouped_gemm_kernel(const KernelArgs args) {
             else
                 epilogue_lds(cur);
             if (!more) {
+                GG_STAMP_REAL(kStampRealEnd);
                 GG_STAMP(kStampSlots - 1);
                 return;
             }
@@ -2125,6 +2139,7 @@ grouped_gemm_kernel(const KernelArgs args) {
         GG_STAMP(kStampSlots - 2);
         epilogue_lds(cur); // TAIL: a K range's partial sums instead of its C tile
     }
+    GG_STAMP_REAL(kStampRealEnd);
     GG_STAMP(kStampSlots - 1);
 }
 

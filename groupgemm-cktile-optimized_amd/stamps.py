@@ -76,6 +76,31 @@ def unchecked_steps(T: int, masks: bool) -> int:
     return 6 * passes
 
 
+REAL_START, REAL_END = 48, 49  # s_memrealtime at kernel start and end (kStampRealStart / End)
+
+
+def per_xcd(st: np.ndarray, hz: float, n_xcd: int = 8) -> list:
+    """Wall time and shader clock per XCD from the constant-rate stamps (workgroup w runs on XCD
+    w % n_xcd). Times in microseconds from the launch's first workgroup start."""
+    grid = st.shape[0]
+    t0 = st[:, REAL_START].min()
+    rows = []
+    for x in range(min(n_xcd, grid)):
+        w = np.arange(x, grid, n_xcd)
+        ticks = (st[w, REAL_END] - st[w, REAL_START]).astype(np.float64)
+        cyc = (st[w, 63] - st[w, 0]).astype(np.float64)
+        rows.append({
+            "xcd": x,
+            "start_us_max": float((st[w, REAL_START] - t0).max() / hz * 1e6),
+            "end_us_mean": float((st[w, REAL_END] - t0).mean() / hz * 1e6),
+            "end_us_max": float((st[w, REAL_END] - t0).max() / hz * 1e6),
+            "wall_us_mean": float(ticks.mean() / hz * 1e6),
+            "cycles_mean": float(cyc.mean()),
+            "mhz": float((cyc / (ticks / hz)).mean() / 1e6),
+        })
+    return rows
+
+
 def analyse(st: np.ndarray, T: int, masks: bool) -> dict:
     """st: [grid, 64] stamps of one launch (int64); masks: the instance has tail masks."""
     grid = st.shape[0]
@@ -125,6 +150,10 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     sh = torch.cuda.current_stream(dev).cuda_stream
+    words = torch.zeros(5, dtype=torch.int64, device=dev)
+    lib.gg_clock_probe(words.data_ptr(), 0.001, sh)  # its fifth word: the constant clock's rate (Hz)
+    torch.cuda.synchronize()
+    real_hz = float(words[4].item())
     dt = pkg.DType.FP16 if args.fp16 else pkg.DType.BF16
     tdt = torch.float16 if args.fp16 else torch.bfloat16
     results = []
@@ -185,6 +214,8 @@ def main():
         else:
             masks = k % ks != 0
         r = analyse(best, -(-contraction // ks), masks)
+        if real_hz > 0 and (best[:, REAL_START] > 0).all() and (best[:, REAL_END] > 0).all():
+            r["per_xcd"] = per_xcd(best, real_hz)
         r.update({"shape": [b, m, n, k], "plan": detail, "stamps": best.tolist()})
         results.append(r)
         print(f"  {detail}", flush=True)
@@ -197,6 +228,10 @@ def main():
         if "boundary" in r:
             print(f"  tile {r['tile_cycles']:.0f} cycles, of which {r['boundary']:.0f} beyond its K steps at the "
                   f"unchecked rate", flush=True)
+        for x in r.get("per_xcd", []):
+            print(f"  XCD {x['xcd']}: wall {x['wall_us_mean']:8.1f} us, ends at {x['end_us_mean']:8.1f} "
+                  f"(max {x['end_us_max']:8.1f}, last start {x['start_us_max']:6.1f}) us, {x['cycles_mean']:10.0f} "
+                  f"cycles, {x['mhz']:7.1f} MHz", flush=True)
     if args.json:
         os.makedirs(os.path.dirname(os.path.abspath(args.json)), exist_ok=True)
         with open(args.json, "w") as f:
