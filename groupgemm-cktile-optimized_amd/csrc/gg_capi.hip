@@ -672,8 +672,13 @@ int plan_device_lens(gg_plan *plan, bool noalloc, int op, int a_dtype, int b_dty
         ka.d_total     = &plan->d_header->total_tiles;
     }
     // At most kInKernelTableGroups groups: the GEMM builds the table itself (one group per lane of
-    // every wave) and writes the header, so a run is one launch.
-    if (group_num <= gg::kInKernelTableGroups) {
+    // every wave) and writes the header, so a run is one launch. Not for an fp8 wgrad plan that
+    // would run the per-tile variant (only in builds without the cross-tile pipeline): that
+    // instance has no in-kernel table.
+    gg::KernelArgs probe = ka;
+    probe.d_lens         = group_lens;
+    const bool lane_table_ok = !(f8 && op == GG_OP_WGRAD && !gg::uses_cross_tile(probe, plan->grid, plan->mode));
+    if (group_num <= gg::kInKernelTableGroups && lane_table_ok) {
         plan->in_kernel_table = true;
         ka.d_lens             = group_lens;
         ka.d_offs             = group_offs;

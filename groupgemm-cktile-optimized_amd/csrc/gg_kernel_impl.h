@@ -1037,7 +1037,11 @@ grouped_gemm_kernel(const KernelArgs args) {
     int       T = args.k_tiles; // K steps of the current tile (per group for wgrad)
     // In-kernel group table (device-resident sizes, at most 64 groups): every wave builds it,
     // lane g holding group g; workgroup 0 reports the tile count and the first invalid group.
-    const bool in_kernel_table = !SHORT && args.d_lens != nullptr; // short tiles: host tables only
+    // Short tiles and the per-tile fp8 wgrad instances take host-built tables only: the host never
+    // plans them with an in-kernel table (a device-size wgrad plan runs cross-tile), and the lane
+    // table's registers would push the fp8 wgrad instance with tail masks past 256 VGPRs.
+    constexpr bool kLaneTable = !SHORT && !(F8 && !CROSS && LAYOUT == kWgrad);
+    const bool     in_kernel_table = kLaneTable && args.d_lens != nullptr;
     LaneGroup  lgrp{0, 0, 0, 0};
     int        lg_total = 0;
     if (in_kernel_table) {

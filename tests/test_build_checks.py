@@ -6,6 +6,8 @@
   wait states, across a fall-through and a loop's back edge; reads of other AGPRs pass; SGPR
   spill traffic in a K-loop block (many MFMAs) fails, in a single step's block it does not.
 - The product library carries no cycle stamps (those are the `make stamps` build's).
+- Every GEMM instance of the product library compiles with 0 VGPR spills and 0 scratch (the
+  compiler's resource report, lib/resource_usage.txt).
 """
 import importlib.util
 import os
@@ -165,3 +167,29 @@ def test_product_library_has_no_cycle_stamps():
         pytest.skip("library not built")
     lib = ctypes.CDLL(path)
     assert not hasattr(lib, "gg_stamps_read_p0") and not hasattr(lib, "gg_stamps_clear_p18")
+
+
+def test_no_vgpr_spills_or_scratch_in_any_instance():
+    """The compiler's report of every grouped_gemm_kernel instance (Function Name, then its
+    VGPRs Spill and ScratchSize lines) shows no VGPR spill and no scratch: spilled values would
+    travel through memory, next to the operand DMAs."""
+    import re
+    import pytest
+    path = os.path.join(ROOT, "groupgemm-cktile-optimized_amd", "lib", "resource_usage.txt")
+    if not os.path.exists(path):
+        pytest.skip("library not built")
+    seen, bad, cur = 0, [], None
+    with open(path, errors="replace") as f:
+        for line in f:
+            m = re.search(r"Function Name: (\S+)", line)
+            if m:
+                cur = m.group(1) if "grouped_gemm_kernel" in m.group(1) else None
+                seen += cur is not None
+                continue
+            if cur is None:
+                continue
+            m = re.search(r"\s(VGPRs Spill|ScratchSize \[bytes/lane\]): (\d+)", line)
+            if m and int(m.group(2)) != 0:
+                bad.append((cur, m.group(1), int(m.group(2))))
+    assert seen >= 60, seen  # every (type, mode, shape, variant) instance is in the report
+    assert not bad, bad
