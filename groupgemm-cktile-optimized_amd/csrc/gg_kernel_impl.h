@@ -823,6 +823,11 @@ template <bool F16> __device__ __forceinline__ u32x2 pack4(const f32x4 &v) {
 constexpr bool kCrossAllowed  = GG_CROSS_TILE;
 constexpr int  kCrossMinSteps = kCrossMinStepsHost; // the three prefetching steps follow the first
 constexpr int  kStoreCpol     = GG_STORE_CPOL;
+// The ninth column block of short-wide tiles goes out in 32-byte row pieces, the two halves of
+// each 64-byte piece from two waves: with the default (write-back) policy the halves meet in L2
+// and leave as one write; non-temporal, each half went out on its own and the launch wrote 1.13x
+// its output bytes (32 x 520 x 2880 x 2880; 1.00x now, same time).
+constexpr int kStoreCpolHalf = 0;
 #ifndef GG_PARTIAL_NT
 #define GG_PARTIAL_NT 0
 #endif
@@ -1788,7 +1793,7 @@ grouped_gemm_kernel(const KernelArgs args) {
         fresh_s(bs);
         const int vo = col < n_valid ? ((wm * 16 + (lane & 15)) * N + col) * 2 + r * static_cast<int>(bs)
                                      : static_cast<int>(0x80000000u);
-        __builtin_amdgcn_raw_buffer_store_b64(pack4<F16>(v), crs, vo, 0, kStoreCpol);
+        __builtin_amdgcn_raw_buffer_store_b64(pack4<F16>(v), crs, vo, 0, kStoreCpolHalf);
     };
     // Row-major accumulators: store s (0-3) of row block r, lane l writing row 4 (l/16) + s of
     // the block at columns ecol .. +7, element s of its 8 column blocks' accumulators (column slot
