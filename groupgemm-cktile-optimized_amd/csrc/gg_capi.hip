@@ -110,7 +110,7 @@ void fill_args(gg_plan *plan, int n_xcd) {
     a.n_tiles   = static_cast<int>(gg::cdiv(plan->n, gg::kTileN));
     a.k_tiles   = static_cast<int>(gg::cdiv(plan->k, gg::kTileK));
     a.n_xcd     = plan->grid % n_xcd == 0 ? n_xcd : 1;
-    a.band      = gg::kBand;
+    a.band      = gg::band_for(plan->n, plan->k, plan->mode / 4 == gg::kIn16 ? 2 : 1);
     // GG_BAND=<1..64> in the environment overrides the M-tiles per band of the in-group order
     // (measurements only)
     if (const char *env = std::getenv("GG_BAND"); env != nullptr && std::atoi(env) >= 1 && std::atoi(env) <= 64)
@@ -207,14 +207,14 @@ int use_narrow_tiles(gg_plan *plan, const int64_t *group_m, const hipDeviceProp_
 // 129-255 rows, and 0.70-0.85 for at most 128 rows (thin steps); with short tiles (at most 192
 // rows, six row blocks per wave) the same below 129 rows and 0.85-0.88 above.
 double busiest_workgroup(const int64_t *group_m, int group_num, int64_t n_tiles, int tile_m, int tiles,
-                         int grid, int n_xcd) {
+                         int grid, int n_xcd, int band) {
     std::vector<float> cost(static_cast<size_t>(tiles));
     int                L = 0;
     for (int g = 0; g < group_num; ++g) {
         const int m_tiles = static_cast<int>(gg::cdiv(group_m[g], tile_m));
         for (int local = 0; local < m_tiles * n_tiles; ++local, ++L) {
             int tm, tn;
-            gg::band_coords(local, m_tiles, static_cast<int>(n_tiles), gg::kBand, &tm, &tn);
+            gg::band_coords(local, m_tiles, static_cast<int>(n_tiles), band, &tm, &tn);
             const double m = static_cast<double>(std::min<int64_t>(tile_m, group_m[g] - int64_t(tm) * tile_m));
             double       c;
             if (m <= 128)
@@ -250,9 +250,9 @@ int use_short_tiles(gg_plan *plan, const int64_t *group_m, hipStream_t s) {
         return GG_OK;
     if (opt != 1) {
         const double wide  = busiest_workgroup(group_m, plan->group_num, a.n_tiles, gg::kTileM,
-                                               plan->total_tiles, plan->grid, a.n_xcd);
+                                               plan->total_tiles, plan->grid, a.n_xcd, a.band);
         const double short_ = busiest_workgroup(group_m, plan->group_num, a.n_tiles, rows,
-                                                plan->total_tiles, plan->grid, a.n_xcd);
+                                                plan->total_tiles, plan->grid, a.n_xcd, a.band);
         if (short_ > 0.97 * wide)
             return GG_OK;
     }
@@ -304,9 +304,9 @@ int use_short_wide_tiles(gg_plan *plan, const int64_t *group_m, const hipDeviceP
         return GG_OK;
     if (opt != 1) {
         const double short_ = busiest_workgroup(group_m, plan->group_num, a.n_tiles, a.tile_m, plan->total_tiles,
-                                                plan->grid, a.n_xcd);
+                                                plan->grid, a.n_xcd, a.band);
         const double wide   = kWideTileCost * busiest_workgroup(group_m, plan->group_num, n_tiles, a.tile_m,
-                                                                w.total_tiles, grid, n_xcd);
+                                                                w.total_tiles, grid, n_xcd, a.band);
         if (wide > 0.95 * short_)
             return GG_OK;
     }
@@ -693,6 +693,7 @@ int plan_device_lens(gg_plan *plan, bool noalloc, int op, int a_dtype, int b_dty
                        (op == GG_OP_WGRAD ? std::to_string(plan->total_tiles) : std::string("device")) +
                        " xcd=" + std::to_string(ka.n_xcd) +
                        (gg::uses_cross_tile(ka, plan->grid, plan->mode) ? " cross-tile" : " per-tile") +
+                       (ka.band != gg::kBand ? " band=" + std::to_string(ka.band) : "") +
                        (plan->in_kernel_table ? " (device group sizes, in-kernel table)" : " (device group sizes)");
     return GG_OK;
 }
@@ -846,6 +847,7 @@ int gg_prepare(int dtype, int group_num, int64_t n, int64_t k, const int64_t *gr
                        " tiles=" + std::to_string(plan->total_tiles) +
                        " xcd=" + std::to_string(a.n_xcd) +
                        (gg::uses_cross_tile(a, plan->grid) ? " cross-tile" : " per-tile") +
+                       (a.band != gg::kBand ? " band=" + std::to_string(a.band) : "") +
                        (a.splits > 1 ? " split-k=" + std::to_string(a.splits) : "") +
                        (a.tail_splits > 1 ? " tail-split=" + std::to_string(a.tail_splits) : "");
     } else {
@@ -1020,6 +1022,7 @@ static int prepare_backward(int layout, int dtype_a, int dtype_b, int group_num,
                        " grid=" + std::to_string(plan->grid) + " tiles=" + std::to_string(plan->total_tiles) +
                        " xcd=" + std::to_string(ka.n_xcd) +
                        (gg::uses_cross_tile(ka, plan->grid, plan->mode) ? " cross-tile" : " per-tile") +
+                       (ka.band != gg::kBand ? " band=" + std::to_string(ka.band) : "") +
                        (ka.splits > 1 ? " split-k=" + std::to_string(ka.splits) : "") +
                        (ka.tail_splits > 1 ? " tail-split=" + std::to_string(ka.tail_splits) : "");
     } else {
@@ -1124,6 +1127,7 @@ int gg_prepare_fp8(int dtype, int group_num, int64_t n, int64_t k, const int64_t
                        " persistent 256x256x128 bf16-out grid=" + std::to_string(plan->grid) +
                        " tiles=" + std::to_string(plan->total_tiles) + " xcd=" + std::to_string(a.n_xcd) +
                        (gg::uses_cross_tile(a, plan->grid, plan->mode) ? " cross-tile" : " per-tile") +
+                       (a.band != gg::kBand ? " band=" + std::to_string(a.band) : "") +
                        (a.splits > 1 ? " split-k=" + std::to_string(a.splits) : "") +
                        (a.tail_splits > 1 ? " tail-split=" + std::to_string(a.tail_splits) : "");
     } else {

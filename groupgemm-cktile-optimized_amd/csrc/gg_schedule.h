@@ -34,6 +34,8 @@ constexpr int kTileM = 256; // output rows per tile (tokens)
 constexpr int kTileN = 256; // output columns per tile (w rows)
 constexpr int kTileK = 64;  // K per main-loop step: one 128-byte cache line per operand row
 constexpr int kBand  = 4;   // M-tiles per band of the in-group order
+constexpr int kBandWide = 8; // M-tiles per band when a group's B operand outgrows the Infinity Cache
+constexpr int64_t kInfinityCacheBytes = int64_t(256) << 20; // MI355X: 256 MB, shared by the 8 XCDs
 constexpr int kNarrowTileN = 224; // output columns of a narrow tile (one-round forward problems)
 constexpr int kShortTileM  = 192; // most output rows of a short tile (6 row blocks per wave)
 constexpr int kShortWideTileN = 288; // output columns of a short-wide tile (9 column blocks per wave)
@@ -66,6 +68,16 @@ GG_HD void band_coords(int local, int m_tiles, int n_tiles, int band, int *tm, i
     const int h        = left < band ? left : band; // height of this (possibly last) band
     *tn                = p / h;
     *tm                = b * band + (p - (p / h) * h);
+}
+
+// M-tiles per band for a plan whose every group multiplies by a B operand (the w rows of the
+// output columns) of n x k elements of elt bytes; k = 0 where the contraction varies by group.
+// With 4-tile bands one round of 256 tiles covers 4 M-tiles by 64 N-tiles: when a group's B is
+// larger than the Infinity Cache, each round reads its 64 w panels from HBM and the next band
+// reads them again. 8-tile bands (8 x 4 tiles per XCD: the same 12 panels per XCD and round)
+// read 32 w panels per round and half the w bytes per launch.
+GG_HD int band_for(int64_t n, int64_t k, int elt) {
+    return n * k * elt > kInfinityCacheBytes ? kBandWide : kBand;
 }
 
 // Partial tiles: the row blocks (bit mi) of wave (wm, wn) of the 2 x 2 wave grid that hold a

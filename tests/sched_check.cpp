@@ -10,6 +10,7 @@
 //   * active_rows: for every tile size (1..256 valid rows and columns, both row mappings) each
 //     16 x 16 block that holds a valid output belongs to exactly one wave's active row blocks,
 //     and every active block holds a valid row (no MFMA skipped that a stored output needs);
+//   * band_for: 8-tile bands exactly where one group's B operand passes the Infinity Cache;
 //   * desc_rows_fit: tile descriptors (32-bit first rows) are refused when a wgrad plan's input
 //     tokens pass 2^31 although its output rows (group_num * N) are few, and accepted when every
 //     group's first token from build_group_table fits.
@@ -95,7 +96,7 @@ static void check_band(int m_tiles, int n_tiles, int band) {
 // out_rows x n output.
 // tile_m: rows per M-tile (short tiles: fewer than 256).
 static void check_walk(const std::vector<int64_t> &group_m, int64_t n, int grid, int n_xcd,
-                       int64_t out_rows = 0, int tile_m = gg::kTileM) {
+                       int64_t out_rows = 0, int tile_m = gg::kTileM, int band = gg::kBand) {
     const int64_t n_tiles = gg::cdiv(n, gg::kTileN);
     std::vector<gg::GroupEntry> table(group_m.size());
     const int64_t total = gg::build_group_table(group_m.data(), (int)group_m.size(), n_tiles,
@@ -109,7 +110,7 @@ static void check_walk(const std::vector<int64_t> &group_m, int64_t n, int grid,
             CHECK(L > prevL, "logical tiles of workgroup %d not increasing", wg);
             prevL = L;
             int tm, tn;
-            gg::locate_tile(L, table.data(), (int)group_m.size(), (int)n_tiles, gg::kBand, &g, &tm,
+            gg::locate_tile(L, table.data(), (int)group_m.size(), (int)n_tiles, band, &g, &tm,
                             &tn, (int)out_rows, tile_m);
             const int64_t rows = out_rows > 0 ? out_rows : group_m[g];
             CHECK(rows > 0, "tile assigned to empty group %d", g);
@@ -228,6 +229,16 @@ int main() {
                 check_band(m, nt, band);
     check_band(16, 16, 4);
     check_band(16, 28, 4);
+    check_band(64, 128, gg::kBandWide);
+    check_band(20, 112, gg::kBandWide);
+    // band_for: 8-tile bands only where one group's B operand is larger than the Infinity Cache
+    CHECK(gg::band_for(32768, 8192, 2) == gg::kBandWide, "w of 512 MB keeps 4-tile bands");
+    CHECK(gg::band_for(32768, 6144, 2) == gg::kBandWide, "w of 384 MB keeps 4-tile bands");
+    CHECK(gg::band_for(8192, 16384, 2) == gg::kBand, "w of exactly 256 MB takes 8-tile bands");
+    CHECK(gg::band_for(28672, 4096, 2) == gg::kBand, "w of 224 MB takes 8-tile bands");
+    CHECK(gg::band_for(32768, 8192, 1) == gg::kBand, "fp8 w of 256 MB takes 8-tile bands");
+    CHECK(gg::band_for(32768, 0, 2) == gg::kBand, "per-group contraction takes 8-tile bands");
+    CHECK(gg::band_for(int64_t(1) << 21, int64_t(1) << 21, 2) == gg::kBandWide, "largest shape");
     // the BASELINE configs and ragged / empty groups
     check_walk(std::vector<int64_t>(4, 256), 512, 8, 8);
     check_walk(std::vector<int64_t>(8, 4096), 4096, 256, 8);
@@ -242,6 +253,11 @@ int main() {
     check_walk({0, 300, 0, 0, 1, 2000, 0}, 1000, 24, 8, 776);
     check_walk({0, 0, 0}, 64, 3, 1, 64);
     check_walk({520, 0, 520}, 2880, 256, 8, 2880);
+    // 8-tile bands: single GEMMs whose w outgrows the Infinity Cache, and ragged groups
+    check_walk({4096}, 32768, 256, 8, 0, gg::kTileM, gg::kBandWide);
+    check_walk({16384}, 32768, 256, 8, 0, gg::kTileM, gg::kBandWide);
+    check_walk({0, 300, 0, 0, 1, 2000, 0}, 1000, 24, 8, 0, gg::kTileM, gg::kBandWide);
+    check_walk({257, 0, 255, 4096, 3}, 264, 256, 8, 0, gg::kTileM, gg::kBandWide);
     if (failures) {
         std::printf("%d failures\n", failures);
         return 1;
