@@ -486,7 +486,7 @@ BACKENDS = {"mi355x": make_mi355x_backend}
 
 # Sources that decide which kernel runs and what it does: a profile measured on one build is
 # matched to the current one by their hash (kernel_source_sha).
-KERNEL_SOURCES = ("csrc/gg_kernel_impl.h", "csrc/gg_schedule.h", "csrc/gg_kernel.h", "csrc/gg_inst.hip",
+KERNEL_SOURCES = ("csrc/gg_kernel_impl.h", "csrc/gg_schedule.h", "csrc/gg_kernel.h", "csrc/gg_inst.hip", "csrc/gg_small.hip",
                   "csrc/gg_kernel.hip", "csrc/gg_capi.hip")
 
 

@@ -42,6 +42,10 @@ struct gg_plan {
     float              *d_ws        = nullptr; // split-K / tail-split partial sums (args.ws)
     gg::TileDesc       *d_desc      = nullptr; // tile descriptors (args.desc)
     int64_t             in_rows     = 0;       // device-size plans: rows of the inputs
+    // Small-tile plans (use_small_tiles): the launch of gg_small.hip instead of the persistent one.
+    bool                small       = false;
+    gg::SmallArgs       sargs{};
+    gg::SmallTile      *d_small     = nullptr; // [sargs.tiles]
 };
 
 namespace {
@@ -386,7 +390,101 @@ int setup_tail_split(gg_plan *plan) {
     return GG_OK;
 }
 
+// Small tiles (128 x 128, one per workgroup, gg_small.hip) for 16-bit forward plans of host-size
+// groups whose 256 x 256 tiles fill at most half the CUs (one round of the per-tile variant).
+// The small-tile kernel runs its K steps at about half the MFMA rate of the persistent kernel
+// (twice the LDS reads per MFMA) but brings about four times the workgroups. Taken when its
+// tiles fit one round (unsplit unless GG_SMALL_SPLIT says otherwise) and a launch-time model (microseconds, MI355X) predicts
+// at most kSmallGain of the persistent plan's time: kSmallFixedUs + K steps * kSmallStepUs
+// against kSmallFixedUs + the split-K model of choose_splits for the plan's own splits.
+// Measured (gg_bench, bf16, forced against off): the suite's TestIDs 109, 112, 122, 157, 160,
+// 170 and 194 1.12-1.34x faster, pad_test's 9002 1.40x and 9004 1.10x; slower where the
+// persistent plan splits a long K (146, 266, 268, 278: 0.63-0.75x, which the model keeps off)
+// and where the small tiles need two rounds (0.45-0.81x).
+// For forced plans (GG_SMALL=1) the K ranges fill up to one workgroup per CU (128 KB of LDS
+// each) with at least kMinSmallSteps K steps per range; they write fp32 partial sums (64 KB per
+// tile and range) that a second launch adds in range order. GG_SMALL=0 in the environment turns
+// small tiles off; GG_SMALL_SPLIT=<S> forces the ranges.
+constexpr int    kMinSmallSteps = 8;
+constexpr double kSmallFixedUs  = 4.0;  // launch, first DMAs, epilogue
+constexpr double kSmallStepUs   = 0.62; // one K step of a 128 x 128 tile, one round
+constexpr double kSmallGain     = 0.85;
+
+int use_small_tiles(gg_plan *plan, const int64_t *group_m, const hipDeviceProp_t &prop, hipStream_t s) {
+    const char *env = std::getenv("GG_SMALL");
+    const int   opt = env != nullptr && *env != '\0' ? std::atoi(env) : -1;
+    const int   cus = prop.multiProcessorCount;
+    const gg::KernelArgs &a = plan->args;
+    if (opt == 0 || plan->group_num > 32767 || (opt != 1 && (2 * plan->total_tiles > cus || a.tail_splits > 1)))
+        return GG_OK;
+    const int64_t              nt = gg::cdiv(plan->n, gg::kSmallTile);
+    std::vector<gg::SmallTile> list;
+    int64_t                    row = 0;
+    for (int g = 0; g < plan->group_num; ++g) {
+        const int64_t mt = gg::cdiv(group_m[g], gg::kSmallTile);
+        for (int64_t tn = 0; tn < nt; ++tn)
+            for (int64_t tm = 0; tm < mt; ++tm)
+                list.push_back({row + tm * gg::kSmallTile,
+                                static_cast<int32_t>(std::min<int64_t>(gg::kSmallTile, group_m[g] - tm * gg::kSmallTile)),
+                                static_cast<int16_t>(g), static_cast<int16_t>(tn)});
+        row += group_m[g];
+    }
+    const int64_t tiles   = static_cast<int64_t>(list.size());
+    const int     k_steps = static_cast<int>(gg::cdiv(plan->k, gg::kSmallK));
+    if (tiles == 0 || tiles > 65536)
+        return GG_OK;
+    int sp = 1;
+    if (opt == 1 && tiles < cus) // forced: fill the CUs with K ranges
+        sp = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(cus / tiles, k_steps / kMinSmallSteps)));
+    if (const char *e2 = std::getenv("GG_SMALL_SPLIT"); e2 != nullptr && std::atoi(e2) >= 1)
+        sp = std::min(std::atoi(e2), k_steps);
+    const int per = static_cast<int>(gg::cdiv(k_steps, sp));
+    sp            = static_cast<int>(gg::cdiv(k_steps, per)); // no empty K range
+    if (opt != 1) {
+        const double big   = kSmallFixedUs + gg::cdiv(a.k_tiles, a.splits) * kStepUs +
+                           (a.splits > 1 ? kSplitUs + double(a.splits) * plan->total_tiles * kSlabUs : 0.0);
+        const double small = kSmallFixedUs + double(per) * kSmallStepUs;
+        if (tiles * sp > cus || small > kSmallGain * big)
+            return GG_OK;
+    }
+    // the persistent plan's workspace and descriptors are not used by this launch
+    if (plan->d_ws != nullptr)
+        (void)hipFree(plan->d_ws);
+    if (plan->d_desc != nullptr)
+        (void)hipFree(plan->d_desc);
+    plan->d_ws   = nullptr;
+    plan->d_desc = nullptr;
+    const size_t bytes = list.size() * sizeof(gg::SmallTile);
+    hipError_t   e     = hipMalloc(&plan->d_small, bytes);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(plan->d_small, list.data(), bytes, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess)
+        e = hipStreamSynchronize(s);
+    if (e == hipSuccess && sp > 1)
+        e = hipMalloc(&plan->d_ws, size_t(sp) * size_t(tiles) * gg::kSmallTile * gg::kSmallTile * sizeof(float));
+    if (e != hipSuccess)
+        return hip_fail(e, "small-tile plan");
+    gg::SmallArgs &sa    = plan->sargs;
+    sa.x                 = plan->x;
+    sa.w                 = plan->w;
+    sa.out               = plan->out;
+    sa.tile_list         = plan->d_small;
+    sa.ws                = plan->d_ws;
+    sa.tiles             = static_cast<int>(tiles);
+    sa.n                 = static_cast<int>(plan->n);
+    sa.k                 = static_cast<int>(plan->k);
+    sa.k_steps           = k_steps;
+    sa.splits            = sp;
+    sa.steps_per_split   = per;
+    plan->small          = true;
+    plan->total_tiles    = static_cast<int>(tiles);
+    plan->grid           = static_cast<int>(tiles) * sp;
+    return GG_OK;
+}
+
 void free_plan(gg_plan *plan) {
+    if (plan->d_small != nullptr)
+        (void)hipFree(plan->d_small);
     if (plan->d_groups != nullptr)
         (void)hipFree(plan->d_groups);
     if (plan->d_ws != nullptr)
@@ -728,6 +826,10 @@ int run_plan(const gg_plan *plan, void *stream, bool zero_kernel) {
         }
         return GG_OK;
     }
+    if (plan->small) {
+        const hipError_t e = gg::launch_small_gemm(plan->sargs, plan->dtype == GG_DTYPE_FP16, s);
+        return e == hipSuccess ? GG_OK : hip_fail(e, "small-tile GEMM launch");
+    }
     hipError_t e = gg::launch_grouped_gemm(plan->args, plan->dtype == GG_DTYPE_FP16, plan->grid, s, plan->mode);
     if (e != hipSuccess)
         return hip_fail(e, "grouped GEMM launch");
@@ -841,15 +943,23 @@ int gg_prepare(int dtype, int group_num, int64_t n, int64_t k, const int64_t *gr
             free_plan(plan);
             return st3;
         }
-        plan->detail      = "mi355x persistent " + std::to_string(a.tile_m) + "x" + std::to_string(a.tile_n) + "x64 " +
-                       std::string(dtype == GG_DTYPE_BF16 ? "bf16" : "fp16") +
-                       " grid=" + std::to_string(plan->grid) +
-                       " tiles=" + std::to_string(plan->total_tiles) +
-                       " xcd=" + std::to_string(a.n_xcd) +
-                       (gg::uses_cross_tile(a, plan->grid) ? " cross-tile" : " per-tile") +
-                       (a.band != gg::kBand ? " band=" + std::to_string(a.band) : "") +
-                       (a.splits > 1 ? " split-k=" + std::to_string(a.splits) : "") +
-                       (a.tail_splits > 1 ? " tail-split=" + std::to_string(a.tail_splits) : "");
+        if (const int st4 = use_small_tiles(plan, group_m, prop, s); st4 != GG_OK) {
+            free_plan(plan);
+            return st4;
+        }
+        const std::string dt = dtype == GG_DTYPE_BF16 ? "bf16" : "fp16";
+        if (plan->small)
+            plan->detail = "mi355x small 128x128x64 " + dt + " grid=" + std::to_string(plan->grid) +
+                           " tiles=" + std::to_string(plan->total_tiles) +
+                           (plan->sargs.splits > 1 ? " split-k=" + std::to_string(plan->sargs.splits) : "");
+        else
+            plan->detail = "mi355x persistent " + std::to_string(a.tile_m) + "x" + std::to_string(a.tile_n) +
+                           "x64 " + dt + " grid=" + std::to_string(plan->grid) +
+                           " tiles=" + std::to_string(plan->total_tiles) + " xcd=" + std::to_string(a.n_xcd) +
+                           (gg::uses_cross_tile(a, plan->grid) ? " cross-tile" : " per-tile") +
+                           (a.band != gg::kBand ? " band=" + std::to_string(a.band) : "") +
+                           (a.splits > 1 ? " split-k=" + std::to_string(a.splits) : "") +
+                           (a.tail_splits > 1 ? " tail-split=" + std::to_string(a.tail_splits) : "");
     } else {
         plan->detail = "mi355x: no launch (" +
                        std::string(has_output ? "K = 0, zero fill" : "empty output") + ")";

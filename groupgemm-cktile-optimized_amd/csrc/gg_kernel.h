@@ -158,6 +158,33 @@ hipError_t launch_group_offsets(const int64_t *lens, int64_t *offs, int group_nu
 // capture it in a graph, where a hipMemsetAsync node must not be recorded.
 hipError_t launch_zero_fill(void *out, size_t bytes, hipStream_t stream);
 
+// Small-tile forward plans (16-bit, host-size groups) for problems whose 256 x 256 tiles leave
+// most CUs idle: 128 x 128 tiles, one per workgroup, optionally split over K.
+constexpr int kSmallTile = 128; // output rows and columns of a small tile
+constexpr int kSmallK    = 64;  // K per step
+constexpr int kSmallStages = 4; // LDS ring of K steps (32 KB each): DMAs run 3 steps ahead
+struct SmallTile {
+    int64_t row0; // first row of the tile in x and out
+    int32_t m;    // valid rows (1 .. 128)
+    int16_t g;    // group (the small-tile plans take at most 32767 groups)
+    int16_t tn;   // N-tile (128 columns; N <= 2^21 gives at most 16384)
+};
+struct SmallArgs {
+    const void      *x;     // [sum(M), K]
+    const void      *w;     // [B, N, K]
+    void            *out;   // [sum(M), N]
+    const SmallTile *tile_list; // [tiles], device memory
+    float           *ws;    // split-K: splits * tiles slabs of 128 x 128 fp32 (64 KB)
+    int              tiles;
+    int              n, k;
+    int              k_steps;         // ceil(K / 64)
+    int              splits;          // K ranges per tile (1 = none)
+    int              steps_per_split; // K steps per range (the last range may have fewer)
+};
+// Enqueue a small-tile plan: tiles * splits workgroups of 256 threads, then (splits > 1) the
+// reduction of the partial sums, one workgroup per tile, on the same stream.
+hipError_t launch_small_gemm(const SmallArgs &args, bool fp16, hipStream_t stream);
+
 // Seeded N(0,1) fill (benchmark input generator).
 hipError_t launch_fill_randn(void *p, size_t count, uint64_t seed, bool fp16, hipStream_t stream);
 hipError_t launch_clock_probe(unsigned long long *out, unsigned long long ticks, unsigned long long wall_hz,

@@ -14,6 +14,15 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (runs the native HIP path)")
 
 
+@pytest.fixture(autouse=True)
+def _persistent_plans_by_default(monkeypatch):
+    """Tests of the persistent kernel's plans (per-tile, split-K, narrow and short tiles) keep their
+    shapes on that kernel: small-tile plans are off unless a test turns them on
+    (tests/test_gpu_small_tiles.py forces them and checks the planner's own choice; the
+    random-shape tests let the planner choose)."""
+    monkeypatch.setenv("GG_SMALL", "0")
+
+
 @pytest.fixture(scope="session")
 def pkg():
     return entry.load_package()

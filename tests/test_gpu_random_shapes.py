@@ -3,7 +3,7 @@
 Each case draws B groups of ragged sizes (some empty), N and K multiples of 8 up to 3200, bf16 or
 fp16, and one of the forward, dgrad and wgrad passes, with the group sizes on the host or on the
 device. The planner picks whatever it picks for the shape (cross-tile or per-tile, split-K, tail
-split, short, short-wide or narrow tiles, descriptors or the table walk, masks or none), so the
+split, short, short-wide, narrow or small tiles, descriptors or the table walk, masks or none), so the
 sweep covers the plan boundaries that hand-picked shapes may miss. Every output is checked at
 |got - ref| <= 1e-2 + 1e-2 * |ref| (bench/bench_main.cpp:264-268); the host-size forward
 output is NaN-prefilled, so an unwritten tile fails.
@@ -56,7 +56,8 @@ def _check(got, ref, what):
 
 
 @pytest.mark.parametrize("case", CASES, ids=[f"{c[0]}-{c[1]}" for c in CASES])
-def test_random_shape(pkg, case):
+def test_random_shape(pkg, monkeypatch, case):
+    monkeypatch.delenv("GG_SMALL", raising=False)  # the planner's own choice, small tiles included
     i, op, dt, b, n, k, ms, device_sizes = case
     print(f"[random] case {i}: {op} {'fp16' if dt else 'bf16'} B={b} N={n} K={k} rows={sum(ms)} "
           f"device_sizes={device_sizes}", flush=True)
