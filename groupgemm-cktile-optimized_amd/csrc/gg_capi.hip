@@ -394,13 +394,14 @@ int setup_tail_split(gg_plan *plan) {
 // groups whose 256 x 256 tiles fill at most half the CUs (one round of the per-tile variant).
 // The small-tile kernel runs its K steps at about half the MFMA rate of the persistent kernel
 // (twice the LDS reads per MFMA) but brings about four times the workgroups. Taken when its
-// tiles fit one round (unsplit unless GG_SMALL_SPLIT says otherwise) and a launch-time model (microseconds, MI355X) predicts
-// at most kSmallGain of the persistent plan's time: kSmallFixedUs + K steps * kSmallStepUs
-// against kSmallFixedUs + the split-K model of choose_splits for the plan's own splits.
-// Measured (gg_bench, bf16, forced against off): the suite's TestIDs 109, 112, 122, 157, 160,
-// 170 and 194 1.12-1.34x faster, pad_test's 9002 1.40x and 9004 1.10x; slower where the
-// persistent plan splits a long K (146, 266, 268, 278: 0.63-0.75x, which the model keeps off)
-// and where the small tiles need two rounds (0.45-0.81x).
+// tiles fit one round (unsplit unless GG_SMALL_SPLIT says otherwise) and a launch-time model
+// (microseconds, MI355X) predicts at most kSmallGain of the persistent plan's time:
+// kSmallFixedUs + K steps * kSmallStepUs against kSmallFixedUs + the split-K model of
+// choose_splits for the plan's own splits. It takes (gg_bench, bf16, against GG_SMALL=0) the
+// suite's TestIDs 109, 110, 112, 122, 157, 160, 170 and 194 (1.23-1.49x faster), pad_test's
+// 9002 and 9004 and config 1; it leaves out those where the persistent plan splits a long K
+// (146, 266, 268, 278: small tiles 0.63-0.78x) and where the small tiles need two rounds
+// (0.6-0.85x).
 // For forced plans (GG_SMALL=1) the K ranges fill up to one workgroup per CU (128 KB of LDS
 // each) with at least kMinSmallSteps K steps per range; they write fp32 partial sums (64 KB per
 // tile and range) that a second launch adds in range order. GG_SMALL=0 in the environment turns
@@ -433,6 +434,17 @@ int use_small_tiles(gg_plan *plan, const int64_t *group_m, const hipDeviceProp_t
     const int     k_steps = static_cast<int>(gg::cdiv(plan->k, gg::kSmallK));
     if (tiles == 0 || tiles > 65536)
         return GG_OK;
+    // Workgroup i runs on XCD i % n_xcd: deal the list (N-tile by N-tile, M-tiles inside) to the
+    // XCDs in contiguous runs (xcd_remap), so that the workgroups of one XCD share a few x and w
+    // panels in its L2 instead of every XCD reading every w panel.
+    // (A grid of whole XCD rows: XCD y takes ceil((tiles - y) / n_xcd) of the list.)
+    if (const int n_xcd = xcd_count(prop); n_xcd > 1) {
+        const int                  rows = static_cast<int>(gg::cdiv(tiles, n_xcd)) * n_xcd;
+        std::vector<gg::SmallTile> dealt(list.size());
+        for (int t = 0; t < static_cast<int>(tiles); ++t)
+            dealt[static_cast<size_t>(t)] = list[static_cast<size_t>(gg::xcd_remap(t, static_cast<int>(tiles), rows, n_xcd))];
+        list.swap(dealt);
+    }
     int sp = 1;
     if (opt == 1 && tiles < cus) // forced: fill the CUs with K ranges
         sp = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(cus / tiles, k_steps / kMinSmallSteps)));

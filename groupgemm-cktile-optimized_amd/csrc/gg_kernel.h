@@ -181,8 +181,8 @@ struct SmallArgs {
     int              splits;          // K ranges per tile (1 = none)
     int              steps_per_split; // K steps per range (the last range may have fewer)
 };
-// Enqueue a small-tile plan: tiles * splits workgroups of 256 threads, then (splits > 1) the
-// reduction of the partial sums, one workgroup per tile, on the same stream.
+// Enqueue a small-tile plan: tiles * splits workgroups of 512 threads, then (splits > 1) the
+// reduction of the partial sums, one workgroup of 256 threads per tile, on the same stream.
 hipError_t launch_small_gemm(const SmallArgs &args, bool fp16, hipStream_t stream);
 
 // Seeded N(0,1) fill (benchmark input generator).

@@ -1,13 +1,15 @@
 // Small-tile forward kernel (16-bit inputs and output, out[g] = x[g] @ w[g]^T, RCR) for problems
 // whose 256 x 256 tiles cannot fill the GPU: one 128 x 128 output tile, or one K range of it
-// (split-K), per workgroup of 256 threads, one workgroup per CU (128 KB of LDS).
+// (split-K), per workgroup of 512 threads, one workgroup per CU (128 KB of LDS).
 //
 // Operands go from global memory to LDS by DMA (buffer_load ... lds, 16 bytes per lane) into a
 // ring of 4 K steps of 64, issued 3 steps ahead. Rows are 128 bytes in LDS, their 16-byte pieces
 // stored at (piece ^ (row % 8)) so that 8 lanes reading 8 consecutive rows hit 8 different bank
-// groups. The 4 waves (2 x 2) each compute 64 x 64 of the tile with v_mfma_f32_16x16x32 (bf16 or
-// f16): w rows are the first source and x rows the second, so a lane's 4 accumulators are 4
-// consecutive output columns of one row (one 8-byte store).
+// groups. Eight waves, two per SIMD: waves 0-3 multiply the first 32 K of every step and waves
+// 4-7 the second, each for a 64 x 64 quarter of the tile, with v_mfma_f32_16x16x32 (bf16 or
+// f16); while one wave of a SIMD waits on its LDS reads the other issues MFMAs. w rows are the
+// first source and x rows the second, so a lane's 4 accumulators are 4 consecutive output
+// columns of one row (one 8-byte store). The two K halves are added through LDS at the end.
 //
 // Bounds: the x and w resources end at the tile's last valid row (loads past it return 0); a
 // row piece past K (K % 64 != 0), which would read the next row, is loaded from an offset past
@@ -95,12 +97,13 @@ __device__ __forceinline__ si32x4 raw_rsrc(const void *p, int bytes) {
 }
 
 template <bool F16, bool SPLIT>
-__global__ void __launch_bounds__(256, 1) small_gemm_kernel(const SmallArgs a) {
+__global__ void __launch_bounds__(512, 1) small_gemm_kernel(const SmallArgs a) {
     constexpr int S = kSmallStages;
     __shared__ __attribute__((aligned(1024))) unsigned char lds[S][2][kStage]; // [stage][x, w]
     // wave is uniform: readfirstlane keeps it (and the DMAs' LDS addresses) in SGPRs
     const int tid = static_cast<int>(threadIdx.x), lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
+    const int kh = wave >> 2, wq = wave & 3; // K half of every step, quarter of the tile
+    const int wm = wq >> 1, wn = wq & 1;
     const int tile  = static_cast<int>(blockIdx.x) % a.tiles;
     const int split = static_cast<int>(blockIdx.x) / a.tiles;
     const SmallTile t = a.tile_list[tile];
@@ -117,17 +120,17 @@ __global__ void __launch_bounds__(256, 1) small_gemm_kernel(const SmallArgs a) {
 
     // DMA d (0..15) of an operand fills rows 8 d .. 8 d + 7 (1 KB): lane l takes row 8 d + l / 8
     // and the K piece (l % 8) ^ (l / 8), which lands at piece position l % 8 of that row. Wave w
-    // issues DMAs 4 w .. 4 w + 3 of each operand. A piece past K (K % 64 != 0), which would
+    // issues DMAs 2 w and 2 w + 1 of each operand. A piece past K (K % 64 != 0), which would
     // read the next row, takes an offset past both resources (at most 128 * 2^21 * 2 = 2^29
     // bytes), so the DMA writes zeros.
     const int      drow = lane >> 3, dpiece = (lane & 7) ^ drow;
-    const int      dbase = (wave * 32 + drow) * K * 2 + dpiece * 16;
+    const int      dbase = (wave * 16 + drow) * K * 2 + dpiece * 16;
     const uint32_t lds0  = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(&lds[0][0][0]));
     auto issue = [&](int s) {
-        const uint32_t st  = lds0 + static_cast<uint32_t>(s % S) * (2 * kStage) + wave * 4096;
+        const uint32_t st  = lds0 + static_cast<uint32_t>(s % S) * (2 * kStage) + wave * 2048;
         const int      oob = ((K - 1 - s * kSmallK - dpiece * 8) >> 31) & 0x40000000;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < 2; ++j) {
             const int off = (dbase + j * 8 * K * 2 + s * 128) | oob;
             dma16(st + j * 1024, off, xr);
             dma16(st + kStage + j * 1024, off, wr);
@@ -141,47 +144,65 @@ __global__ void __launch_bounds__(256, 1) small_gemm_kernel(const SmallArgs a) {
         for (int j = 0; j < 4; ++j)
             acc[i][j] = sf32x4{0.f, 0.f, 0.f, 0.f};
 
-    // Fragment reads: row (wm or wn) * 64 + 16 i + lane % 16, piece 4 h + lane / 16.
+    // Eight waves, two per SIMD: waves 0-3 take the first 32 K of every step and waves 4-7 the
+    // second, each for its quarter (wm, wn) of the tile; the two halves are added at the end.
+    // Fragment reads: row (wm or wn) * 64 + 16 i + lane % 16, piece 4 kh + lane / 16.
     // The ring: step s in stage s % S, its DMAs issued S - 1 steps ahead, right after the barrier
     // that ends every wave's reads of the stage they overwrite (step s - 1's).
     const int frow = lane & 15, fpiece = lane >> 4;
+    const int p    = ((4 * kh + fpiece) ^ (frow & 7)) << 4;
     for (int s = s0; s < min(s1, s0 + S - 1); ++s)
         issue(s);
     for (int s = s0; s < s1; ++s) {
-        if (s + S - 2 < s1) // the DMAs of steps s + 1 .. s + S - 2 (8 per step and wave) may run on
-            wait_vm_barrier<(S - 2) * 8>();
+        if (s + S - 2 < s1) // the DMAs of steps s + 1 .. s + S - 2 (4 per step and wave) may run on
+            wait_vm_barrier<(S - 2) * 4>();
         else
             wait_vm_barrier<0>();
         if (s + S - 1 < s1)
             issue(s + S - 1);
         const unsigned char *sa = &lds[s % S][0][0];
+        su32x4               fa[4], fb[4];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            su32x4 fa[4], fb[4];
-            const int p = ((4 * h + fpiece) ^ (frow & 7)) << 4;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                fa[i] = *reinterpret_cast<const su32x4 *>(sa + (wm * 64 + 16 * i + frow) * 128 + p);
-                fb[i] = *reinterpret_cast<const su32x4 *>(sa + kStage + (wn * 64 + 16 * i + frow) * 128 + p);
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    acc[i][j] = mma<F16>(fb[j], fa[i], acc[i][j]);
+        for (int i = 0; i < 4; ++i) {
+            fa[i] = *reinterpret_cast<const su32x4 *>(sa + (wm * 64 + 16 * i + frow) * 128 + p);
+            fb[i] = *reinterpret_cast<const su32x4 *>(sa + kStage + (wn * 64 + 16 * i + frow) * 128 + p);
         }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] = mma<F16>(fb[j], fa[i], acc[i][j]);
     }
 
     // 20 wait states between the last MFMA and the first read of its accumulators (gfx950 needs
     // up to 19 after a 16-pass MFMA; the build's hazard scan counts each MFMA issue as 4)
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" ::: "memory");
+    // The second K halves through LDS (the ring is free: every DMA has landed and been read):
+    // waves 4-7 write theirs, waves 0-3 add them to their own (first half + second half).
+    float *red = reinterpret_cast<float *>(&lds[0][0][0]);
+    __syncthreads();
+    if (kh == 1) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                *reinterpret_cast<sf32x4 *>(red + ((wq * 16 + i * 4 + j) * 64 + lane) * 4) = acc[i][j];
+    }
+    __syncthreads();
+    if (kh == 1)
+        return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            acc[i][j] += *reinterpret_cast<const sf32x4 *>(red + ((wq * 16 + i * 4 + j) * 64 + lane) * 4);
     if constexpr (SPLIT) {
         float *slab = a.ws + (static_cast<int64_t>(split) * a.tiles + tile) * (kSmallTile * kSmallTile);
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                *reinterpret_cast<sf32x4 *>(slab + ((wave * 16 + i * 4 + j) * 64 + lane) * 4) = acc[i][j];
+                *reinterpret_cast<sf32x4 *>(slab + ((wq * 16 + i * 4 + j) * 64 + lane) * 4) = acc[i][j];
     } else {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -214,7 +235,7 @@ template <bool F16> __global__ void __launch_bounds__(256) small_reduce_kernel(c
 } // namespace
 
 hipError_t launch_small_gemm(const SmallArgs &a, bool fp16, hipStream_t stream) {
-    const dim3 grid(static_cast<unsigned>(a.tiles * a.splits)), block(256);
+    const dim3 grid(static_cast<unsigned>(a.tiles * a.splits)), block(512), rblock(256);
     if (a.splits > 1) {
         if (fp16)
             small_gemm_kernel<true, true><<<grid, block, 0, stream>>>(a);
@@ -224,9 +245,9 @@ hipError_t launch_small_gemm(const SmallArgs &a, bool fp16, hipStream_t stream) 
         if (e != hipSuccess)
             return e;
         if (fp16)
-            small_reduce_kernel<true><<<dim3(a.tiles), block, 0, stream>>>(a);
+            small_reduce_kernel<true><<<dim3(a.tiles), rblock, 0, stream>>>(a);
         else
-            small_reduce_kernel<false><<<dim3(a.tiles), block, 0, stream>>>(a);
+            small_reduce_kernel<false><<<dim3(a.tiles), rblock, 0, stream>>>(a);
     } else if (fp16) {
         small_gemm_kernel<true, false><<<grid, block, 0, stream>>>(a);
     } else {

@@ -223,6 +223,9 @@ int main() {
                 check_remap(total, grid, n_xcd);
     check_remap(2048, 256, 8);
     check_remap(7168, 256, 8);
+    // small-tile plans deal their whole list as one partial round of whole XCD rows
+    for (int total = 1; total <= 3000; ++total)
+        check_remap(total, (total + 7) / 8 * 8, 8);
     for (int band = 1; band <= 5; ++band)
         for (int m = 1; m <= 18; ++m)
             for (int nt = 1; nt <= 30; nt += 3)
