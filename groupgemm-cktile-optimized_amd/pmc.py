@@ -105,8 +105,16 @@ def mean_after_first(ds, key):
     return sum(vals) / len(vals) if vals else None
 
 
+# The GEMM launch of a plan: the persistent kernel, or the small-tile kernel (gg_small.hip).
+GEMM_KERNEL = re.compile(r"(?:grouped_gemm_kernel|small_gemm_kernel)<[^>]*>")
+
+
+def is_gemm(name: str) -> bool:
+    return "grouped_gemm_kernel" in name or "small_gemm_kernel" in name
+
+
 def instance(name: str) -> str:
-    m = re.search(r"grouped_gemm_kernel<[^>]*>", name)
+    m = GEMM_KERNEL.search(name)
     return m.group(0) if m else name
 
 
@@ -133,9 +141,9 @@ def profile_workload(w: str, op: str, raw: str, limit: int, cal, commit: str, sh
     counters, plan, name, trace_ns = {}, None, None, None
     for p, names in PASSES.items():
         files, err = run_pass(f"{tag0}_{p}", ["--pmc"] + names + ["--kernel-trace"], bench_args, raw, limit)
-        ds = dispatches(files, lambda n: "grouped_gemm_kernel" in n)
+        ds = dispatches(files, is_gemm)
         if not ds:
-            raise RuntimeError(f"{tag0}_{p}: no grouped_gemm_kernel dispatch in the counters")
+            raise RuntimeError(f"{tag0}_{p}: no GEMM kernel dispatch in the counters")
         name = next(iter(ds.values()))["name"]
         for c in names:
             counters[c] = mean_after_first(ds, c)
@@ -145,7 +153,7 @@ def profile_workload(w: str, op: str, raw: str, limit: int, cal, commit: str, sh
     trace_args = ["--workload", w, "--op", op, "--steps", "20", "--warmup", "5", "--no-cpu-baseline",
                   "--power-seconds", "0", "--baselines", ""]
     files, _ = run_pass(f"{tag0}_trace", ["--kernel-trace"], trace_args, raw, limit)
-    ds = dispatches(files, lambda n: "grouped_gemm_kernel" in n)
+    ds = dispatches(files, is_gemm)
     ns = [d["ns"] for _, d in sorted(ds.items()) if d["ns"]]
     timed = ns[-20:] if len(ns) >= 25 else ns[1:] or ns
     trace_ns = sum(timed) / len(timed) if timed else None

@@ -39,15 +39,19 @@ def log(msg: str) -> None:
     print(f"[trace {time.strftime('%H:%M:%S')}] {msg}", flush=True)
 
 
+# The GEMM launch of a plan: the persistent kernel, or the small-tile kernel (gg_small.hip).
+GEMM_KERNEL = re.compile(r"(grouped_gemm_kernel|small_gemm_kernel)<([^>]*)>")
+
+
 def mangled_instance(name: str) -> str:
     """Itanium mangling of the kernel instance in a demangled name, for the resource report."""
-    m = re.search(r"grouped_gemm_kernel<([^>]*)>", name)
+    m = GEMM_KERNEL.search(name)
     if not m:
         return ""
     parts = []
-    for a in (x.strip() for x in m.group(1).split(",")):
+    for a in (x.strip() for x in m.group(2).split(",")):
         parts.append(("Lb1E" if a == "true" else "Lb0E") if a in ("true", "false") else f"Li{a}E")
-    return "grouped_gemm_kernelI" + "".join(parts) + "E"
+    return m.group(1) + "I" + "".join(parts) + "E"
 
 
 def resource_line(name: str) -> str:
@@ -106,7 +110,7 @@ def trace_workload(w: str, op: str, raw: str, profiles: str, limit: int, workloa
                 stats = list(csv.DictReader(f))
         elif base.endswith("_kernel_trace.csv"):
             with open(path) as f:
-                rows = [r for r in csv.DictReader(f) if "grouped_gemm_kernel" in r.get("Kernel_Name", "")]
+                rows = [r for r in csv.DictReader(f) if GEMM_KERNEL.search(r.get("Kernel_Name", ""))]
             rows.sort(key=lambda r: int(r["Start_Timestamp"]))
             launches = [int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in rows]
             name = rows[0]["Kernel_Name"] if rows else ""
@@ -117,7 +121,7 @@ def trace_workload(w: str, op: str, raw: str, profiles: str, limit: int, workloa
     timed = launches[-20:]
     mean_ns = sum(timed) / len(timed)
     plan = re.search(r"\[bench\] \S+ \S+: (.*)", p.stderr)
-    short = re.search(r"grouped_gemm_kernel<[^>]*>", name)
+    short = GEMM_KERNEL.search(name)
     short = short.group(0) if short else name
     lines = [
         f"# rocprofv3 kernel trace: `{short}`, {tag}",

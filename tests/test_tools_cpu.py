@@ -118,6 +118,11 @@ def test_mangled_instance_and_label():
     assert trace.kernel_label("gg::split_reduce_kernel<false, false>(float const*, int)") == \
         "gg::split_reduce_kernel<false, false>"
     assert trace.mangled_instance("gg::split_reduce_kernel<false, false>") == ""
+    small = "void gg::(anonymous namespace)::small_gemm_kernel<true, false>(gg::SmallArgs)"
+    assert trace.mangled_instance(small) == "small_gemm_kernelILb1ELb0EE"
+    assert trace.kernel_label(small) == "gg::small_gemm_kernel<true, false>"
+    assert pmc.instance(small) == "small_gemm_kernel<true, false>" and pmc.is_gemm(small)
+    assert not pmc.is_gemm("gg::(anonymous namespace)::small_reduce_kernel<true>(gg::SmallArgs)")
 
 
 def test_profiled_instances_are_in_the_resource_report():
