@@ -14,6 +14,7 @@ statement of what it reads:
 """
 import importlib.util
 import os
+import re
 
 import numpy as np
 import pytest
@@ -140,7 +141,7 @@ def test_profiled_instances_are_in_the_resource_report():
     assert names, "no kernel-trace summaries"
     for n in names:
         key = trace.mangled_instance(n)
-        assert key and f"_ZN2gg12_GLOBAL__N_119{key}EvNS_10KernelArgsE" in text, n
+        assert key and re.search(rf"_ZN2gg12_GLOBAL__N_1\d+{key}EvNS_\d+(KernelArgs|SmallArgs)E", text), n
         assert "not in the resource report" not in trace.resource_line(n), n
 
 
