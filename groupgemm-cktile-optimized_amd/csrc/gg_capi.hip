@@ -394,22 +394,24 @@ int setup_tail_split(gg_plan *plan) {
 // groups whose 256 x 256 tiles fill at most half the CUs (one round of the per-tile variant).
 // The small-tile kernel runs its K steps at about half the MFMA rate of the persistent kernel
 // (twice the LDS reads per MFMA) but brings about four times the workgroups. Taken when its
-// tiles fit one round (unsplit unless GG_SMALL_SPLIT says otherwise) and a launch-time model
+// tiles (unsplit unless GG_SMALL_SPLIT says otherwise) fit two per CU and a launch-time model
 // (microseconds, MI355X) predicts at most kSmallGain of the persistent plan's time:
-// kSmallFixedUs + K steps * kSmallStepUs against kSmallFixedUs + the split-K model of
-// choose_splits for the plan's own splits. It takes (gg_bench, bf16, against GG_SMALL=0) the
-// suite's TestIDs 109, 110, 112, 122, 157, 160, 170 and 194 (1.23-1.49x faster), pad_test's
-// 9002 and 9004 and config 1; it leaves out those where the persistent plan splits a long K
-// (146, 266, 268, 278: small tiles 0.63-0.78x) and where the small tiles need two rounds
-// (0.6-0.85x).
+// kSmallFixedUs + K steps * kSmallStepUs (one workgroup per CU, a 4-step ring) or
+// kSmallStepTwoUs (up to two, a 2-step ring) against kSmallFixedUs + the split-K model of
+// choose_splits for the plan's own splits. Against GG_SMALL=0 (gg_bench and ab runs, bf16): one
+// per CU, the suite's TestIDs 109, 110, 112, 122, 157, 160, 170 and 194 1.23-1.49x, pad_test's
+// 9002 and 9004 and config 1; two per CU, 1 x 2048 x 2880 x 2880 1.13x, 1 x 1024 x 5760 x 2880
+// 1.05x, 2 x 1024 x 2816 x 2048 1.03x. Left out: where the persistent plan splits a long K
+// (146, 266, 268, 278, 148: small tiles 0.63-0.78x) and more than two tiles per CU.
 // For forced plans (GG_SMALL=1) the K ranges fill up to one workgroup per CU (128 KB of LDS
 // each) with at least kMinSmallSteps K steps per range; they write fp32 partial sums (64 KB per
 // tile and range) that a second launch adds in range order. GG_SMALL=0 in the environment turns
 // small tiles off; GG_SMALL_SPLIT=<S> forces the ranges.
 constexpr int    kMinSmallSteps = 8;
 constexpr double kSmallFixedUs  = 4.0;  // launch, first DMAs, epilogue
-constexpr double kSmallStepUs   = 0.62; // one K step of a 128 x 128 tile, one round
-constexpr double kSmallGain     = 0.85;
+constexpr double kSmallStepUs    = 0.62; // one K step of a 128 x 128 tile, one workgroup per CU
+constexpr double kSmallStepTwoUs = 1.0;  // the same with up to two workgroups per CU
+constexpr double kSmallGain      = 0.85;
 
 int use_small_tiles(gg_plan *plan, const int64_t *group_m, const hipDeviceProp_t &prop, hipStream_t s) {
     const char *env = std::getenv("GG_SMALL");
@@ -452,11 +454,14 @@ int use_small_tiles(gg_plan *plan, const int64_t *group_m, const hipDeviceProp_t
         sp = std::min(std::atoi(e2), k_steps);
     const int per = static_cast<int>(gg::cdiv(k_steps, sp));
     sp            = static_cast<int>(gg::cdiv(k_steps, per)); // no empty K range
+    // a 4-step ring while every workgroup has a CU of its own, else a 2-step ring, two per CU
+    const int stages = tiles * sp <= cus ? gg::kSmallStagesOne : gg::kSmallStagesTwo;
     if (opt != 1) {
         const double big   = kSmallFixedUs + gg::cdiv(a.k_tiles, a.splits) * kStepUs +
                            (a.splits > 1 ? kSplitUs + double(a.splits) * plan->total_tiles * kSlabUs : 0.0);
-        const double small = kSmallFixedUs + double(per) * kSmallStepUs;
-        if (tiles * sp > cus || small > kSmallGain * big)
+        const double step  = stages == gg::kSmallStagesOne ? kSmallStepUs : kSmallStepTwoUs;
+        const double small = kSmallFixedUs + double(per) * step;
+        if (tiles * sp > 2 * int64_t(cus) || small > kSmallGain * big)
             return GG_OK;
     }
     // the persistent plan's workspace and descriptors are not used by this launch
@@ -488,6 +493,7 @@ int use_small_tiles(gg_plan *plan, const int64_t *group_m, const hipDeviceProp_t
     sa.k_steps           = k_steps;
     sa.splits            = sp;
     sa.steps_per_split   = per;
+    sa.stages            = stages;
     plan->small          = true;
     plan->total_tiles    = static_cast<int>(tiles);
     plan->grid           = static_cast<int>(tiles) * sp;
@@ -963,6 +969,7 @@ int gg_prepare(int dtype, int group_num, int64_t n, int64_t k, const int64_t *gr
         if (plan->small)
             plan->detail = "mi355x small 128x128x64 " + dt + " grid=" + std::to_string(plan->grid) +
                            " tiles=" + std::to_string(plan->total_tiles) +
+                           (plan->sargs.stages == gg::kSmallStagesTwo ? " two-per-cu" : "") +
                            (plan->sargs.splits > 1 ? " split-k=" + std::to_string(plan->sargs.splits) : "");
         else
             plan->detail = "mi355x persistent " + std::to_string(a.tile_m) + "x" + std::to_string(a.tile_n) +

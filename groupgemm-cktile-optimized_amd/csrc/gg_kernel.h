@@ -162,7 +162,10 @@ hipError_t launch_zero_fill(void *out, size_t bytes, hipStream_t stream);
 // most CUs idle: 128 x 128 tiles, one per workgroup, optionally split over K.
 constexpr int kSmallTile = 128; // output rows and columns of a small tile
 constexpr int kSmallK    = 64;  // K per step
-constexpr int kSmallStages = 4; // LDS ring of K steps (32 KB each): DMAs run 3 steps ahead
+// LDS ring of K steps (32 KB each), DMAs S - 1 steps ahead: 4 steps (128 KB, one workgroup per
+// CU) for plans of at most one tile per CU, 2 steps (64 KB, two workgroups per CU) for up to two.
+constexpr int kSmallStagesOne = 4;
+constexpr int kSmallStagesTwo = 2;
 struct SmallTile {
     int64_t row0; // first row of the tile in x and out
     int32_t m;    // valid rows (1 .. 128)
@@ -180,6 +183,7 @@ struct SmallArgs {
     int              k_steps;         // ceil(K / 64)
     int              splits;          // K ranges per tile (1 = none)
     int              steps_per_split; // K steps per range (the last range may have fewer)
+    int              stages;          // kSmallStagesOne or kSmallStagesTwo
 };
 // Enqueue a small-tile plan: tiles * splits workgroups of 512 threads, then (splits > 1) the
 // reduction of the partial sums, one workgroup of 256 threads per tile, on the same stream.

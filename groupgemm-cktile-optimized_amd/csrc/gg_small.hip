@@ -1,9 +1,11 @@
 // Small-tile forward kernel (16-bit inputs and output, out[g] = x[g] @ w[g]^T, RCR) for problems
 // whose 256 x 256 tiles cannot fill the GPU: one 128 x 128 output tile, or one K range of it
-// (split-K), per workgroup of 512 threads, one workgroup per CU (128 KB of LDS).
+// (split-K), per workgroup of 512 threads.
 //
 // Operands go from global memory to LDS by DMA (buffer_load ... lds, 16 bytes per lane) into a
-// ring of 4 K steps of 64, issued 3 steps ahead. Rows are 128 bytes in LDS, their 16-byte pieces
+// ring of S K steps of 64, issued S - 1 steps ahead: S = 4 (128 KB, one workgroup per CU) for
+// plans of at most one tile per CU, S = 2 (64 KB, two workgroups per CU, 97 registers per lane)
+// for up to two. Rows are 128 bytes in LDS, their 16-byte pieces
 // stored at (piece ^ (row % 8)) so that 8 lanes reading 8 consecutive rows hit 8 different bank
 // groups. Eight waves, two per SIMD: waves 0-3 multiply the first 32 K of every step and waves
 // 4-7 the second, each for a 64 x 64 quarter of the tile, with v_mfma_f32_16x16x32 (bf16 or
@@ -96,9 +98,8 @@ __device__ __forceinline__ si32x4 raw_rsrc(const void *p, int bytes) {
     return r;
 }
 
-template <bool F16, bool SPLIT>
-__global__ void __launch_bounds__(512, 1) small_gemm_kernel(const SmallArgs a) {
-    constexpr int S = kSmallStages;
+template <bool F16, bool SPLIT, int S>
+__global__ void __launch_bounds__(512, S == kSmallStagesTwo ? 4 : 2) small_gemm_kernel(const SmallArgs a) {
     __shared__ __attribute__((aligned(1024))) unsigned char lds[S][2][kStage]; // [stage][x, w]
     // wave is uniform: readfirstlane keeps it (and the DMAs' LDS addresses) in SGPRs
     const int tid = static_cast<int>(threadIdx.x), lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -154,24 +155,26 @@ __global__ void __launch_bounds__(512, 1) small_gemm_kernel(const SmallArgs a) {
     for (int s = s0; s < min(s1, s0 + S - 1); ++s)
         issue(s);
     for (int s = s0; s < s1; ++s) {
-        if (s + S - 2 < s1) // the DMAs of steps s + 1 .. s + S - 2 (4 per step and wave) may run on
-            wait_vm_barrier<(S - 2) * 4>();
+        if (S > 2 && s + S - 2 < s1) // the DMAs of steps s + 1 .. s + S - 2 (4 per step and wave) may run on
+            wait_vm_barrier<(S > 2 ? S - 2 : 0) * 4>();
         else
             wait_vm_barrier<0>();
         if (s + S - 1 < s1)
             issue(s + S - 1);
         const unsigned char *sa = &lds[s % S][0][0];
-        su32x4               fa[4], fb[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            fa[i] = *reinterpret_cast<const su32x4 *>(sa + (wm * 64 + 16 * i + frow) * 128 + p);
-            fb[i] = *reinterpret_cast<const su32x4 *>(sa + kStage + (wn * 64 + 16 * i + frow) * 128 + p);
-        }
+        su32x4               fa[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
+            fa[i] = *reinterpret_cast<const su32x4 *>(sa + (wm * 64 + 16 * i + frow) * 128 + p);
+        // one w fragment at a time: 20 fragment registers instead of 32 (two workgroups per CU
+        // with a 2-step ring leave 128 registers per lane)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                acc[i][j] = mma<F16>(fb[j], fa[i], acc[i][j]);
+        for (int j = 0; j < 4; ++j) {
+            const su32x4 fb = *reinterpret_cast<const su32x4 *>(sa + kStage + (wn * 64 + 16 * j + frow) * 128 + p);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                acc[i][j] = mma<F16>(fb, fa[i], acc[i][j]);
+        }
     }
 
     // 20 wait states between the last MFMA and the first read of its accumulators (gfx950 needs
@@ -191,24 +194,21 @@ __global__ void __launch_bounds__(512, 1) small_gemm_kernel(const SmallArgs a) {
     __syncthreads();
     if (kh == 1)
         return;
+    // Add the second K half and store (or write the range's slab) one row of blocks at a time,
+    // so that few loaded values are in flight beside the accumulators.
+    float *slab = SPLIT ? a.ws + (static_cast<int64_t>(split) * a.tiles + tile) * (kSmallTile * kSmallTile) : nullptr;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 4; ++i) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            acc[i][j] += *reinterpret_cast<const sf32x4 *>(red + ((wq * 16 + i * 4 + j) * 64 + lane) * 4);
-    if constexpr (SPLIT) {
-        float *slab = a.ws + (static_cast<int64_t>(split) * a.tiles + tile) * (kSmallTile * kSmallTile);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                *reinterpret_cast<sf32x4 *>(slab + ((wq * 16 + i * 4 + j) * 64 + lane) * 4) = acc[i][j];
-    } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                store_block<F16>(a, t, wm, wn, i, j, lane, acc[i][j]);
+        for (int j = 0; j < 4; ++j) {
+            const int    q = ((wq * 16 + i * 4 + j) * 64 + lane) * 4;
+            const sf32x4 v = acc[i][j] + *reinterpret_cast<const sf32x4 *>(red + q);
+            if constexpr (SPLIT)
+                *reinterpret_cast<sf32x4 *>(slab + q) = v;
+            else
+                store_block<F16>(a, t, wm, wn, i, j, lane, v);
+        }
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
@@ -234,13 +234,23 @@ template <bool F16> __global__ void __launch_bounds__(256) small_reduce_kernel(c
 
 } // namespace
 
+template <bool F16, bool SPLIT>
+void launch_ring(const SmallArgs &a, dim3 grid, dim3 block, hipStream_t stream) {
+    if (a.stages == kSmallStagesTwo)
+        small_gemm_kernel<F16, SPLIT, kSmallStagesTwo><<<grid, block, 0, stream>>>(a);
+    else
+        small_gemm_kernel<F16, SPLIT, kSmallStagesOne><<<grid, block, 0, stream>>>(a);
+}
+
 hipError_t launch_small_gemm(const SmallArgs &a, bool fp16, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(a.tiles * a.splits)), block(512), rblock(256);
+    if (a.stages != kSmallStagesOne && a.stages != kSmallStagesTwo)
+        return hipErrorInvalidValue;
     if (a.splits > 1) {
         if (fp16)
-            small_gemm_kernel<true, true><<<grid, block, 0, stream>>>(a);
+            launch_ring<true, true>(a, grid, block, stream);
         else
-            small_gemm_kernel<false, true><<<grid, block, 0, stream>>>(a);
+            launch_ring<false, true>(a, grid, block, stream);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess)
             return e;
@@ -249,9 +259,9 @@ hipError_t launch_small_gemm(const SmallArgs &a, bool fp16, hipStream_t stream) 
         else
             small_reduce_kernel<false><<<dim3(a.tiles), rblock, 0, stream>>>(a);
     } else if (fp16) {
-        small_gemm_kernel<true, false><<<grid, block, 0, stream>>>(a);
+        launch_ring<true, false>(a, grid, block, stream);
     } else {
-        small_gemm_kernel<false, false><<<grid, block, 0, stream>>>(a);
+        launch_ring<false, false>(a, grid, block, stream);
     }
     return hipGetLastError();
 }

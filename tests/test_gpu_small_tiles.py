@@ -6,8 +6,9 @@ and checks every output against float32 at rtol = atol = 1e-2 (bench/bench_main.
 NaN-prefilled so that an unwritten tile fails. Small-integer inputs, whose products and sums are
 exact in fp32, must give the exact integer GEMM rounded to the 16-bit output, bit for bit, with
 and without split-K. Shapes: ragged and empty groups, one-row groups, N with a partial 128-column
-tile (N = 8, 136, 2000), K % 64 in {8, 40} and K = 8, and more ranges than a K of 64 steps
-divides evenly.
+tile (N = 8, 136, 2000, 2056), K % 64 in {8, 40} and K = 8, more ranges than a K of 64 steps
+divides evenly, and plans of more workgroups than CUs (a 2-step LDS ring, two workgroups per
+CU).
 """
 import pytest
 import torch
@@ -32,6 +33,8 @@ CASES = [
     (torch.float16, [512, 512], 2048, 1408, None),
     (torch.bfloat16, [2048], 4096, 4096, 1),
     (torch.bfloat16, [129], 4096, 16384, 64),
+    (torch.float16, [700, 0, 1300, 513], 2000, 1000, None),
+    (torch.bfloat16, [300, 2000, 17], 2056, 2120, 2),
 ]
 
 
@@ -64,6 +67,13 @@ def test_small_tiles_against_fp32(pkg, monkeypatch, case):
     w = torch.randn((len(gm), n, k), generator=g, device=DEV).to(dt)
     out, detail = _run(pkg, x, w, gm, monkeypatch, split)
     assert "small 128x128x64" in detail, detail
+    tiles, steps = sum((m + 127) // 128 for m in gm) * ((n + 127) // 128), (k + 63) // 64
+    if split is None:  # forced plans fill the 256 CUs with K ranges of at least 8 steps
+        ranges = max(1, min(256 // tiles, steps // 8)) if tiles < 256 else 1
+    else:
+        ranges = -(-steps // -(-steps // min(split, steps)))
+    # more workgroups than CUs: the 2-step ring, two workgroups per CU
+    assert ("two-per-cu" in detail) == (tiles * ranges > 256), detail
     if split is not None:
         steps = (k + 63) // 64
         per = -(-steps // min(split, steps))
@@ -105,6 +115,7 @@ AUTO = [
     ([512], 5760, 2880, True),                # suite TestID 157: 46 tiles in 3 K ranges -> 180 small
     ([1024, 1024], 2048, 1408, True),         # TestID 112: narrow per-tile plan -> 256 small
     ([300, 300, 300], 1024, 512, True),       # pad_test 9002: 8 K steps, 72 small tiles
+    ([2048], 2880, 2880, True),               # TestID 162: 368 small tiles, two per CU
     ([512], 2880, 2880, False),               # TestID 158: 92 small tiles gain too little
     ([1024], 8192, 16384, False),             # TestID 148: the persistent plan splits K
     ([4096] * 8, 4096, 7168, False),          # config 2
@@ -129,3 +140,4 @@ def test_planner_choice(pkg, monkeypatch, case):
     assert ("small 128x128x64" in detail) == small, detail
     if small:
         assert "split-k" not in detail, detail
+        assert ("two-per-cu" in detail) == (sum((m + 127) // 128 for m in gm) * ((n + 127) // 128) > 256), detail
